@@ -1,0 +1,235 @@
+"""Benchmark of the FP8 W8A8 DiT linear path on one MI355X.
+
+Workload (default): the QKV projection of one DiT block at one SP8 rank's
+token share of a 768p 5 s clip — x bf16 [15624, 3072] (0.1% outlier channels
+x50), W [9216, 3072] quantized per output channel to e4m3fn at init, bias
+bf16.  One step = per-token FP8 quantization of x + the FP8 MFMA GEMM with the
+fused per-token x per-channel dequant + bias epilogue -> bf16 [15624, 9216].
+Inputs are resident in HBM; activations rotate over 4 buffers (384 MB) so the
+256 MB last-level cache cannot hold them across steps.
+
+Also timed (HIP events on the launch stream, same process): the GEMM alone
+(roofline), the per-token quantizer alone, the fused LayerNorm + AdaLN
+modulate + FP8 quant front end, the FFN up (+GELU) / down GEMMs and the INT8
+QKV GEMM.  The CPU baseline is the oracle's quantize-dequantize fp32 linear on
+a bounded row sample of the same workload.
+
+Prints ONE JSON line.  --gpus above 1 is refused: this build measures one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_FP8_TFLOPS = 5000.0   # MI355X dense FP8 MFMA
+PEAK_INT8_TOPS = 5000.0    # MI355X dense INT8 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+METRIC = "FP8 W8A8 linear TFLOP/s (% MFMA peak) + quant GB/s, M=15.6k d=3072, 1 GPU"
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--only", default="", help="comma list of extra kernels to time (default all)")
+    return p.parse_args()
+
+
+def timed(fn, iters, warmup):
+    """Average milliseconds per call of fn() over iters calls (HIP events on the current stream)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(iters):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / iters
+
+
+def cpu_baseline(x_cpu, qw, sw, bias, flop_per_row):
+    """Oracle fake-quant linear on a bounded row sample: (TFLOP/s, sample rows, seconds per run)."""
+    import torch
+    import oracle.ref as R
+    threads = torch.get_num_threads()
+    probe_rows = 64
+    t0 = time.perf_counter()
+    R.cpu_fake_quant_linear_fp8(x_cpu[:probe_rows], qw, sw, bias)
+    per_row = (time.perf_counter() - t0) / probe_rows
+    rows = int(min(x_cpu.shape[0], max(probe_rows, 2.0 / max(per_row, 1e-9))))  # ~2 s per run
+    sample = x_cpu[:rows].contiguous()
+    R.cpu_fake_quant_linear_fp8(sample, qw, sw, bias)  # warm-up
+    runs = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        R.cpu_fake_quant_linear_fp8(sample, qw, sw, bias)
+        runs.append(time.perf_counter() - t0)
+    sec = statistics.median(runs)
+    return flop_per_row * rows / sec / 1e12, rows, sec, threads
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
+              "(the W8A8 linear path has no cross-GPU work at one SP rank's token share)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import xgen_amd  # noqa: F401
+    from xgen_amd import _native as N
+    from xgen_amd import workloads as W
+
+    xops = torch.ops.xgen_amd
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    M, K, Nf = W.M_5S, W.D_MODEL, 3 * W.D_MODEL
+    g = W.generator(0, dev)
+    xs = []
+    for _ in range(4):
+        x, _ = W.activations(M, K, g, dev)
+        xs.append(x)
+    w, b = W.weight("qkv", g, dev)
+    qw, sw = xops.quantize_rows(w, torch.float8_e4m3fn)
+    torch.cuda.synchronize()
+
+    fp8 = torch.float8_e4m3fn
+    state = {"i": 0}
+
+    def nxt():
+        state["i"] += 1
+        return xs[state["i"] & 3]
+
+    def step():
+        qa, sa = xops.quantize_rows(nxt(), fp8)
+        out, _ = xops.scaled_mm(qa, qw, sa, sw, b, torch.bfloat16, N.ACT_NONE, False)
+        return out
+
+    # ---- whole step (quant + GEMM), the headline value
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        step()
+    stop.record()
+    torch.cuda.synchronize()
+    ms_step = start.elapsed_time(stop) / args.steps
+    flop = 2.0 * M * Nf * K
+    value = flop / (ms_step * 1e-3) / 1e12
+
+    # ---- GEMM alone (dominant kernel)
+    qa0, sa0 = xops.quantize_rows(xs[0], fp8)
+    ms_gemm = timed(lambda: xops.scaled_mm(qa0, qw, sa0, sw, b, torch.bfloat16, N.ACT_NONE, False),
+                    args.steps, args.warmup)
+    gemm_tflops = flop / (ms_gemm * 1e-3) / 1e12
+
+    # ---- per-token quantizer alone (rotating inputs)
+    quant_bytes = M * K * 2 + M * K + 4 * M
+    ms_quant = timed(lambda: xops.quantize_rows(nxt(), fp8), args.steps, args.warmup)
+    quant_gbs = quant_bytes / (ms_quant * 1e-3) / 1e9
+
+    kernels = {
+        "gemm_fp8_qkv": {"ms": ms_gemm, "tflops": gemm_tflops, "frac_of_peak": gemm_tflops / PEAK_FP8_TFLOPS},
+        "quant_rows_fp8": {"ms": ms_quant, "gbs": quant_gbs, "frac_of_hbm": quant_gbs / PEAK_HBM_GBS,
+                           "bytes": quant_bytes},
+    }
+
+    only = set(filter(None, args.only.split(",")))
+
+    def want(name):
+        return not only or name in only
+
+    # ---- fused LayerNorm + AdaLN modulate + FP8 quant front end (M=15,624)
+    if want("front_end"):
+        shift, scale = W.adaln_tables(20, K, g, dev)
+        idx = torch.randint(20, (M,), generator=g, device=dev)
+        fe_bytes = M * K * 2 + M * K + 4 * M + 8 * M
+        ms_fe = timed(lambda: xops.norm_affine_quant(nxt()[None], None, scale, shift, idx, 1e-6, N.NORM_LAYER,
+                                                     fp8, False),
+                      args.steps, args.warmup)
+        fe_gbs = fe_bytes / (ms_fe * 1e-3) / 1e9
+        kernels["front_end_ln_mod_quant_fp8"] = {"ms": ms_fe, "gbs": fe_gbs, "frac_of_hbm": fe_gbs / PEAK_HBM_GBS,
+                                                 "bytes": fe_bytes}
+
+    # ---- FFN GEMMs and INT8 QKV
+    if want("ffn"):
+        wu, bu = W.weight("ffn_up", g, dev)
+        wd, bd = W.weight("ffn_down", g, dev)
+        qu, su = xops.quantize_rows(wu, fp8)
+        qd, sd = xops.quantize_rows(wd, fp8)
+        h, _ = xops.scaled_mm(qa0, qu, sa0, su, bu, torch.bfloat16, N.ACT_GELU_TANH, False)
+        qh, sh = xops.quantize_rows(h, fp8)
+        f_up = 2.0 * M * qu.shape[0] * K
+        ms_up = timed(lambda: xops.scaled_mm(qa0, qu, sa0, su, bu, torch.bfloat16, N.ACT_GELU_TANH, False),
+                      args.steps, args.warmup)
+        ms_dn = timed(lambda: xops.scaled_mm(qh, qd, sh, sd, bd, torch.bfloat16, N.ACT_NONE, False),
+                      args.steps, args.warmup)
+        ms_rq = timed(lambda: xops.quantize_rows(h, fp8), args.steps, args.warmup)
+        kernels["gemm_fp8_ffn_up_gelu"] = {"ms": ms_up, "tflops": f_up / (ms_up * 1e-3) / 1e12,
+                                           "frac_of_peak": f_up / (ms_up * 1e-3) / 1e12 / PEAK_FP8_TFLOPS}
+        kernels["gemm_fp8_ffn_down"] = {"ms": ms_dn, "tflops": f_up / (ms_dn * 1e-3) / 1e12,
+                                        "frac_of_peak": f_up / (ms_dn * 1e-3) / 1e12 / PEAK_FP8_TFLOPS}
+        rq_bytes = M * 4 * K * 3 + 4 * M
+        kernels["requant_fp8_12288"] = {"ms": ms_rq, "gbs": rq_bytes / (ms_rq * 1e-3) / 1e9}
+        del wu, wd, qu, qd, h, qh
+    if want("int8"):
+        qai, sai = xops.quantize_rows(xs[0], torch.int8)
+        qwi, swi = xops.quantize_rows(w, torch.int8)
+        ms_i8 = timed(lambda: xops.scaled_mm(qai, qwi, sai, swi, b, torch.bfloat16, N.ACT_NONE, False),
+                      args.steps, args.warmup)
+        kernels["gemm_int8_qkv"] = {"ms": ms_i8, "tops": flop / (ms_i8 * 1e-3) / 1e12,
+                                    "frac_of_peak": flop / (ms_i8 * 1e-3) / 1e12 / PEAK_INT8_TOPS}
+
+    # ---- CPU baseline (oracle fake-quant path) on a bounded sample
+    cpu = None
+    if not args.no_cpu_baseline:
+        x_cpu = xs[0][:4096].cpu()
+        tf, rows, sec, threads = cpu_baseline(x_cpu, qw.cpu(), sw.cpu(), b.cpu(), 2.0 * Nf * K)
+        cpu = {"value": tf, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+               "sample": f"first {rows} of {M} token rows of the QKV workload (per-token FP8 quant -> fp32 "
+                         f"dequant -> F.linear fp32 -> +bias -> bf16); median of 5 runs of {sec:.2f} s",
+               "cpu": platform.processor() or platform.machine()}
+
+    result = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3",
+        "data": "synthetic (seeded; x ~ N(0,1) bf16 with 0.1% outlier channels x50, W ~ N(0,0.02))",
+        "config": {"workload": "c2_qkv: per-token FP8 quant + FP8 W8A8 GEMM, M=15624 K=3072 N=9216, bf16 out",
+                   "M": M, "K": K, "N": Nf, "weight_scaling": "per-channel", "activation_scaling": "per-token"},
+        "roofline": {"bound": "mfma", "achieved": gemm_tflops, "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
+                     "frac": gemm_tflops / PEAK_FP8_TFLOPS, "traffic": None,
+                     "kernel": "gemm_w8a8_kernel<fp8> (QKV)", "flop_per_launch": flop},
+        "quant": {"gbs": quant_gbs, "frac_of_hbm": quant_gbs / PEAK_HBM_GBS},
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

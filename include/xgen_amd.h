@@ -1,0 +1,178 @@
+/*
+ * xgen_amd — C ABI of the MI355X (gfx950) quantized DiT linear path.
+ *
+ * Every entry point takes plain device pointers, element counts and strides
+ * (in elements), and the HIP stream to launch on.  Nothing here allocates,
+ * frees or synchronizes; outputs are caller-owned.  Each call validates its
+ * arguments on the host before any HIP call and returns XGEN_OK or an error
+ * code; xgen_last_error() returns a per-thread message for the last failure.
+ *
+ * Dtype codes (XGEN_DTYPE_*) name element types of the buffers:
+ *   BF16, F16, F32 (IEEE), E4M3 (OCP float8 e4m3fn), I8, I32.
+ *
+ * Row convention: a matrix [rows, cols] with leading dimension ld (elements
+ * between the starts of consecutive rows); the last dimension is contiguous.
+ *
+ * Each declaration cites the reference interface it replaces
+ * (paths relative to the reference repository root).
+ */
+#ifndef XGEN_AMD_H
+#define XGEN_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define XGEN_ABI_VERSION 1
+
+/* status codes */
+#define XGEN_OK 0
+#define XGEN_ERR_INVALID_ARGUMENT 1 /* null pointer, negative size, unknown code */
+#define XGEN_ERR_UNSUPPORTED 2      /* valid request outside the kernels' limits */
+#define XGEN_ERR_HIP 3              /* the HIP runtime reported a launch error */
+
+/* dtype codes */
+#define XGEN_DTYPE_BF16 0
+#define XGEN_DTYPE_F16 1
+#define XGEN_DTYPE_F32 2
+#define XGEN_DTYPE_E4M3 3
+#define XGEN_DTYPE_I8 4
+#define XGEN_DTYPE_I32 5
+#define XGEN_DTYPE_NONE (-1)
+
+/* normalisation kinds for xgen_norm_affine_quant */
+#define XGEN_NORM_LAYER 0 /* (x - mean) * rsqrt(var + eps), biased variance */
+#define XGEN_NORM_RMS 1   /* x * rsqrt(mean(x^2) + eps) */
+
+/* GEMM epilogue activations */
+#define XGEN_ACT_NONE 0
+#define XGEN_ACT_GELU_TANH 1 /* out = bf16(gelu_tanh(bf16(linear))) */
+
+/* Largest row width of the fused norm kernel (the reference limit,
+ * x_base/x_base/operator/npu_fusion/capabilities.py:7, is 6144). */
+#define XGEN_NORM_MAX_WIDTH 8192
+
+int xgen_abi_version(void);
+const char *xgen_status_string(int status);
+/* Message of the last failing call on the calling host thread ("" if none). */
+const char *xgen_last_error(void);
+
+/*
+ * Per-row FP8 (e4m3fn) or INT8 dynamic quantization of a BF16/F16 matrix.
+ *
+ * out_dtype == XGEN_DTYPE_E4M3 — the per-tensor arithmetic of
+ *   quantize_per_tensor, x_base/x_base/operator/h3_fp8.py:9-12, applied to
+ *   each row r:  s[r] = max(amax_r / 448, FLT_MIN);
+ *   q[r,c] = e4m3fn_rne(clamp(x[r,c] / s[r], -448, 448)).
+ * out_dtype == XGEN_DTYPE_I8 — torch_npu.npu_dynamic_quant as called at
+ *   x_base/x_base/operator/matmul.py:60, with the arithmetic the reference
+ *   restates in npu_fusion/f2bc/op_kernel/f2bc_kernel.asc:89-107:
+ *   s[r] = amax_r * fl(1/127); alpha = fl(127 / amax_r);
+ *   q[r,c] = rint_half_even(fl(x[r,c] * alpha)); a zero row gives q = 0 and
+ *   s = 0 (npu_fusion/f1b/op_kernel/swiglu_quant_kernel.asc:72-75).
+ * amax propagates NaN. q is [rows, cols] with leading dimension ldq; scale is
+ * float32 [rows].
+ */
+int xgen_quantize_rows(int in_dtype, const void *x, int64_t rows, int64_t cols, int64_t ldx,
+                       int out_dtype, void *q, int64_t ldq, float *scale, hipStream_t stream);
+
+/*
+ * NaN-propagating max |x| over a contiguous BF16/F16 tensor of numel elements
+ * (activation_abs_peak, x_base/x_base/operator/h3_abs_peak.py:21-25).
+ * peak: one float32 on the device.  workspace: device memory of at least
+ * xgen_abs_peak_workspace_bytes(numel) bytes (partial peaks).
+ */
+size_t xgen_abs_peak_workspace_bytes(int64_t numel);
+int xgen_abs_peak(int in_dtype, const void *x, int64_t numel, float *peak, void *workspace,
+                  size_t workspace_bytes, hipStream_t stream);
+
+/*
+ * Per-tensor FP8 activation scale: scale = max(abs_peak(x) / 448, FLT_MIN)
+ * (quantize_activation, x_base/x_base/operator/h3_fp8_quant.py:19).
+ * Same workspace as xgen_abs_peak.
+ */
+int xgen_fp8_tensor_scale(int in_dtype, const void *x, int64_t numel, float *scale,
+                          void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/*
+ * FP8 pack with a device-resident per-tensor scale
+ * (_pack, x_base/x_base/operator/h3_fp8_quant.py:9-15):
+ * q[i] = e4m3fn_rne(clamp(x[i] / scale[0], -448, 448)) over numel contiguous elements.
+ */
+int xgen_fp8_pack(int in_dtype, const void *x, int64_t numel, const float *scale, void *q,
+                  hipStream_t stream);
+
+/*
+ * Fused normalisation + AdaLN-table modulation + per-row quantization
+ * (torch.ops.h3_phaa_nq2.fused, npu_fusion/f2_nq2/op_extension/nq2_queued.asc:53-61,
+ *  kernel npu_fusion/f2bc/op_kernel/f2bc_kernel.asc:57-107; LayerNorm form of
+ *  x_diffusers/x_diffusers/framework/transformer/hunyuan.py:390-393).
+ *
+ * x: BF16 [batch, seq, width], element (b, s, c) at x[b*x_stride_batch + s*x_stride_seq + c].
+ * Row r = b*seq + s uses table row g = indices[s] (int64, 0 <= g < table_rows):
+ *   n    = bf16(norm(x_r) [* weight])          norm_kind LAYER or RMS, fp32 math
+ *   f    = bf16(1 + scale_table[g])
+ *   m    = bf16(bf16(n * f) + shift_table[g])
+ *   q[r] = per-row quantization of m (out_dtype E4M3 or I8, as xgen_quantize_rows)
+ * norm_weight: NULL (no affine) or [width] of dtype BF16/F32.
+ * scale_table/shift_table: BF16 [table_rows, width], rows scale_row_stride /
+ * shift_row_stride elements apart.  q: [batch*seq, width] contiguous;
+ * token_scale: float32 [batch*seq].  normed_out: NULL or BF16 [batch*seq, width]
+ * receiving m (the pre-quantization row; the reference's debug output,
+ * f2bc_kernel.asc:86).  An out-of-range index yields q = NaN bytes (E4M3) or 0
+ * (I8) and a NaN scale for that row; nothing out of bounds is read.
+ */
+int xgen_norm_affine_quant(const void *x, int64_t batch, int64_t seq, int64_t width,
+                           int64_t x_stride_batch, int64_t x_stride_seq, int norm_kind,
+                           const void *norm_weight, int norm_weight_dtype, float eps,
+                           const void *scale_table, int64_t scale_row_stride,
+                           const void *shift_table, int64_t shift_row_stride, int64_t table_rows,
+                           const int64_t *indices, int out_dtype, void *q, float *token_scale,
+                           void *normed_out, hipStream_t stream);
+
+/*
+ * FP8 W8A8 GEMM with fused dequant epilogue
+ * (torch._scaled_mm as called at x_base/x_base/operator/h3_fp8.py:63-66):
+ *   acc[m,n] = sum_k a[m,k] * w[n,k]            (e4m3fn operands, fp32 accumulation)
+ *   y[m,n]   = acc * (a_scale[m*a_scale_stride] * w_scale[n*w_scale_stride]) + bias[n]
+ *   out[m,n] = out_dtype(y), or with XGEN_ACT_GELU_TANH out_dtype(gelu_tanh(out_dtype(y)))
+ * a: [M, K] (lda), w: [N, K] (ldw) — the weight as stored by H3FP8Linear, so
+ * the product is a @ w.T.  Scale strides 0 (per-tensor) or 1 (per-token /
+ * per-channel).  bias: NULL or [N] of bias_dtype (BF16/F16/F32).
+ * out_dtype BF16 or F16, out [M, N] with leading dimension ldo.
+ * acc_out: NULL or float32 [M, N] (leading dimension N) receiving acc.
+ * Requires K % 16 == 0 and N % 16 == 0 (the reference's alignment,
+ * h3_fp8.py:20-21), 16-byte aligned a/w rows.
+ */
+int xgen_scaled_mm_fp8(const void *a, int64_t lda, const void *w, int64_t ldw, int64_t M,
+                       int64_t N, int64_t K, const float *a_scale, int64_t a_scale_stride,
+                       const float *w_scale, int64_t w_scale_stride, const void *bias,
+                       int bias_dtype, int activation, void *out, int out_dtype, int64_t ldo,
+                       float *acc_out, hipStream_t stream);
+
+/*
+ * INT8 W8A8 GEMM with fused dequant epilogue
+ * (torch_npu.npu_quant_matmul as called at x_base/x_base/operator/matmul.py:63-64 and
+ *  npu_fusion/runtime.py:87-91):
+ *   acc[m,n] = sum_k a[m,k] * w[n,k]            (int8 operands, exact int32 accumulation)
+ *   y[m,n]   = float(acc) * (pertoken_scale[m] * w_scale[n]) + bias[n]
+ *   out = out_dtype(y) or, with XGEN_ACT_GELU_TANH, out_dtype(gelu_tanh(out_dtype(y))).
+ * Scale strides as in xgen_scaled_mm_fp8.  acc_out: NULL or int32 [M, N]
+ * (leading dimension N) receiving the exact accumulators.  Requires K % 16 == 0.
+ */
+int xgen_quant_matmul_int8(const void *a, int64_t lda, const void *w, int64_t ldw, int64_t M,
+                           int64_t N, int64_t K, const float *pertoken_scale,
+                           int64_t pertoken_scale_stride, const float *w_scale,
+                           int64_t w_scale_stride, const void *bias, int bias_dtype,
+                           int activation, void *out, int out_dtype, int64_t ldo,
+                           int32_t *acc_out, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* XGEN_AMD_H */

@@ -1,0 +1,284 @@
+"""CPU oracle: restatement of the reference's arithmetic on the W8A8 DiT linear path.
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).  Torch CPU and numpy ops,
+plus the C restatement in oracle/quant_ref.c for bit-level quantizer work.
+
+Function -> reference -> how it is pinned (tests/test_oracle_*.py):
+  e4m3 encode/decode  h3_fp8.py:12 (.to(float8_e4m3fn))
+        C encoder from the format definition == torch's conversion on every
+        bf16 value and 2^20 random floats; decode table == torch; closed forms
+        (2^-9 -> 0x01, tie 1.5*2^-9 -> 0x02, 448 -> 0x7e, 464 -> NaN).
+  quantize_per_tensor h3_fp8.py:9-12
+        reference known answers: zero tensor -> finite scale, zero bytes
+        (x_base/tests/test_h3_cuda_precision_ops.py:8-11); linspace(-2,3) weight
+        bytes (x_diffusers/tests/test_h3_tp_cp.py:42-66) against a brute-force
+        nearest-value search over the 256 codes; per-row form == per-tensor form
+        on each single row; torch restatement == C restatement.
+  quantize_rows_int8  f2bc_kernel.asc:89-107 (+ zero row swiglu_quant_kernel.asc:72-75)
+        torch == C; |q| <= 127 with +-127 at the row max; exact ties on bf16
+        inputs (amax = 127 -> alpha = 1) round half to even; |x - q*s| <= s/2 + eps.
+  abs_peak            h3_abs_peak.py:14-25   max is order-free; NaN propagates.
+  layer/rms norm      hunyuan.py:359 (nn.LayerNorm, eps 1e-6), f2bc_kernel.asc:68-81
+        float64 statistics; == torch.nn.functional.layer_norm within 1 bf16 ulp;
+        invariants (zero mean, unit variance of the fp64 result).
+  modulate            h3_indexed_affine.py:22-28 / hunyuan.py:393
+        eager bf16 torch expression == numpy restatement with explicit RNE
+        rounding after each op, bit for bit.
+  gelu_tanh           diffusers FeedForward('gelu-approximate') = F.gelu(tanh)
+        (hunyuan.py:358) — parity unpinned against diffusers itself (absent);
+        checked against the closed formula in float64 within 1 bf16 ulp.
+  fp8 / int8 GEMM     h3_fp8.py:63-66 (_scaled_mm), matmul.py:63-64 (npu_quant_matmul)
+        accumulators exact (float64 BLAS of decoded operands; every partial
+        sum is an exact multiple of 2^-18 below 2^35) == int64 brute force on
+        small shapes; torch._int_mm on CPU for int8.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from pathlib import Path
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+FP8_MAX = 448.0
+FLT_TINY = torch.finfo(torch.float32).tiny
+_C = None
+_LIB_PATH = Path(__file__).resolve().parent / "_lib" / "liboracle_quant.so"
+
+
+def clib() -> ctypes.CDLL:
+    """The C restatement (built on first use if missing)."""
+    global _C
+    if _C is None:
+        if not _LIB_PATH.is_file():
+            from . import build
+            build.build()
+        L = ctypes.CDLL(str(_LIB_PATH))
+        L.oracle_e4m3_encode.restype = ctypes.c_uint8
+        L.oracle_e4m3_encode.argtypes = [ctypes.c_float]
+        L.oracle_e4m3_decode.restype = ctypes.c_float
+        L.oracle_e4m3_decode.argtypes = [ctypes.c_uint8]
+        L.oracle_e4m3_encode_array.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+        L.oracle_quant_rows_fp8.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                                            ctypes.c_void_p, ctypes.c_void_p]
+        L.oracle_quant_rows_int8.argtypes = L.oracle_quant_rows_fp8.argtypes
+        L.oracle_check_fast_division.restype = ctypes.c_int64
+        L.oracle_check_fast_division.argtypes = [ctypes.c_int, ctypes.c_uint32, ctypes.c_uint32]
+        _C = L
+    return _C
+
+
+# ----------------------------------------------------------------------------- bf16 / e4m3 helpers
+def round_bf16_np(v: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 precision (round to nearest even), as float32; NaN stays NaN."""
+    v = np.asarray(v, dtype=np.float32)
+    u = v.view(np.uint32).astype(np.uint64)
+    rounded = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    out = rounded.astype(np.uint32).view(np.float32)
+    return np.where(np.isnan(v), v, out)
+
+
+def bf16_to_np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().float().numpy()
+
+
+def e4m3_encode(v: np.ndarray) -> np.ndarray:
+    """C encoder (oracle_e4m3_encode) over a float32 array -> uint8 array."""
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    out = np.empty(v.shape, dtype=np.uint8)
+    clib().oracle_e4m3_encode_array(v.ctypes.data, v.size, out.ctypes.data)
+    return out
+
+
+def e4m3_decode_table() -> np.ndarray:
+    L = clib()
+    return np.array([L.oracle_e4m3_decode(b) for b in range(256)], dtype=np.float32)
+
+
+def canonical_nan_e4m3(q: torch.Tensor) -> torch.Tensor:
+    """Every e4m3fn NaN code (0x7f / 0xff) written as 0x7f."""
+    u = q.view(torch.uint8).clone()
+    u[(u & 0x7F) == 0x7F] = 0x7F
+    return u.view(torch.float8_e4m3fn)
+
+
+# ----------------------------------------------------------------------------- quantizers
+def quantize_per_tensor(value: torch.Tensor):
+    """h3_fp8.py:9-12: (e4m3fn tensor, float32 0-dim scale)."""
+    v = value.detach().cpu().float()
+    scale = (v.abs().amax() / FP8_MAX).clamp_min(FLT_TINY)
+    q = (v / scale).clamp(-FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn)
+    return canonical_nan_e4m3(q), scale
+
+
+def quantize_rows_fp8(x: torch.Tensor):
+    """quantize_per_tensor's arithmetic per row of [..., K]: (e4m3fn like x, float32 [rows])."""
+    v = x.detach().cpu().float().reshape(-1, x.shape[-1])
+    scale = (v.abs().amax(dim=-1) / FP8_MAX).clamp_min(FLT_TINY)
+    q = (v / scale[:, None]).clamp(-FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn)
+    return canonical_nan_e4m3(q).reshape(x.shape), scale
+
+
+def quantize_rows_int8(x: torch.Tensor):
+    """f2bc_kernel.asc:89-107: scale = amax*fl(1/127), q = rint(x*fl(127/amax)), NaN -> 0."""
+    v = x.detach().cpu().float().reshape(-1, x.shape[-1])
+    amax = v.abs().amax(dim=-1)
+    inv127 = torch.tensor(1.0, dtype=torch.float32) / 127.0
+    scale = amax * inv127
+    alpha = torch.tensor(127.0, dtype=torch.float32) / amax
+    y = v * alpha[:, None]
+    q = torch.where(torch.isnan(y), torch.zeros_like(y), torch.round(y)).to(torch.int8)
+    return q.reshape(x.shape), scale
+
+
+def _half_fmt(x: torch.Tensor) -> int:
+    if x.dtype == torch.bfloat16:
+        return 0
+    if x.dtype == torch.float16:
+        return 1
+    raise ValueError("bf16 / f16 input required")
+
+
+def quantize_rows_c(x: torch.Tensor, out: str):
+    """C restatement of the row quantizers ('fp8' or 'int8')."""
+    fmt = _half_fmt(x)
+    m = x.detach().cpu().contiguous().reshape(-1, x.shape[-1])
+    bits = m.view(torch.int16).numpy()
+    rows, cols = bits.shape
+    scale = np.empty(rows, dtype=np.float32)
+    q = np.empty((rows, cols), dtype=np.uint8 if out == "fp8" else np.int8)
+    fn = clib().oracle_quant_rows_fp8 if out == "fp8" else clib().oracle_quant_rows_int8
+    fn(fmt, bits.ctypes.data, rows, cols, q.ctypes.data, scale.ctypes.data)
+    qt = torch.from_numpy(q)
+    qt = qt.view(torch.float8_e4m3fn) if out == "fp8" else qt
+    return qt.reshape(x.shape), torch.from_numpy(scale)
+
+
+def abs_peak(x: torch.Tensor) -> torch.Tensor:
+    """h3_abs_peak.py:21-25: NaN-propagating max |x| as float32 0-dim."""
+    return x.detach().cpu().float().abs().amax()
+
+
+# ----------------------------------------------------------------------------- front end
+def layer_norm_f64(x: torch.Tensor, eps: float, weight: torch.Tensor | None = None) -> torch.Tensor:
+    """LayerNorm (no bias) with float64 statistics, rounded to bf16 via float32."""
+    v = x.detach().cpu().double()
+    mean = v.mean(dim=-1, keepdim=True)
+    var = ((v - mean) ** 2).mean(dim=-1, keepdim=True)
+    n = (v - mean) / torch.sqrt(var + eps)
+    if weight is not None:
+        n = n * weight.detach().cpu().double()
+    return n.float().to(torch.bfloat16)
+
+
+def rms_norm_f64(x: torch.Tensor, eps: float, weight: torch.Tensor | None = None) -> torch.Tensor:
+    """RMSNorm (f2bc_kernel.asc:68-81 order: x * rsqrt(mean(x^2) + eps) * w) in float64 -> bf16."""
+    v = x.detach().cpu().double()
+    n = v / torch.sqrt((v * v).mean(dim=-1, keepdim=True) + eps)
+    if weight is not None:
+        n = n * weight.detach().cpu().double()
+    return n.float().to(torch.bfloat16)
+
+
+def modulate(n: torch.Tensor, scale_rows: torch.Tensor, shift_rows: torch.Tensor) -> torch.Tensor:
+    """Eager bf16 AdaLN modulation n * (1 + scale) + shift (hunyuan.py:393,
+    h3_npu_fusion.py:352): every op rounds to bf16."""
+    return n * (1.0 + scale_rows) + shift_rows
+
+
+def modulate_np(n: np.ndarray, scale_rows: np.ndarray, shift_rows: np.ndarray) -> np.ndarray:
+    """The same with explicit RNE rounding after each op (h3_indexed_affine.py:22-28)."""
+    f = round_bf16_np(np.float32(1.0) + scale_rows)
+    p = round_bf16_np(n * f)
+    return round_bf16_np(p + shift_rows)
+
+
+def norm_affine_quant(x, weight, scale_tab, shift_tab, indices, eps, norm="layer", out="fp8"):
+    """A10: (q [B*S,H], token scale [B*S], pre-quant bf16 m [B*S,H]).
+    Row r = b*S + s uses table row indices[s] (nq2_queued.asc / f2bc_kernel.asc:31-41)."""
+    B, S, H = x.shape
+    rows = x.detach().cpu().reshape(B * S, H)
+    n = (layer_norm_f64 if norm == "layer" else rms_norm_f64)(rows, eps, weight)
+    g = indices.detach().cpu().long().repeat(B)
+    m = modulate(n, scale_tab.detach().cpu()[g], shift_tab.detach().cpu()[g])
+    q, s = quantize_rows_fp8(m) if out == "fp8" else quantize_rows_int8(m)
+    return q, s, m
+
+
+def gelu_tanh_bf16(y: torch.Tensor) -> torch.Tensor:
+    """diffusers GELU(approximate='tanh') on a bf16 tensor (hunyuan.py:358)."""
+    return F.gelu(y.detach().cpu(), approximate="tanh")
+
+
+# ----------------------------------------------------------------------------- GEMMs
+def decode_fp8(q: torch.Tensor) -> torch.Tensor:
+    """e4m3fn codes -> float64 (exact)."""
+    return q.detach().cpu().float().double()
+
+
+def fp8_accumulate_exact(qa: torch.Tensor, qw: torch.Tensor) -> torch.Tensor:
+    """sum_k a[m,k] w[n,k] exactly (float64 [M,N])."""
+    return decode_fp8(qa) @ decode_fp8(qw).T
+
+
+def int8_accumulate_exact(qa: torch.Tensor, qw: torch.Tensor) -> torch.Tensor:
+    """sum_k a[m,k] w[n,k] exactly (int64 [M,N]); |acc| < 2^53 so float64 BLAS is exact."""
+    return (qa.detach().cpu().double() @ qw.detach().cpu().double().T).round().long()
+
+
+def dequant_epilogue(acc: torch.Tensor, sa: torch.Tensor, sw: torch.Tensor, bias, out_dtype=torch.bfloat16,
+                     activation=None) -> torch.Tensor:
+    """y = acc * (sa[m] * sw[n]) + bias[n] in float32 -> out_dtype [-> gelu_tanh -> out_dtype]."""
+    acc32 = acc.float()
+    sa = sa.detach().cpu().float().reshape(-1)
+    sw = sw.detach().cpu().float().reshape(-1)
+    sa = sa.expand(acc32.shape[0]) if sa.numel() == 1 else sa
+    sw = sw.expand(acc32.shape[1]) if sw.numel() == 1 else sw
+    y = acc32 * (sa[:, None] * sw[None, :])
+    if bias is not None:
+        y = y + bias.detach().cpu().float()[None, :]
+    y = y.to(out_dtype)
+    if activation == "gelu_tanh":
+        y = F.gelu(y, approximate="tanh")
+    return y
+
+
+def w8a8_linear_fp8(qa, sa, qw, sw, bias, out_dtype=torch.bfloat16, activation=None):
+    """_scaled_mm(qa, qw.T, sa, sw, bias) restated (h3_fp8.py:63-66) with per-row/per-col scales."""
+    return dequant_epilogue(fp8_accumulate_exact(qa, qw), sa, sw, bias, out_dtype, activation)
+
+
+def w8a8_linear_int8(qa, sa, qw, sw, bias, out_dtype=torch.bfloat16, activation=None):
+    """npu_quant_matmul(qa, qw.T, sw, bias, pertoken_scale=sa) restated (matmul.py:63-64)."""
+    return dequant_epilogue(int8_accumulate_exact(qa, qw).double(), sa, sw, bias, out_dtype, activation)
+
+
+def cpu_fake_quant_linear_fp8(x: torch.Tensor, qw: torch.Tensor, sw: torch.Tensor, bias) -> torch.Tensor:
+    """CPU quantize-dequantize W8A8 linear (the reported CPU baseline): per-token FP8
+    quantization, dequantize to fp32, F.linear in fp32, + bias, bf16."""
+    qa, sa = quantize_rows_fp8(x)
+    a = qa.float() * sa[:, None]
+    w = qw.float() * sw.reshape(-1, 1).float()
+    y = F.linear(a, w, None if bias is None else bias.float())
+    return y.to(torch.bfloat16)
+
+
+# ----------------------------------------------------------------------------- metrics
+def rel_l2(a: torch.Tensor, b: torch.Tensor) -> float:
+    a, b = a.detach().cpu().double(), b.detach().cpu().double()
+    return float((a - b).norm() / b.norm().clamp_min(1e-300))
+
+
+def cosine(a: torch.Tensor, b: torch.Tensor) -> float:
+    a, b = a.detach().cpu().double().reshape(-1), b.detach().cpu().double().reshape(-1)
+    return float((a @ b) / (a.norm() * b.norm()).clamp_min(1e-300))
+
+
+def bf16_ulp_diff(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """|a - b| in units of bf16 ulps (ordered bit distance), elementwise int64."""
+    def ordered(t):
+        u = t.detach().cpu().contiguous().view(torch.int16).long() & 0xFFFF
+        return torch.where(u >= 0x8000, 0x8000 - u, u)
+    return (ordered(a) - ordered(b)).abs()

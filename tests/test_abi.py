@@ -1,0 +1,78 @@
+"""The C ABI: every symbol include/xgen_amd.h declares is exported by the built
+library and declared to ctypes; argument validation fails before any HIP call
+(no GPU needed)."""
+import ctypes
+import re
+
+import pytest
+
+from xgen_amd import _native as N
+
+HEADER = N.Path(__file__).resolve().parents[1] / "include" / "xgen_amd.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^(?:int|size_t|const char \*)\s*(xgen_\w+)\(", text, re.M)))
+
+
+def test_header_declares_the_path():
+    names = declared_functions()
+    for required in ("xgen_quantize_rows", "xgen_abs_peak", "xgen_fp8_tensor_scale", "xgen_fp8_pack",
+                     "xgen_norm_affine_quant", "xgen_scaled_mm_fp8", "xgen_quant_matmul_int8"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol(built_library):
+    raw = ctypes.CDLL(str(built_library))
+    for name in declared_functions():
+        assert hasattr(raw, name), name
+
+
+def test_ctypes_signatures_cover_the_header():
+    assert set(N.SIGNATURES) == set(declared_functions())
+
+
+def test_status_strings(built_library):
+    L = N.lib()
+    assert L.xgen_abi_version() == 1
+    assert L.xgen_status_string(N.OK) == b"ok"
+    assert L.xgen_status_string(N.ERR_UNSUPPORTED) == b"unsupported shape or layout"
+
+
+@pytest.mark.parametrize("call,status,needle", [
+    (lambda L: L.xgen_quantize_rows(9, 16, 4, 64, 64, N.DTYPE_E4M3, 16, 64, 16, None), N.ERR_INVALID_ARGUMENT, b"input dtype"),
+    (lambda L: L.xgen_quantize_rows(N.DTYPE_BF16, 16, 4, 64, 32, N.DTYPE_E4M3, 16, 64, 16, None), N.ERR_INVALID_ARGUMENT, b"bad shape"),
+    (lambda L: L.xgen_quantize_rows(N.DTYPE_BF16, None, 4, 64, 64, N.DTYPE_I8, 16, 64, 16, None), N.ERR_INVALID_ARGUMENT, b"null"),
+    (lambda L: L.xgen_fp8_pack(N.DTYPE_BF16, 8, 64, 16, 16, None), N.ERR_UNSUPPORTED, b"aligned"),
+    (lambda L: L.xgen_abs_peak(N.DTYPE_BF16, 16, 4096, 16, 16, 0, None), N.ERR_INVALID_ARGUMENT, b"workspace"),
+    (lambda L: L.xgen_scaled_mm_fp8(16, 8, 16, 32, 4, 16, 32, 16, 1, 16, 1, None, N.DTYPE_NONE, 0, 16, N.DTYPE_BF16, 16, None, None),
+     N.ERR_INVALID_ARGUMENT, b"leading"),
+    (lambda L: L.xgen_scaled_mm_fp8(16, 48, 16, 48, 4, 16, 17, 16, 1, 16, 1, None, N.DTYPE_NONE, 0, 16, N.DTYPE_BF16, 16, None, None),
+     N.ERR_UNSUPPORTED, b"multiples of 16"),
+    (lambda L: L.xgen_quant_matmul_int8(16, 32, 16, 32, 4, 16, 32, 16, 2, 16, 1, None, N.DTYPE_NONE, 0, 16, N.DTYPE_BF16, 16, None, None),
+     N.ERR_INVALID_ARGUMENT, b"stride"),
+    (lambda L: L.xgen_quant_matmul_int8(16, 32, 16, 32, 4, 16, 32, 16, 1, 16, 1, None, N.DTYPE_NONE, 7, 16, N.DTYPE_BF16, 16, None, None),
+     N.ERR_INVALID_ARGUMENT, b"activation"),
+    (lambda L: L.xgen_norm_affine_quant(16, 1, 4, 9000, 9000, 9000, N.NORM_LAYER, None, N.DTYPE_NONE, 1e-6,
+                                        16, 9000, 16, 9000, 20, 16, N.DTYPE_E4M3, 16, 16, None, None),
+     N.ERR_UNSUPPORTED, b"exceeds"),
+    (lambda L: L.xgen_norm_affine_quant(16, 1, 4, 64, 64, 64, 5, None, N.DTYPE_NONE, 1e-6,
+                                        16, 64, 16, 64, 20, 16, N.DTYPE_E4M3, 16, 16, None, None),
+     N.ERR_INVALID_ARGUMENT, b"norm kind"),
+    (lambda L: L.xgen_norm_affine_quant(16, 1, 4, 64, 64, 64, N.NORM_RMS, 16, N.DTYPE_NONE, 1e-6,
+                                        16, 64, 16, 64, 20, 16, N.DTYPE_E4M3, 16, 16, None, None),
+     N.ERR_INVALID_ARGUMENT, b"disagree"),
+])
+def test_validation_fails_before_launch(built_library, call, status, needle):
+    L = N.lib()
+    assert call(L) == status
+    assert needle in L.xgen_last_error()
+
+
+def test_empty_inputs_are_no_ops(built_library):
+    L = N.lib()
+    assert L.xgen_quantize_rows(N.DTYPE_BF16, None, 0, 64, 64, N.DTYPE_E4M3, None, 64, None, None) == N.OK
+    assert L.xgen_scaled_mm_fp8(None, 32, None, 32, 0, 16, 32, None, 1, None, 1, None, N.DTYPE_NONE, 0,
+                                None, N.DTYPE_BF16, 16, None, None) == N.OK
+    assert L.xgen_last_error() == b""

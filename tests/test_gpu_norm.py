@@ -1,0 +1,97 @@
+"""GPU parity of the fused norm + AdaLN modulate + quantize kernel.
+
+Contract (the reductions of the norm are order-dependent in float32):
+  * pre-quant bf16 rows within 1 ulp of the oracle (float64 statistics, eager
+    bf16 modulation), >= 99.9% bit-identical;
+  * quantized bytes and scales bit-exact given the kernel's own pre-quant rows.
+"""
+import pytest
+import torch
+
+import oracle.ref as R
+import xgen_amd  # noqa: F401
+from xgen_amd import _native as N
+from xgen_amd import workloads
+from xgen_amd.operator.nq2 import norm_affine_quant
+
+pytestmark = pytest.mark.gpu
+xops = torch.ops.xgen_amd
+
+
+def inputs(B, S, H, T, seed, dev):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn((B, S, H), generator=g)
+    x[..., 3] *= 50
+    x = x.to(torch.bfloat16)
+    shift = (torch.randn((T, H), generator=g) * 0.1).to(torch.bfloat16)
+    scale = (torch.randn((T, H), generator=g) * 0.1).to(torch.bfloat16)
+    idx = torch.randint(T, (S,), generator=g)
+    return x.to(dev), scale.to(dev), shift.to(dev), idx.to(dev)
+
+
+def check(x, weight, scale, shift, idx, eps, norm, out, q, s, m):
+    qr, sr, mr = R.norm_affine_quant(x.cpu(), None if weight is None else weight.cpu(), scale.cpu(), shift.cpu(),
+                                     idx.cpu(), eps, norm, out)
+    ulps = R.bf16_ulp_diff(m.cpu(), mr)
+    assert ulps.max() <= 1
+    assert (ulps == 0).float().mean() >= 0.999
+    q2, s2 = (R.quantize_rows_fp8 if out == "fp8" else R.quantize_rows_int8)(m.cpu())
+    if out == "fp8":
+        assert torch.equal(q.cpu().view(torch.uint8), q2.view(torch.uint8))
+    else:
+        assert torch.equal(q.cpu(), q2)
+    assert torch.equal(s.cpu().view(torch.int32), s2.view(torch.int32))
+    same_rows = (ulps == 0).all(dim=-1)
+    if out == "fp8":
+        assert torch.equal(q.cpu().view(torch.uint8)[same_rows], qr.view(torch.uint8)[same_rows])
+    assert torch.equal(s.cpu()[same_rows], sr[same_rows])
+
+
+@pytest.mark.parametrize("norm", ["layer", "rms"])
+@pytest.mark.parametrize("out", ["fp8", "int8"])
+@pytest.mark.parametrize("B,S,H", [(2, 37, 128), (1, 300, 3072), (3, 20, 1000), (1, 64, 5376), (1, 33, 8192)])
+def test_fused_front_end_matches_oracle(cuda, norm, out, B, S, H):
+    x, scale, shift, idx = inputs(B, S, H, 20, seed=H + S, dev=cuda)
+    q, s, m = xops.norm_affine_quant(x, None, scale, shift, idx, 1e-6, N.NORM_LAYER if norm == "layer" else N.NORM_RMS,
+                                     torch.float8_e4m3fn if out == "fp8" else torch.int8, True)
+    check(x, None, scale, shift, idx, 1e-6, norm, out, q, s, m)
+
+
+@pytest.mark.parametrize("wdtype", [torch.bfloat16, torch.float32])
+def test_rms_with_weight_reference_signature(cuda, wdtype):
+    # the reference op's surface: norm_affine_quant(x, weight, scale, shift, indices, eps=1e-5) -> int8
+    x, scale, shift, idx = inputs(2, 17, 512, 3, seed=9, dev=cuda)
+    w = (torch.randn(512, generator=torch.Generator().manual_seed(4)) * 0.5 + 1).to(wdtype).to(cuda)
+    q, s = norm_affine_quant(x, w, scale, shift, idx)
+    assert q.dtype == torch.int8 and q.shape == (34, 512) and s.shape == (34,)
+    q, s, m = norm_affine_quant(x, w, scale, shift, idx, return_normed=True)
+    check(x, w, scale, shift, idx, 1e-5, "rms", "int8", q, s, m)
+
+
+def test_strided_input_and_tables(cuda):
+    big, scale, shift, idx = inputs(2, 24, 1024, 6, seed=3, dev=cuda)
+    x = big[:, :, 256:256 + 512]           # row stride 1024
+    tab = torch.cat([scale, shift], dim=1)  # tables with row stride 2048
+    sc, sh = tab[:, 256:768], tab[:, 1024 + 256:1024 + 768]
+    q, s, m = xops.norm_affine_quant(x, None, sc, sh, idx, 1e-6, N.NORM_LAYER, torch.float8_e4m3fn, True)
+    check(x, None, sc, sh, idx, 1e-6, "layer", "fp8", q, s, m)
+
+
+def test_out_of_range_index_poisons_only_its_row(cuda):
+    x, scale, shift, idx = inputs(1, 8, 256, 4, seed=1, dev=cuda)
+    idx = idx.clone()
+    idx[5] = 99
+    q, s, _ = xops.norm_affine_quant(x, None, scale, shift, idx, 1e-6, N.NORM_LAYER, torch.float8_e4m3fn, True)
+    assert torch.isnan(s[5]) and (q[5].view(torch.uint8) == 0x7F).all()
+    assert torch.isfinite(s[torch.arange(8, device=cuda) != 5]).all()
+
+
+def test_full_size_front_end_c5_share(cuda):
+    """LayerNorm(eps 1e-6) + 20-row AdaLN table + per-token FP8 at M=15,624, d=3,072."""
+    M, H = workloads.M_5S, workloads.D_MODEL
+    g = workloads.generator(0, cuda)
+    x, _ = workloads.activations(M, H, g, cuda)
+    shift, scale = workloads.adaln_tables(20, H, g, cuda)
+    idx = torch.randint(20, (M,), generator=g, device=cuda)
+    q, s, m = xops.norm_affine_quant(x[None], None, scale, shift, idx, 1e-6, N.NORM_LAYER, torch.float8_e4m3fn, True)
+    check(x[None], None, scale, shift, idx, 1e-6, "layer", "fp8", q, s, m)

@@ -1,0 +1,117 @@
+"""GPU parity of the quantizers: bytes and scales bit-exact against the oracle."""
+import numpy as np
+import pytest
+import torch
+
+import oracle.ref as R
+import xgen_amd  # noqa: F401
+from xgen_amd import workloads
+from xgen_amd.operator.h3_abs_peak import activation_abs_peak
+from xgen_amd.operator.h3_fp8_quant import quantize_activation
+
+pytestmark = pytest.mark.gpu
+xops = torch.ops.xgen_amd
+
+
+def u8(q):
+    return q.detach().cpu().view(torch.uint8)
+
+
+def assert_same_quant(q_gpu, s_gpu, q_ref, s_ref):
+    assert torch.equal(u8(q_gpu) if q_gpu.dtype == torch.float8_e4m3fn else q_gpu.cpu(),
+                       u8(q_ref) if q_ref.dtype == torch.float8_e4m3fn else q_ref)
+    assert torch.equal(s_gpu.cpu().view(torch.int32), s_ref.view(torch.int32))
+
+
+def test_hardware_e4m3_conversion_on_every_bf16_value(cuda):
+    """Rows holding +-448 have scale 1, so the bytes are the e4m3 conversion of
+    every finite bf16 value in [-448, 448]."""
+    bits = np.arange(1 << 16, dtype=np.uint32) << 16
+    v = bits.view(np.float32)
+    v = v[np.isfinite(v) & (np.abs(v) <= 448)]
+    pad = (-len(v)) % 511
+    v = np.concatenate([v, np.zeros(pad, np.float32)]).reshape(-1, 511)
+    rows = np.concatenate([np.full((v.shape[0], 1), 448.0, np.float32), v], axis=1)
+    x = torch.from_numpy(rows).to(torch.bfloat16)
+    q, s = xops.quantize_rows(x.to(cuda), torch.float8_e4m3fn)
+    assert (s.cpu() == 1.0).all()
+    expected = R.e4m3_encode(rows)
+    assert np.array_equal(u8(q).numpy(), expected)
+
+
+def rows_with_edges(M, K, dtype, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn((M, K), generator=g)
+    x[:, K // 7] *= 50
+    x[0] = 0
+    x[1] = -0.0
+    x[2] *= 1e-30
+    x[3] *= 1e-36  # amax below the fast-division gate
+    x[4, K // 2] = float("inf")
+    x[5, K // 3] = float("nan")
+    x[6] *= 3e4
+    if dtype == torch.float16:
+        x[6] /= 3e4  # keep the row finite in f16
+    return x.to(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("K", [16, 13, 64, 1000, 3072, 5376, 12288, 16384, 20000])
+@pytest.mark.parametrize("out", ["fp8", "int8"])
+def test_row_quantizers_match_oracle(cuda, dtype, K, out):
+    x = rows_with_edges(67, K, dtype, seed=K)
+    q, s = xops.quantize_rows(x.to(cuda), torch.float8_e4m3fn if out == "fp8" else torch.int8)
+    q_ref, s_ref = R.quantize_rows_c(x, out)
+    assert_same_quant(q, s, q_ref, s_ref)
+
+
+def test_row_quantizer_on_strided_rows(cuda):
+    x = rows_with_edges(40, 1024, torch.bfloat16).to(cuda)
+    view = x[:, 128:128 + 768]  # leading dimension 1024
+    q, s = xops.quantize_rows(view, torch.float8_e4m3fn)
+    q_ref, s_ref = R.quantize_rows_c(view.cpu().contiguous(), "fp8")
+    assert_same_quant(q, s, q_ref, s_ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(32, 128), (997, 5376), (2048, 14336)])
+def test_per_tensor_packing_matches_reference_quantizer(cuda, dtype, shape):
+    # x_base/tests/test_h3_cuda_precision_ops.py:35-58 (Triton pack == torch quantizer)
+    value = torch.randn(shape, dtype=dtype, generator=torch.Generator().manual_seed(1))
+    for sample in (value, torch.zeros_like(value)):
+        expected, scale = R.quantize_per_tensor(sample)
+        actual, actual_scale = quantize_activation(sample.to(cuda))
+        assert torch.equal(actual_scale.cpu(), scale)
+        assert torch.equal(u8(actual), expected.view(torch.uint8))
+
+
+def test_abs_peak_propagates_nan_and_inf(cuda):
+    x = torch.randn(3, 1000, dtype=torch.bfloat16)
+    assert activation_abs_peak(x.to(cuda)).item() == R.abs_peak(x).item()
+    x[1, 7] = -float("inf")
+    assert activation_abs_peak(x.to(cuda)).item() == float("inf")
+    x[2, 999] = float("nan")
+    assert torch.isnan(activation_abs_peak(x.to(cuda)))
+    tail = torch.randn(1001, dtype=torch.bfloat16)  # numel % 8 != 0
+    tail[1000] = 77.0
+    assert activation_abs_peak(tail.to(cuda)).item() == 77.0
+
+
+def test_pack_with_caller_scale(cuda):
+    x = torch.randn(4096, dtype=torch.bfloat16) * 10
+    scale = torch.tensor(0.0173, dtype=torch.float32)  # quotients exceed 448: clamped
+    q = xops.fp8_pack(x.to(cuda), scale.to(cuda))
+    ref = (x.float() / scale).clamp(-448, 448).to(torch.float8_e4m3fn)
+    assert torch.equal(u8(q), R.canonical_nan_e4m3(ref).view(torch.uint8))
+
+
+def test_full_size_token_quant_c2(cuda):
+    """C2 activations (M=15,624, K=3,072, outlier channels) quantized per token."""
+    g = workloads.generator(0, cuda)
+    x, _ = workloads.activations(workloads.M_5S, workloads.D_MODEL, g, cuda)
+    q, s = xops.quantize_rows(x, torch.float8_e4m3fn)
+    q_ref, s_ref = R.quantize_rows_c(x.cpu(), "fp8")
+    assert_same_quant(q, s, q_ref, s_ref)
+    qi, si = xops.quantize_rows(x, torch.int8)
+    qi_ref, si_ref = R.quantize_rows_c(x.cpu(), "int8")
+    assert_same_quant(qi, si, qi_ref, si_ref)

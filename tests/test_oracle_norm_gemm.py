@@ -1,0 +1,148 @@
+"""Pins the oracle's front end (LayerNorm/RMSNorm, AdaLN modulation, fused
+composite), GELU-tanh and GEMM accumulators."""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle.ref as R
+
+
+def test_layer_norm_f64_matches_torch_within_one_ulp():
+    torch.manual_seed(0)
+    x = torch.randn(256, 3072, dtype=torch.bfloat16)
+    x[:, :3] = (x[:, :3].float() * 50).to(torch.bfloat16)
+    ours = R.layer_norm_f64(x, 1e-6)
+    ref = F.layer_norm(x, (3072,), eps=1e-6)  # nn.LayerNorm(3072, elementwise_affine=False, eps=1e-6)
+    ulps = R.bf16_ulp_diff(ours, ref)
+    assert ulps.max() <= 1
+    assert (ulps == 0).float().mean() >= 0.999
+
+
+def test_layer_norm_f64_invariants():
+    torch.manual_seed(1)
+    x = torch.randn(64, 1024, dtype=torch.bfloat16) * 7 + 3
+    v = x.double()
+    n = (v - v.mean(-1, keepdim=True)) / torch.sqrt(v.var(-1, unbiased=False, keepdim=True) + 1e-6)
+    assert torch.allclose(n.mean(-1), torch.zeros(64, dtype=torch.float64), atol=1e-12)
+    assert torch.allclose((n * n).mean(-1), torch.ones(64, dtype=torch.float64), atol=1e-5)
+    assert torch.equal(R.layer_norm_f64(x, 1e-6), n.float().to(torch.bfloat16))
+
+
+def test_rms_norm_order_and_weight():
+    torch.manual_seed(2)
+    x = torch.randn(16, 512, dtype=torch.bfloat16)
+    w = torch.randn(512, dtype=torch.bfloat16)
+    v = x.double()
+    expected = (v * torch.rsqrt((v * v).mean(-1, keepdim=True) + 1e-5) * w.double()).float().to(torch.bfloat16)
+    assert R.bf16_ulp_diff(R.rms_norm_f64(x, 1e-5, w), expected).max() <= 1
+
+
+def test_modulate_eager_equals_explicit_rounding():
+    # the reference's own bitwise check of its fused modulation against eager bf16
+    # (x_base/tests/test_h3_indexed_affine.py:7-23)
+    g = torch.Generator().manual_seed(42)
+    x = torch.randn((2, 37, 128), generator=g, dtype=torch.bfloat16)
+    tables = torch.randn((7, 6 * 128), generator=g, dtype=torch.bfloat16)
+    shift, scale, *_ = tables.chunk(6, dim=-1)
+    idx = torch.randint(7, (37,), generator=g)
+    eager = R.modulate(x, scale.index_select(0, idx), shift.index_select(0, idx))
+    explicit = R.modulate_np(R.bf16_to_np(x), R.bf16_to_np(scale.index_select(0, idx)),
+                             R.bf16_to_np(shift.index_select(0, idx)))
+    assert np.array_equal(eager.float().numpy().view(np.uint32), explicit.view(np.uint32))
+
+
+def test_round_bf16_np_matches_torch():
+    rng = np.random.default_rng(3)
+    v = np.concatenate([rng.standard_normal(1 << 16).astype(np.float32) * 100,
+                        (np.arange(1 << 16, dtype=np.uint32) << 16 | 0x8000).view(np.float32)])
+    ours = R.round_bf16_np(v)
+    ref = torch.from_numpy(v).to(torch.bfloat16).float().numpy()
+    fin = np.isfinite(ref)
+    assert np.array_equal(ours[fin].view(np.uint32), ref[fin].view(np.uint32))
+
+
+@pytest.mark.parametrize("norm,out", [("layer", "fp8"), ("rms", "int8")])
+def test_norm_affine_quant_composite(norm, out):
+    g = torch.Generator().manual_seed(5)
+    B, S, H, T = 2, 13, 256, 5
+    x = torch.randn((B, S, H), generator=g).to(torch.bfloat16)
+    shift = (torch.randn((T, H), generator=g) * 0.1).to(torch.bfloat16)
+    scale = (torch.randn((T, H), generator=g) * 0.1).to(torch.bfloat16)
+    idx = torch.randint(T, (S,), generator=g)
+    q, s, m = R.norm_affine_quant(x, None, scale, shift, idx, 1e-6, norm, out)
+    assert q.shape == (B * S, H) and s.shape == (B * S,) and m.shape == (B * S, H)
+    # row r = b*S + s uses table row idx[s]
+    r = S + 4
+    n = (R.layer_norm_f64 if norm == "layer" else R.rms_norm_f64)(x[1, 4:5], 1e-6)
+    expect_m = R.modulate(n, scale[idx[4]][None], shift[idx[4]][None])
+    assert torch.equal(m[r:r + 1], expect_m)
+    qq, ss = (R.quantize_rows_fp8 if out == "fp8" else R.quantize_rows_int8)(m)
+    assert torch.equal(q.view(torch.uint8) if out == "fp8" else q, qq.view(torch.uint8) if out == "fp8" else qq)
+    assert torch.equal(s, ss)
+
+
+def test_gelu_tanh_against_closed_form():
+    v = torch.linspace(-12, 12, 20001).to(torch.bfloat16)
+    ours = R.gelu_tanh_bf16(v)
+    x = v.double()
+    exact = 0.5 * x * (1 + torch.tanh(math.sqrt(2 / math.pi) * (x + 0.044715 * x ** 3)))
+    # float32 evaluation of 1 + tanh(z) cancels for negative x (to 0 below ~-9):
+    # ulp comparison where it does not, absolute bound in the tail
+    body = x > -3
+    assert R.bf16_ulp_diff(ours[body], exact[body].float().to(torch.bfloat16)).max() <= 1
+    assert (ours[~body].double() - exact[~body]).abs().max() < 1e-5
+
+
+def test_fp8_accumulators_exact_against_integer_brute_force():
+    torch.manual_seed(7)
+    a = (torch.randn(17, 96) * 30).to(torch.float8_e4m3fn)
+    w = (torch.randn(23, 96) * 30).to(torch.float8_e4m3fn)
+    acc = R.fp8_accumulate_exact(a, w)
+    ai = (a.double() * 512).long()   # every e4m3 value is a multiple of 2^-9
+    wi = (w.double() * 512).long()
+    exact = (ai[:, None, :] * wi[None, :, :]).sum(-1)
+    assert torch.equal((acc * (1 << 18)).long(), exact)
+
+
+def test_int8_accumulators_exact():
+    torch.manual_seed(8)
+    a = torch.randint(-127, 128, (32, 1024), dtype=torch.int8)
+    w = torch.randint(-127, 128, (48, 1024), dtype=torch.int8)
+    acc = R.int8_accumulate_exact(a, w)
+    brute = (a.long()[:, None, :] * w.long()[None, :, :]).sum(-1)
+    assert torch.equal(acc, brute)
+    assert torch.equal(acc.int(), torch._int_mm(a, w.T.contiguous()))
+
+
+def test_fp8_linear_close_to_bf16_linear():
+    # the reference's FP8-vs-BF16 statistic (x_base/tests/test_h3_cuda_precision_ops.py:19-32)
+    torch.manual_seed(42)
+    weight = torch.randn(256, 128, dtype=torch.bfloat16)
+    bias = torch.randn(256, dtype=torch.bfloat16)
+    x = torch.randn(38, 128, dtype=torch.bfloat16)
+    qw, sw = R.quantize_per_tensor(weight)
+    qa, sa = R.quantize_per_tensor(x)
+    y = R.w8a8_linear_fp8(qa, sa, qw, sw, bias)
+    ref = F.linear(x.float(), weight.float(), bias.float())
+    rel = (y.float() - ref).square().mean().sqrt() / ref.square().mean().sqrt()
+    assert rel < 0.08
+    # per-token x per-channel scaling is at least as close
+    qa2, sa2 = R.quantize_rows_fp8(x)
+    qw2, sw2 = R.quantize_rows_fp8(weight)
+    y2 = R.w8a8_linear_fp8(qa2, sa2, qw2, sw2, bias)
+    assert R.rel_l2(y2, ref) <= R.rel_l2(y, ref) + 1e-3
+
+
+def test_cpu_fake_quant_path_equals_oracle_linear():
+    torch.manual_seed(9)
+    x = torch.randn(64, 256, dtype=torch.bfloat16)
+    w = (torch.randn(128, 256) * 0.02).to(torch.bfloat16)
+    b = (torch.randn(128) * 0.01).to(torch.bfloat16)
+    qw, sw = R.quantize_rows_fp8(w)
+    qa, sa = R.quantize_rows_fp8(x)
+    a = R.cpu_fake_quant_linear_fp8(x, qw, sw, b)
+    ref = R.w8a8_linear_fp8(qa, sa, qw, sw, b)
+    assert R.rel_l2(a, ref) < 1e-2 and R.cosine(a, ref) > 0.9999

@@ -1,0 +1,306 @@
+// Fused normalisation + AdaLN-table modulation + per-row quantization (gfx950).
+//
+// Replaces torch.ops.h3_phaa_nq2.fused (npu_fusion/f2_nq2/op_extension/nq2_queued.asc:53-61,
+// kernel npu_fusion/f2bc/op_kernel/f2bc_kernel.asc:57-107) and, with LayerNorm,
+// the eager front end of x_diffusers/x_diffusers/framework/transformer/hunyuan.py:390-393:
+//
+//   n = bf16(norm(x) [* weight]);  f = bf16(1 + scale[g]);
+//   m = bf16(bf16(n * f) + shift[g]);  (q, s) = quantize_row(m)
+//
+// with every intermediate rounded to bf16 as the eager bf16 ops round it
+// (x_base/x_base/operator/h3_indexed_affine.py:22-28).
+//
+// Layout: one row per wave (two waves per row above 4096 columns).  The row
+// stays in registers from the single HBM read to the single quantized write;
+// mean / variance / max |m| are wave reductions (plus an LDS exchange when a
+// row spans two waves).  The two table rows come from L2 (the table is small).
+#include "xgen_common.h"
+
+namespace xgen {
+
+namespace {
+
+constexpr int kThreads = 256;
+
+struct NormArgs {
+  const uint8_t *x;
+  int64_t seq;
+  int64_t rows;
+  int width;
+  int64_t xsb_bytes, xss_bytes;
+  const void *weight;
+  int weight_dtype;  // XGEN_DTYPE_NONE / BF16 / F32
+  float eps;
+  const uint8_t *scale_tab;
+  int64_t scale_stride_bytes;
+  const uint8_t *shift_tab;
+  int64_t shift_stride_bytes;
+  int64_t table_rows;
+  const int64_t *indices;
+  uint8_t *q;
+  float *token_scale;
+  uint8_t *normed;  // optional bf16 [rows, width]
+};
+
+template <int WPR>
+__device__ __forceinline__ float row_sum(float v, int wave, int lane, float *red) {
+  v = wave_sum_f32(v);
+  if constexpr (WPR > 1) {
+    __syncthreads();  // red[] reuse
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    const int w0 = (wave / WPR) * WPR;
+    v = red[w0];
+#pragma unroll
+    for (int i = 1; i < WPR; ++i) v += red[w0 + i];
+  }
+  return v;
+}
+
+template <int WPR>
+__device__ __forceinline__ uint32_t row_max_u32(uint32_t v, int wave, int lane, uint32_t *red) {
+  v = wave_max_u32(v);
+  if constexpr (WPR > 1) {
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    const int w0 = (wave / WPR) * WPR;
+    v = red[w0];
+#pragma unroll
+    for (int i = 1; i < WPR; ++i) v = v > red[w0 + i] ? v : red[w0 + i];
+  }
+  return v;
+}
+
+__device__ __forceinline__ void load_weight8(const void *w, int dtype, int ci, float (&wv)[8]) {
+  if (dtype == XGEN_DTYPE_BF16) {
+    const u32x4 c = *reinterpret_cast<const u32x4 *>(static_cast<const uint8_t *>(w) + (int64_t)ci * 16);
+    unpack8<XGEN_DTYPE_BF16>(c, wv);
+  } else {
+    const f32x4 *p = reinterpret_cast<const f32x4 *>(static_cast<const uint8_t *>(w) + (int64_t)ci * 32);
+    const f32x4 a = p[0], b = p[1];
+    wv[0] = a.x; wv[1] = a.y; wv[2] = a.z; wv[3] = a.w;
+    wv[4] = b.x; wv[5] = b.y; wv[6] = b.z; wv[7] = b.w;
+  }
+}
+
+template <int NORM, int OUT, int WPR, int CH>
+__global__ __launch_bounds__(kThreads) void norm_affine_quant_kernel(NormArgs a) {
+  constexpr int kRowsPerBlock = 4 / WPR;
+  __shared__ float red_f[4];
+  __shared__ uint32_t red_u[4];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + wave / WPR;
+  const bool row_ok = row < a.rows;
+  const int lane_in_row = (wave % WPR) * 64 + lane;
+  const int nchunks = a.width >> 3;
+  const int64_t r = row_ok ? row : 0;
+  const int64_t b = r / a.seq, s = r % a.seq;
+  const uint8_t *xr = a.x + b * a.xsb_bytes + s * a.xss_bytes;
+
+  // 1. one read of the row
+  u32x4 c[CH];
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    const int ci = lane_in_row + j * 64 * WPR;
+    c[j] = (row_ok && ci < nchunks) ? *reinterpret_cast<const u32x4 *>(xr + (int64_t)ci * 16)
+                                    : u32x4{0, 0, 0, 0};
+  }
+  const int64_t g = row_ok ? a.indices[s] : 0;
+  const bool g_ok = g >= 0 && g < a.table_rows;
+
+  // 2. statistics (fp32, two passes over registers)
+  const float inv_w = 1.0f / (float)a.width;
+  float rstd, mean = 0.0f;
+  if constexpr (NORM == XGEN_NORM_LAYER) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      float v[8];
+      unpack8<XGEN_DTYPE_BF16>(c[j], v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc += v[i];
+    }
+    mean = row_sum<WPR>(acc, wave, lane, red_f) / (float)a.width;
+    float acc2 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int ci = lane_in_row + j * 64 * WPR;
+      if (ci < nchunks) {
+        float v[8];
+        unpack8<XGEN_DTYPE_BF16>(c[j], v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float d = v[i] - mean;
+          acc2 = __builtin_fmaf(d, d, acc2);
+        }
+      }
+    }
+    const float var = row_sum<WPR>(acc2, wave, lane, red_f) / (float)a.width;
+    rstd = 1.0f / __builtin_sqrtf(var + a.eps);
+  } else {
+    float acc2 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      float v[8];
+      unpack8<XGEN_DTYPE_BF16>(c[j], v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc2 = __builtin_fmaf(v[i], v[i], acc2);
+    }
+    const float ms = row_sum<WPR>(acc2, wave, lane, red_f) / (float)a.width;
+    rstd = 1.0f / __builtin_sqrtf(ms + a.eps);
+  }
+  (void)inv_w;
+
+  // 3. normalise, modulate with the table row, keep m as packed bf16
+  const uint8_t *sr = a.scale_tab + (g_ok ? g : 0) * a.scale_stride_bytes;
+  const uint8_t *tr = a.shift_tab + (g_ok ? g : 0) * a.shift_stride_bytes;
+  u32x4 mp[CH];
+  u16x2 am = {0, 0};
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    const int ci = lane_in_row + j * 64 * WPR;
+    if (row_ok && g_ok && ci < nchunks) {
+      float v[8], sc[8], sh[8];
+      unpack8<XGEN_DTYPE_BF16>(c[j], v);
+      unpack8<XGEN_DTYPE_BF16>(*reinterpret_cast<const u32x4 *>(sr + (int64_t)ci * 16), sc);
+      unpack8<XGEN_DTYPE_BF16>(*reinterpret_cast<const u32x4 *>(tr + (int64_t)ci * 16), sh);
+      float n[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) n[i] = (NORM == XGEN_NORM_LAYER) ? (v[i] - mean) * rstd : v[i] * rstd;
+      if (a.weight_dtype != XGEN_DTYPE_NONE) {
+        float wv[8];
+        load_weight8(a.weight, a.weight_dtype, ci, wv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) n[i] *= wv[i];
+      }
+      uint32_t pk[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float n0 = round_bf16(n[2 * i]), n1 = round_bf16(n[2 * i + 1]);
+        const float f0 = round_bf16(1.0f + sc[2 * i]), f1 = round_bf16(1.0f + sc[2 * i + 1]);
+        const float p0 = round_bf16(n0 * f0), p1 = round_bf16(n1 * f1);
+        pk[i] = pack_bf16x2(p0 + sh[2 * i], p1 + sh[2 * i + 1]);
+      }
+      mp[j] = u32x4{pk[0], pk[1], pk[2], pk[3]};
+      am = absmax_chunk<XGEN_DTYPE_BF16>(mp[j], am);
+    } else {
+      mp[j] = u32x4{0, 0, 0, 0};
+    }
+  }
+  const uint32_t amax_bits = row_max_u32<WPR>(hmax_u16x2(am), wave, lane, red_u);
+  if (!row_ok) return;
+
+  // 4. quantize from registers
+  const float amax = Half2<XGEN_DTYPE_BF16>::from_absbits(amax_bits);
+  RowQuant p = (OUT == XGEN_DTYPE_E4M3) ? fp8_row_params(amax) : i8_row_params(amax);
+  uint8_t *qr = a.q + row * (int64_t)a.width;
+  uint8_t *nr = a.normed ? a.normed + row * (int64_t)a.width * 2 : nullptr;
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    const int ci = lane_in_row + j * 64 * WPR;
+    if (ci < nchunks) {
+      u32x2 out;
+      if (g_ok) {
+        float v[8];
+        unpack8<XGEN_DTYPE_BF16>(mp[j], v);
+        out = quant8<OUT>(v, p);
+      } else {
+        out = (OUT == XGEN_DTYPE_E4M3) ? u32x2{0x7f7f7f7fu, 0x7f7f7f7fu} : u32x2{0u, 0u};
+      }
+      *reinterpret_cast<u32x2 *>(qr + (int64_t)ci * 8) = out;
+      if (nr) *reinterpret_cast<u32x4 *>(nr + (int64_t)ci * 16) = mp[j];
+    }
+  }
+  if (lane_in_row == 0) a.token_scale[row] = g_ok ? p.s : __builtin_nanf("");
+}
+
+template <int NORM, int OUT, int WPR, int CH>
+void launch(const NormArgs &a, hipStream_t stream) {
+  constexpr int kRowsPerBlock = 4 / WPR;
+  const int64_t blocks = (a.rows + kRowsPerBlock - 1) / kRowsPerBlock;
+  norm_affine_quant_kernel<NORM, OUT, WPR, CH><<<dim3((unsigned)blocks), dim3(kThreads), 0, stream>>>(a);
+}
+
+template <int NORM, int OUT>
+void dispatch_width(const NormArgs &a, hipStream_t stream) {
+  const int w = a.width;
+  if (w <= 1024) launch<NORM, OUT, 1, 2>(a, stream);
+  else if (w <= 2048) launch<NORM, OUT, 1, 4>(a, stream);
+  else if (w <= 3072) launch<NORM, OUT, 1, 6>(a, stream);
+  else if (w <= 4096) launch<NORM, OUT, 1, 8>(a, stream);
+  else if (w <= 6144) launch<NORM, OUT, 2, 6>(a, stream);
+  else launch<NORM, OUT, 2, 8>(a, stream);
+}
+
+}  // namespace
+
+}  // namespace xgen
+
+using namespace xgen;
+
+extern "C" int xgen_norm_affine_quant(const void *x, int64_t batch, int64_t seq, int64_t width,
+                                      int64_t x_stride_batch, int64_t x_stride_seq, int norm_kind,
+                                      const void *norm_weight, int norm_weight_dtype, float eps,
+                                      const void *scale_table, int64_t scale_row_stride,
+                                      const void *shift_table, int64_t shift_row_stride,
+                                      int64_t table_rows, const int64_t *indices, int out_dtype,
+                                      void *q, float *token_scale, void *normed_out,
+                                      hipStream_t stream) {
+  const char *fn = "xgen_norm_affine_quant";
+  if (norm_kind != XGEN_NORM_LAYER && norm_kind != XGEN_NORM_RMS)
+    return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: unknown norm kind %d", fn, norm_kind);
+  if (!is_quant_dtype(out_dtype)) return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: output dtype must be E4M3 or I8", fn);
+  if (norm_weight_dtype != XGEN_DTYPE_NONE && norm_weight_dtype != XGEN_DTYPE_BF16 &&
+      norm_weight_dtype != XGEN_DTYPE_F32)
+    return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: norm weight dtype must be NONE, BF16 or F32", fn);
+  if ((norm_weight_dtype == XGEN_DTYPE_NONE) != (norm_weight == nullptr))
+    return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: norm weight pointer and dtype disagree", fn);
+  if (batch < 0 || seq < 0 || width <= 0 || table_rows <= 0)
+    return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: bad shape batch=%lld seq=%lld width=%lld tables=%lld", fn,
+                (long long)batch, (long long)seq, (long long)width, (long long)table_rows);
+  if (!(eps > 0.0f && eps < 1.0f)) return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: eps must be in (0, 1)", fn);
+  if (width > XGEN_NORM_MAX_WIDTH)
+    return fail(XGEN_ERR_UNSUPPORTED, "%s: width %lld exceeds %d", fn, (long long)width, XGEN_NORM_MAX_WIDTH);
+  if (x_stride_seq < width || scale_row_stride < width || shift_row_stride < width)
+    return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: row strides must be >= width", fn);
+  const int64_t rows = batch * seq;
+  if (rows == 0) return ok();
+  if (!x || !scale_table || !shift_table || !indices || !q || !token_scale)
+    return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+  if (width % 8 || x_stride_seq % 8 || x_stride_batch % 8 || scale_row_stride % 8 || shift_row_stride % 8 ||
+      !aligned16(x) || !aligned16(scale_table) || !aligned16(shift_table) || !aligned16(q) ||
+      (normed_out && !aligned16(normed_out)) || (norm_weight && !aligned16(norm_weight)))
+    return fail(XGEN_ERR_UNSUPPORTED, "%s: width and row strides must be multiples of 8 elements and "
+                "buffers 16-byte aligned", fn);
+  if (rows > 0x7fffffffLL * 4) return fail(XGEN_ERR_UNSUPPORTED, "%s: too many rows", fn);
+
+  NormArgs a;
+  a.x = static_cast<const uint8_t *>(x);
+  a.seq = seq;
+  a.rows = rows;
+  a.width = (int)width;
+  a.xsb_bytes = x_stride_batch * 2;
+  a.xss_bytes = x_stride_seq * 2;
+  a.weight = norm_weight;
+  a.weight_dtype = norm_weight_dtype;
+  a.eps = eps;
+  a.scale_tab = static_cast<const uint8_t *>(scale_table);
+  a.scale_stride_bytes = scale_row_stride * 2;
+  a.shift_tab = static_cast<const uint8_t *>(shift_table);
+  a.shift_stride_bytes = shift_row_stride * 2;
+  a.table_rows = table_rows;
+  a.indices = indices;
+  a.q = static_cast<uint8_t *>(q);
+  a.token_scale = token_scale;
+  a.normed = static_cast<uint8_t *>(normed_out);
+  if (norm_kind == XGEN_NORM_LAYER) {
+    if (out_dtype == XGEN_DTYPE_E4M3) dispatch_width<XGEN_NORM_LAYER, XGEN_DTYPE_E4M3>(a, stream);
+    else dispatch_width<XGEN_NORM_LAYER, XGEN_DTYPE_I8>(a, stream);
+  } else {
+    if (out_dtype == XGEN_DTYPE_E4M3) dispatch_width<XGEN_NORM_RMS, XGEN_DTYPE_E4M3>(a, stream);
+    else dispatch_width<XGEN_NORM_RMS, XGEN_DTYPE_I8>(a, stream);
+  }
+  return launch_status(fn);
+}

@@ -1,0 +1,339 @@
+// Dynamic quantizers for the W8A8 linear path (gfx950).
+//
+//  * xgen_quantize_rows  — per-row FP8 e4m3fn (the arithmetic of
+//    x_base/x_base/operator/h3_fp8.py:9-12 applied per row) or per-row INT8
+//    (npu_dynamic_quant as restated in npu_fusion/f2bc/op_kernel/f2bc_kernel.asc:89-107).
+//  * xgen_abs_peak / xgen_fp8_tensor_scale / xgen_fp8_pack — the per-tensor
+//    activation quantizer of x_base/x_base/operator/h3_fp8_quant.py:9-25 and
+//    h3_abs_peak.py:14-25.
+//
+// Row kernel layout: each row is read once into registers as 16-byte chunks
+// (8 elements), consecutive lanes on consecutive chunks; the row's NaN-
+// propagating max |x| is an integer max over the 16-bit magnitudes, reduced
+// across the wave with cross-lane shuffles (and across the row's waves through
+// LDS); the row is then quantized from registers and written as 8-byte chunks.
+#include "xgen_common.h"
+
+namespace xgen {
+
+namespace {
+
+constexpr int kThreads = 256;  // 4 waves per workgroup
+
+// WPR waves per row, CH chunks of 8 elements per lane: one row covers up to
+// 512 * WPR * CH elements.  Requires cols % 8 == 0 and 16-byte aligned rows.
+template <int DT, int OUT, int WPR, int CH>
+__global__ __launch_bounds__(kThreads) void quant_rows_vec_kernel(
+    const uint8_t *__restrict__ x, int64_t rows, int cols, int64_t ldx_bytes,
+    uint8_t *__restrict__ q, int64_t ldq, float *__restrict__ scale) {
+  constexpr int kRowsPerBlock = 4 / WPR;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int row_in_block = wave / WPR;
+  const int wave_in_row = wave % WPR;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + row_in_block;
+  const bool row_ok = row < rows;
+  const int nchunks = cols >> 3;
+  const int lane_in_row = wave_in_row * 64 + lane;
+
+  const uint8_t *xr = x + (row_ok ? row : 0) * ldx_bytes;
+  u32x4 c[CH];
+  u16x2 m = {0, 0};
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    const int ci = lane_in_row + j * 64 * WPR;
+    if (row_ok && ci < nchunks) {
+      c[j] = *reinterpret_cast<const u32x4 *>(xr + (int64_t)ci * 16);
+    } else {
+      c[j] = u32x4{0, 0, 0, 0};
+    }
+    m = absmax_chunk<DT>(c[j], m);
+  }
+  uint32_t amax_bits = wave_max_u32(hmax_u16x2(m));
+  if constexpr (WPR > 1) {
+    __shared__ uint32_t red[4];
+    if (lane == 0) red[wave] = amax_bits;
+    __syncthreads();
+    const int w0 = row_in_block * WPR;
+#pragma unroll
+    for (int i = 0; i < WPR; ++i) amax_bits = amax_bits > red[w0 + i] ? amax_bits : red[w0 + i];
+  }
+  if (!row_ok) return;
+  const float amax = Half2<DT>::from_absbits(amax_bits);
+  const RowQuant p = (OUT == XGEN_DTYPE_E4M3) ? fp8_row_params(amax) : i8_row_params(amax);
+
+  uint8_t *qr = q + row * ldq;
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    const int ci = lane_in_row + j * 64 * WPR;
+    if (ci < nchunks) {
+      float v[8];
+      unpack8<DT>(c[j], v);
+      *reinterpret_cast<u32x2 *>(qr + (int64_t)ci * 8) = quant8<OUT>(v, p);
+    }
+  }
+  if (lane_in_row == 0) scale[row] = p.s;
+}
+
+// Any width / alignment: one workgroup per row, two passes over global memory.
+template <int DT, int OUT>
+__global__ __launch_bounds__(kThreads) void quant_rows_generic_kernel(
+    const uint16_t *__restrict__ x, int64_t rows, int64_t cols, int64_t ldx,
+    uint8_t *__restrict__ q, int64_t ldq, float *__restrict__ scale) {
+  const int64_t row = blockIdx.x;
+  const uint16_t *xr = x + row * ldx;
+  uint32_t mb = 0;
+  for (int64_t c = threadIdx.x; c < cols; c += kThreads) {
+    uint32_t b = xr[c] & 0x7fffu;
+    mb = mb > b ? mb : b;
+  }
+  mb = wave_max_u32(mb);
+  __shared__ uint32_t red[4];
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mb;
+  __syncthreads();
+  mb = red[0];
+#pragma unroll
+  for (int i = 1; i < 4; ++i) mb = mb > red[i] ? mb : red[i];
+  const float amax = Half2<DT>::from_absbits(mb);
+  const RowQuant p = (OUT == XGEN_DTYPE_E4M3) ? fp8_row_params(amax) : i8_row_params(amax);
+  uint8_t *qr = q + row * ldq;
+  for (int64_t c = threadIdx.x; c < cols; c += kThreads) {
+    const uint32_t w = xr[c];
+    const float v = Half2<DT>::lo(w);
+    uint32_t b;
+    if constexpr (OUT == XGEN_DTYPE_E4M3) {
+      b = p.finite ? (pack_e4m3x4(clamp448(div_by_scale(v, p.s, p.mul)), 0.f, 0.f, 0.f) & 0xffu)
+                   : e4m3_slow_byte(v, p.s);
+    } else {
+      b = p.finite ? q_i8(v, p.mul) : i8_slow_byte(v, p.mul);
+    }
+    qr[c] = (uint8_t)b;
+  }
+  if (threadIdx.x == 0) scale[row] = p.s;
+}
+
+template <int DT, int OUT, int WPR, int CH>
+void launch_vec(const void *x, int64_t rows, int64_t cols, int64_t ldx, void *q, int64_t ldq,
+                float *scale, hipStream_t stream) {
+  constexpr int kRowsPerBlock = 4 / WPR;
+  const int64_t blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+  quant_rows_vec_kernel<DT, OUT, WPR, CH><<<dim3((unsigned)blocks), dim3(kThreads), 0, stream>>>(
+      static_cast<const uint8_t *>(x), rows, (int)cols, ldx * 2, static_cast<uint8_t *>(q), ldq,
+      scale);
+}
+
+template <int DT, int OUT>
+int quantize_rows_typed(const void *x, int64_t rows, int64_t cols, int64_t ldx, void *q,
+                        int64_t ldq, float *scale, hipStream_t stream) {
+  const bool vec = (cols % 8 == 0) && (ldx % 8 == 0) && (ldq % 8 == 0) && aligned16(x) &&
+                   ((reinterpret_cast<uintptr_t>(q) & 7u) == 0);
+  // Smallest (waves per row, chunks per lane) that covers the row.
+  if (vec && cols <= 512 * 2) {
+    launch_vec<DT, OUT, 1, 2>(x, rows, cols, ldx, q, ldq, scale, stream);
+  } else if (vec && cols <= 512 * 4) {
+    launch_vec<DT, OUT, 1, 4>(x, rows, cols, ldx, q, ldq, scale, stream);
+  } else if (vec && cols <= 512 * 6) {
+    launch_vec<DT, OUT, 1, 6>(x, rows, cols, ldx, q, ldq, scale, stream);
+  } else if (vec && cols <= 512 * 8) {
+    launch_vec<DT, OUT, 1, 8>(x, rows, cols, ldx, q, ldq, scale, stream);
+  } else if (vec && cols <= 1024 * 6) {
+    launch_vec<DT, OUT, 2, 6>(x, rows, cols, ldx, q, ldq, scale, stream);
+  } else if (vec && cols <= 1024 * 8) {
+    launch_vec<DT, OUT, 2, 8>(x, rows, cols, ldx, q, ldq, scale, stream);
+  } else if (vec && cols <= 2048 * 6) {
+    launch_vec<DT, OUT, 4, 6>(x, rows, cols, ldx, q, ldq, scale, stream);
+  } else if (vec && cols <= 2048 * 8) {
+    launch_vec<DT, OUT, 4, 8>(x, rows, cols, ldx, q, ldq, scale, stream);
+  } else {
+    quant_rows_generic_kernel<DT, OUT><<<dim3((unsigned)rows), dim3(kThreads), 0, stream>>>(
+        static_cast<const uint16_t *>(x), rows, cols, ldx, static_cast<uint8_t *>(q), ldq, scale);
+  }
+  return launch_status("xgen_quantize_rows");
+}
+
+// ---------------------------------------------------------------------------
+// per-tensor path
+// ---------------------------------------------------------------------------
+constexpr int kPeakBlocksMax = 1024;
+
+// Grid-stride NaN-propagating max |x| -> one partial (as 16-bit magnitude bits)
+// per workgroup.
+template <int DT>
+__global__ __launch_bounds__(kThreads) void abs_peak_partial_kernel(
+    const uint8_t *__restrict__ x, int64_t numel, uint32_t *__restrict__ partial) {
+  const int64_t nchunks = numel >> 3;
+  u16x2 m = {0, 0};
+  for (int64_t ci = (int64_t)blockIdx.x * kThreads + threadIdx.x; ci < nchunks;
+       ci += (int64_t)gridDim.x * kThreads) {
+    const u32x4 c = *reinterpret_cast<const u32x4 *>(x + ci * 16);
+    m = absmax_chunk<DT>(c, m);
+  }
+  uint32_t mb = hmax_u16x2(m);
+  // tail elements (numel % 8) handled by the first workgroup
+  if (blockIdx.x == 0) {
+    const uint16_t *xs = reinterpret_cast<const uint16_t *>(x);
+    for (int64_t i = (nchunks << 3) + threadIdx.x; i < numel; i += kThreads) {
+      const uint32_t b = xs[i] & 0x7fffu;
+      mb = mb > b ? mb : b;
+    }
+  }
+  mb = wave_max_u32(mb);
+  __shared__ uint32_t red[4];
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mb;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t r = red[0];
+    for (int i = 1; i < 4; ++i) r = r > red[i] ? r : red[i];
+    partial[blockIdx.x] = r;
+  }
+}
+
+// One workgroup: reduce the partials; write the peak (mode 0) or the FP8
+// per-tensor scale max(peak / 448, FLT_MIN) (mode 1).
+template <int DT>
+__global__ __launch_bounds__(kThreads) void abs_peak_final_kernel(const uint32_t *__restrict__ partial,
+                                                                  int n, float *__restrict__ out,
+                                                                  int mode) {
+  uint32_t mb = 0;
+  for (int i = threadIdx.x; i < n; i += kThreads) mb = mb > partial[i] ? mb : partial[i];
+  mb = wave_max_u32(mb);
+  __shared__ uint32_t red[4];
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mb;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t r = red[0];
+    for (int i = 1; i < 4; ++i) r = r > red[i] ? r : red[i];
+    const float peak = Half2<DT>::from_absbits(r);
+    out[0] = mode == 0 ? peak : fp8_row_params(peak).s;
+  }
+}
+
+// q[i] = e4m3(clamp(x[i] / scale[0])) over a contiguous tensor.
+template <int DT>
+__global__ __launch_bounds__(kThreads) void fp8_pack_kernel(const uint8_t *__restrict__ x,
+                                                            int64_t numel,
+                                                            const float *__restrict__ scale,
+                                                            uint8_t *__restrict__ q) {
+  // The scale may come from a caller (e.g. after a MAX all-reduce), so the
+  // quotient is not bounded by 448: IEEE division, NaN -> 0x7f, then clamp.
+  RowQuant p;
+  p.s = scale[0];
+  p.mul = 0.0f;
+  p.finite = false;
+  const int64_t nchunks = numel >> 3;
+  for (int64_t ci = (int64_t)blockIdx.x * kThreads + threadIdx.x; ci < nchunks;
+       ci += (int64_t)gridDim.x * kThreads) {
+    const u32x4 c = *reinterpret_cast<const u32x4 *>(x + ci * 16);
+    float v[8];
+    unpack8<DT>(c, v);
+    *reinterpret_cast<u32x2 *>(q + ci * 8) = quant8<XGEN_DTYPE_E4M3>(v, p);
+  }
+  if (blockIdx.x == 0) {
+    const uint16_t *xs = reinterpret_cast<const uint16_t *>(x);
+    for (int64_t i = (nchunks << 3) + threadIdx.x; i < numel; i += kThreads) {
+      const float v = Half2<DT>::lo(xs[i]);
+      q[i] = (uint8_t)e4m3_slow_byte(v, p.s);
+    }
+  }
+}
+
+int peak_blocks(int64_t numel) {
+  const int64_t chunks = numel >> 3;
+  int64_t b = (chunks + kThreads * 8 - 1) / (kThreads * 8);
+  if (b < 1) b = 1;
+  if (b > kPeakBlocksMax) b = kPeakBlocksMax;
+  return (int)b;
+}
+
+template <int DT>
+int abs_peak_typed(const void *x, int64_t numel, float *out, int mode, void *ws, hipStream_t stream) {
+  const int nb = peak_blocks(numel);
+  uint32_t *partial = static_cast<uint32_t *>(ws);
+  abs_peak_partial_kernel<DT><<<dim3(nb), dim3(kThreads), 0, stream>>>(
+      static_cast<const uint8_t *>(x), numel, partial);
+  int st = launch_status("xgen_abs_peak(partial)");
+  if (st != XGEN_OK) return st;
+  abs_peak_final_kernel<DT><<<dim3(1), dim3(kThreads), 0, stream>>>(partial, nb, out, mode);
+  return launch_status("xgen_abs_peak(final)");
+}
+
+int check_peak_args(const char *fn, int in_dtype, const void *x, int64_t numel, const void *out,
+                    void *ws, size_t ws_bytes) {
+  if (!is_input_dtype(in_dtype)) return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: input dtype must be BF16 or F16", fn);
+  if (numel <= 0) return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: numel must be positive", fn);
+  if (!x || !out || !ws) return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+  if (!aligned16(x)) return fail(XGEN_ERR_UNSUPPORTED, "%s: input must be 16-byte aligned", fn);
+  if (ws_bytes < xgen_abs_peak_workspace_bytes(numel))
+    return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: workspace too small (%zu < %zu bytes)", fn, ws_bytes,
+                xgen_abs_peak_workspace_bytes(numel));
+  return XGEN_OK;
+}
+
+}  // namespace
+
+}  // namespace xgen
+
+using namespace xgen;
+
+extern "C" int xgen_quantize_rows(int in_dtype, const void *x, int64_t rows, int64_t cols,
+                                  int64_t ldx, int out_dtype, void *q, int64_t ldq, float *scale,
+                                  hipStream_t stream) {
+  const char *fn = "xgen_quantize_rows";
+  if (!is_input_dtype(in_dtype)) return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: input dtype must be BF16 or F16", fn);
+  if (!is_quant_dtype(out_dtype)) return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: output dtype must be E4M3 or I8", fn);
+  if (rows < 0 || cols <= 0 || ldx < cols || ldq < cols)
+    return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: bad shape rows=%lld cols=%lld ldx=%lld ldq=%lld", fn,
+                (long long)rows, (long long)cols, (long long)ldx, (long long)ldq);
+  if (rows > 0x7fffffffLL) return fail(XGEN_ERR_UNSUPPORTED, "%s: too many rows", fn);
+  if (rows == 0) return ok();
+  if (!x || !q || !scale) return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+  if (in_dtype == XGEN_DTYPE_BF16) {
+    return out_dtype == XGEN_DTYPE_E4M3
+               ? quantize_rows_typed<XGEN_DTYPE_BF16, XGEN_DTYPE_E4M3>(x, rows, cols, ldx, q, ldq, scale, stream)
+               : quantize_rows_typed<XGEN_DTYPE_BF16, XGEN_DTYPE_I8>(x, rows, cols, ldx, q, ldq, scale, stream);
+  }
+  return out_dtype == XGEN_DTYPE_E4M3
+             ? quantize_rows_typed<XGEN_DTYPE_F16, XGEN_DTYPE_E4M3>(x, rows, cols, ldx, q, ldq, scale, stream)
+             : quantize_rows_typed<XGEN_DTYPE_F16, XGEN_DTYPE_I8>(x, rows, cols, ldx, q, ldq, scale, stream);
+}
+
+extern "C" size_t xgen_abs_peak_workspace_bytes(int64_t numel) {
+  return (size_t)peak_blocks(numel < 0 ? 0 : numel) * sizeof(uint32_t);
+}
+
+extern "C" int xgen_abs_peak(int in_dtype, const void *x, int64_t numel, float *peak,
+                             void *workspace, size_t workspace_bytes, hipStream_t stream) {
+  int st = check_peak_args("xgen_abs_peak", in_dtype, x, numel, peak, workspace, workspace_bytes);
+  if (st != XGEN_OK) return st;
+  return in_dtype == XGEN_DTYPE_BF16 ? abs_peak_typed<XGEN_DTYPE_BF16>(x, numel, peak, 0, workspace, stream)
+                                     : abs_peak_typed<XGEN_DTYPE_F16>(x, numel, peak, 0, workspace, stream);
+}
+
+extern "C" int xgen_fp8_tensor_scale(int in_dtype, const void *x, int64_t numel, float *scale,
+                                     void *workspace, size_t workspace_bytes, hipStream_t stream) {
+  int st = check_peak_args("xgen_fp8_tensor_scale", in_dtype, x, numel, scale, workspace, workspace_bytes);
+  if (st != XGEN_OK) return st;
+  return in_dtype == XGEN_DTYPE_BF16 ? abs_peak_typed<XGEN_DTYPE_BF16>(x, numel, scale, 1, workspace, stream)
+                                     : abs_peak_typed<XGEN_DTYPE_F16>(x, numel, scale, 1, workspace, stream);
+}
+
+extern "C" int xgen_fp8_pack(int in_dtype, const void *x, int64_t numel, const float *scale, void *q,
+                             hipStream_t stream) {
+  const char *fn = "xgen_fp8_pack";
+  if (!is_input_dtype(in_dtype)) return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: input dtype must be BF16 or F16", fn);
+  if (numel < 0) return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: numel must be non-negative", fn);
+  if (numel == 0) return ok();
+  if (!x || !scale || !q) return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+  if (!aligned16(x) || (reinterpret_cast<uintptr_t>(q) & 7u))
+    return fail(XGEN_ERR_UNSUPPORTED, "%s: input must be 16-byte and output 8-byte aligned", fn);
+  int64_t blocks = ((numel >> 3) + kThreads - 1) / kThreads;
+  if (blocks < 1) blocks = 1;
+  if (blocks > 8192) blocks = 8192;
+  if (in_dtype == XGEN_DTYPE_BF16)
+    fp8_pack_kernel<XGEN_DTYPE_BF16><<<dim3((unsigned)blocks), dim3(kThreads), 0, stream>>>(
+        static_cast<const uint8_t *>(x), numel, scale, static_cast<uint8_t *>(q));
+  else
+    fp8_pack_kernel<XGEN_DTYPE_F16><<<dim3((unsigned)blocks), dim3(kThreads), 0, stream>>>(
+        static_cast<const uint8_t *>(x), numel, scale, static_cast<uint8_t *>(q));
+  return launch_status(fn);
+}

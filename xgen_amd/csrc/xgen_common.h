@@ -1,0 +1,252 @@
+// Shared device helpers and host-side argument checking for the xgen_amd kernels.
+// gfx950 (CDNA4) only: wave64, hardware bf16 and OCP e4m3fn conversions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "xgen_amd.h"
+
+namespace xgen {
+
+// ----------------------------------------------------------------------------
+// host side: error reporting (defined in abi.hip)
+// ----------------------------------------------------------------------------
+int fail(int status, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int ok();
+// Maps the result of the launch just made to XGEN_OK / XGEN_ERR_HIP.
+int launch_status(const char *what);
+
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool is_input_dtype(int dt) { return dt == XGEN_DTYPE_BF16 || dt == XGEN_DTYPE_F16; }
+inline bool is_quant_dtype(int dt) { return dt == XGEN_DTYPE_E4M3 || dt == XGEN_DTYPE_I8; }
+
+// ----------------------------------------------------------------------------
+// device side
+// ----------------------------------------------------------------------------
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kE4M3Max = 448.0f;
+// torch.finfo(torch.float32).tiny, the clamp floor of the FP8 scale (h3_fp8.py:11).
+constexpr float kFltMin = 1.17549435082228750797e-38f;
+// fl32(1/127): the INT8 scale multiplier (f2bc_kernel.asc:97).
+constexpr float kInv127 = 1.0f / 127.0f;
+
+// --- 16-bit float element access on packed dwords --------------------------
+// Input element type tag: BF16 or F16, two elements per dword (element 0 in
+// the low half).
+template <int DT>
+struct Half2;
+
+template <>
+struct Half2<XGEN_DTYPE_BF16> {
+  static __device__ __forceinline__ float lo(uint32_t w) { return __uint_as_float(w << 16); }
+  static __device__ __forceinline__ float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+  // |x| bit patterns of both halves; as unsigned 16-bit integers they order
+  // like |x| with NaN above +inf, so an integer max propagates NaN.
+  static __device__ __forceinline__ u16x2 absbits(uint32_t w) {
+    return __builtin_bit_cast(u16x2, w & 0x7fff7fffu);
+  }
+  static __device__ __forceinline__ float from_absbits(uint32_t b) { return __uint_as_float(b << 16); }
+};
+
+template <>
+struct Half2<XGEN_DTYPE_F16> {
+  static __device__ __forceinline__ float lo(uint32_t w) {
+    return (float)__builtin_bit_cast(f16x2, w).x;
+  }
+  static __device__ __forceinline__ float hi(uint32_t w) {
+    return (float)__builtin_bit_cast(f16x2, w).y;
+  }
+  static __device__ __forceinline__ u16x2 absbits(uint32_t w) {
+    return __builtin_bit_cast(u16x2, w & 0x7fff7fffu);
+  }
+  static __device__ __forceinline__ float from_absbits(uint32_t b) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)b);
+  }
+};
+
+__device__ __forceinline__ u16x2 max_u16x2(u16x2 a, u16x2 b) {
+  return __builtin_elementwise_max(a, b);
+}
+
+// Round-to-nearest-even fp32 -> bf16, two at a time (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+}
+// fp32 rounded to bf16 precision, returned as fp32.
+__device__ __forceinline__ float round_bf16(float x) {
+  return __uint_as_float(pack_bf16x2(x, 0.0f) << 16);
+}
+
+// --- OCP e4m3fn packing -----------------------------------------------------
+// v_cvt_pk_fp8_f32 rounds to nearest even into e4m3fn (gfx950: OCP format).
+// Inputs here are always finite and within [-448, 448].
+__device__ __forceinline__ uint32_t pack_e4m3x4(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+  return (uint32_t)w;
+}
+
+// Saturating clamp of a finite value to [-448, 448] (v_med3_f32).
+__device__ __forceinline__ float clamp448(float v) {
+  return __builtin_amdgcn_fmed3f(v, -kE4M3Max, kE4M3Max);
+}
+
+// x / s for a finite positive normal s, given r = RN(1/s): q0 = RN(x*r),
+// e = x - q0*s (exact with an FMA unless it underflows), q = RN(q0 + e*r)
+// (Markstein's correction step).  With the amax gate of fp8_row_params the
+// e4m3 byte equals that of IEEE x / s for every (bf16|f16 x, amax) pair a row
+// quantizer can see (exhaustive oracle check).
+__device__ __forceinline__ float div_by_scale(float x, float s, float r) {
+  float q0 = x * r;
+  float e = __builtin_fmaf(-q0, s, x);
+  return __builtin_fmaf(e, r, q0);
+}
+
+// INT8 lane value: rint_half_even(x * alpha) as a byte.
+__device__ __forceinline__ uint32_t q_i8(float x, float alpha) {
+  float y = __builtin_rintf(x * alpha);
+  return (uint32_t)(int32_t)y & 0xffu;
+}
+__device__ __forceinline__ uint32_t pack_i8x4(float a, float b, float c, float d, float alpha) {
+  return q_i8(a, alpha) | (q_i8(b, alpha) << 8) | (q_i8(c, alpha) << 16) | (q_i8(d, alpha) << 24);
+}
+
+// --- wave64 reductions ---------------------------------------------------------
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    uint32_t o = __shfl_xor(v, off, 64);
+    v = v > o ? v : o;
+  }
+  return v;
+}
+__device__ __forceinline__ float wave_sum_f32(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Per-row quantization parameters derived from the row's max |x| (as fp32).
+struct RowQuant {
+  float s;      // stored scale
+  float mul;    // FP8: RN(1/s); INT8: alpha = RN(127/amax)
+  bool finite;  // FP8: scale finite (fast division valid)
+};
+
+// Rows with max |x| below this use IEEE division: for smaller scales the FMA
+// residual of div_by_scale can underflow and the e4m3 byte can differ (found
+// only for amax <= 2^-105 by the oracle's exhaustive check).
+constexpr float kFastDivMinAmax = 0x1p-100f;
+
+__device__ __forceinline__ RowQuant fp8_row_params(float amax) {
+  RowQuant p;
+  float s = amax / kE4M3Max;
+  s = (s < kFltMin) ? kFltMin : s;  // clamp_min keeps NaN
+  p.s = s;
+  p.mul = 1.0f / s;
+  p.finite = __builtin_isfinite(s) && amax >= kFastDivMinAmax;
+  return p;
+}
+
+__device__ __forceinline__ RowQuant i8_row_params(float amax) {
+  RowQuant p;
+  p.s = amax * kInv127;
+  p.mul = 127.0f / amax;
+  // amax == 0 (alpha = inf), inf or NaN: products may be NaN -> slow path.
+  p.finite = amax > 0.0f && __builtin_isfinite(amax);
+  return p;
+}
+
+// Slow per-element INT8 path (zero or non-finite amax): a NaN product gives 0,
+// so a zero row quantizes to zeros (swiglu_quant_kernel.asc:72-75).
+__device__ __forceinline__ uint32_t i8_slow_byte(float x, float alpha) {
+  float y = x * alpha;
+  y = (y == y) ? __builtin_rintf(y) : 0.0f;
+  return (uint32_t)(int32_t)y & 0xffu;
+}
+
+// Slow per-element FP8 path for rows whose scale is inf or NaN: IEEE division;
+// NaN results are written as the canonical e4m3fn NaN 0x7f.
+__device__ __forceinline__ uint32_t e4m3_slow_byte(float x, float s) {
+  float v = x / s;
+  if (v != v) return 0x7fu;
+  return pack_e4m3x4(clamp448(v), 0.0f, 0.0f, 0.0f) & 0xffu;
+}
+
+// Quantizes 8 fp32 values (one 16-byte input chunk) into 8 bytes.
+template <int OUT>
+__device__ __forceinline__ u32x2 quant8(const float (&v)[8], const RowQuant &p) {
+  u32x2 r;
+  if constexpr (OUT == XGEN_DTYPE_E4M3) {
+    if (p.finite) {
+      float q[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) q[i] = clamp448(div_by_scale(v[i], p.s, p.mul));
+      r.x = pack_e4m3x4(q[0], q[1], q[2], q[3]);
+      r.y = pack_e4m3x4(q[4], q[5], q[6], q[7]);
+    } else {
+      uint32_t b[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) b[i] = e4m3_slow_byte(v[i], p.s);
+      r.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+      r.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+    }
+  } else {
+    if (p.finite) {
+      r.x = pack_i8x4(v[0], v[1], v[2], v[3], p.mul);
+      r.y = pack_i8x4(v[4], v[5], v[6], v[7], p.mul);
+    } else {
+      uint32_t b[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) b[i] = i8_slow_byte(v[i], p.mul);
+      r.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+      r.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+    }
+  }
+  return r;
+}
+
+// Unpacks a 16-byte chunk of 8 bf16/f16 values to fp32.
+template <int DT>
+__device__ __forceinline__ void unpack8(const u32x4 &c, float (&v)[8]) {
+  v[0] = Half2<DT>::lo(c.x);
+  v[1] = Half2<DT>::hi(c.x);
+  v[2] = Half2<DT>::lo(c.y);
+  v[3] = Half2<DT>::hi(c.y);
+  v[4] = Half2<DT>::lo(c.z);
+  v[5] = Half2<DT>::hi(c.z);
+  v[6] = Half2<DT>::lo(c.w);
+  v[7] = Half2<DT>::hi(c.w);
+}
+
+template <int DT>
+__device__ __forceinline__ u16x2 absmax_chunk(const u32x4 &c, u16x2 m) {
+  m = max_u16x2(m, Half2<DT>::absbits(c.x));
+  m = max_u16x2(m, Half2<DT>::absbits(c.y));
+  m = max_u16x2(m, Half2<DT>::absbits(c.z));
+  m = max_u16x2(m, Half2<DT>::absbits(c.w));
+  return m;
+}
+
+__device__ __forceinline__ uint32_t hmax_u16x2(u16x2 m) {
+  return m.x > m.y ? (uint32_t)m.x : (uint32_t)m.y;
+}
+
+}  // namespace xgen

@@ -1,0 +1,132 @@
+"""FP8 W8A8 projection with the reference module surface, on gfx950 MFMA.
+
+Mirrors x_base/x_base/operator/h3_fp8.py:
+  * quantize_per_tensor(value)           h3_fp8.py:9-12
+  * H3FP8Linear(weight, bias=None)       h3_fp8.py:15-27  (buffers weight / weight_scale / bias, calls)
+  * H3FP8Linear.from_packed(w, s, bias)  h3_fp8.py:29-43
+  * H3FP8Linear.forward / _local_forward h3_fp8.py:45-68
+
+Default scaling is the reference's: one weight scale and one activation scale
+per call.  ``weight_scaling="channel"`` keeps one scale per output feature
+(quantize_per_tensor's arithmetic per row) and ``activation_scaling="token"``
+one scale per token: the W8A8 layout of the DiT linear path.  The GEMM and its
+dequant / bias / optional GELU-tanh epilogue are one HIP kernel; rows need no
+padding to 16 (the reference pads, h3_fp8.py:58-59).
+"""
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from .. import _native as N
+from ..ops import xops
+from .h3_fp8_quant import quantize_activation, quantize_activation_rows
+
+_FP8_MAX = 448.0
+_ACTIVATIONS = {None: N.ACT_NONE, "none": N.ACT_NONE, "gelu_tanh": N.ACT_GELU_TANH}
+
+
+def _device_weight(value: torch.Tensor) -> torch.Tensor:
+    if value.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("xgen_amd FP8 weight quantization requires a BF16/FP16 weight")
+    if not value.is_cuda:
+        if not torch.cuda.is_available():
+            raise RuntimeError("xgen_amd FP8 weight quantization requires a HIP device")
+        value = value.cuda()
+    return value.detach().contiguous()
+
+
+def quantize_per_tensor(value: torch.Tensor):
+    """(e4m3fn tensor, float32 0-dim scale) with scale = max(amax/448, FLT_MIN) (h3_fp8.py:9-12)."""
+    return quantize_activation(_device_weight(value))
+
+
+def quantize_per_channel(value: torch.Tensor):
+    """quantize_per_tensor's arithmetic applied to each row of a 2-D weight:
+    (e4m3fn [N,K], float32 [N])."""
+    if value.ndim != 2:
+        raise ValueError("per-channel quantization requires a 2-D weight")
+    return quantize_activation_rows(_device_weight(value))
+
+
+class H3FP8Linear(nn.Module):
+    """Keep FP8 weights; quantize activations to E4M3 and run the FP8 MFMA GEMM."""
+
+    def __init__(self, weight, bias=None, *, weight_scaling: str = "tensor",
+                 activation_scaling: str = "tensor", activation: str | None = None):
+        super().__init__()
+        if weight.ndim != 2 or weight.shape[0] % 16 or weight.shape[1] % 16:
+            raise ValueError("H3 FP8 requires projection dimensions divisible by 16")
+        if weight_scaling not in ("tensor", "channel") or activation_scaling not in ("tensor", "token"):
+            raise ValueError("weight_scaling must be 'tensor'|'channel', activation_scaling 'tensor'|'token'")
+        if activation not in _ACTIVATIONS:
+            raise ValueError(f"unsupported activation {activation!r}")
+        self.out_features, self.in_features = weight.shape
+        packed, scale = (quantize_per_tensor(weight) if weight_scaling == "tensor"
+                         else quantize_per_channel(weight))
+        self.register_buffer('weight', packed.contiguous())
+        self.register_buffer('weight_scale', scale.reshape(-1) if weight_scaling == "channel" else scale)
+        self.register_buffer('bias', bias.detach().clone().to(packed.device) if bias is not None else None)
+        self.activation_scaling = activation_scaling
+        self.activation = activation
+        self.calls = 0
+
+    @classmethod
+    def from_packed(cls, weight, scale, bias=None, *, activation_scaling: str = "tensor",
+                    activation: str | None = None):
+        """Reuse already quantized bytes and their original scale(s) without requantization."""
+        if weight.dtype != torch.float8_e4m3fn or weight.ndim != 2 or any(n % 16 for n in weight.shape):
+            raise ValueError('Packed H3 FP8 projection requires an aligned E4M3 matrix')
+        if scale.dtype != torch.float32 or scale.numel() not in (1, weight.shape[0]):
+            raise ValueError('Packed H3 FP8 projection requires one FP32 weight scale (or one per row)')
+        if activation_scaling not in ("tensor", "token") or activation not in _ACTIVATIONS:
+            raise ValueError("bad activation_scaling / activation")
+        result = cls.__new__(cls)
+        nn.Module.__init__(result)
+        result.out_features, result.in_features = weight.shape
+        result.register_buffer('weight', weight.contiguous())
+        result.register_buffer('weight_scale', scale.detach().clone())
+        result.register_buffer('bias', bias.detach().clone() if bias is not None else None)
+        result.activation_scaling = activation_scaling
+        result.activation = activation
+        result.calls = 0
+        return result
+
+    def forward(self, x):
+        return self._local_forward(x, self.bias)
+
+    def quantize_input(self, matrix):
+        """(e4m3fn [M,K], float32 scale [1] or [M]) for a [M,K] activation."""
+        if self.activation_scaling == "token":
+            return quantize_activation_rows(matrix)
+        group = getattr(self, 'activation_group', None)
+        packed, scale = quantize_activation(matrix, group=group)
+        return packed, scale.reshape(1)
+
+    def forward_quantized(self, packed, scale, out_dtype=torch.bfloat16, activation=None):
+        """GEMM on an already quantized activation (shared-QKV pattern,
+        x_diffusers/x_diffusers/framework/transformer/h3_npu_fusion.py:103-119)."""
+        act = _ACTIVATIONS[activation if activation is not None else self.activation]
+        out, _ = xops.scaled_mm(packed, self.weight, scale, self.weight_scale.reshape(-1), self.bias,
+                                out_dtype, act, False)
+        self.calls += 1
+        return out
+
+    def _local_forward(self, x, bias):
+        if not x.is_cuda or x.dtype not in (torch.bfloat16, torch.float16):
+            raise ValueError("H3 FP8 Linear requires CUDA BF16/FP16 input")
+        if x.shape[-1] != self.in_features:
+            raise ValueError("H3 FP8 Linear input width does not match its weight")
+        matrix = x.reshape(-1, self.in_features)
+        if not matrix.shape[0]:
+            return x.new_empty((*x.shape[:-1], self.out_features))
+        packed, scale = self.quantize_input(matrix)
+        output, _ = xops.scaled_mm(packed, self.weight, scale, self.weight_scale.reshape(-1), bias, x.dtype,
+                                   _ACTIVATIONS[self.activation], False)
+        self.calls += 1
+        return output.reshape(*x.shape[:-1], self.out_features)
+
+    def extra_repr(self):
+        return (f"in_features={self.in_features}, out_features={self.out_features}, "
+                f"weight_scale={tuple(self.weight_scale.shape)}, activation_scaling={self.activation_scaling}, "
+                f"activation={self.activation}")

@@ -1,0 +1,96 @@
+"""INT8 W8A8 projection with the reference module surface, on gfx950 MFMA.
+
+Mirrors x_base/x_base/operator/matmul.py:
+  * WeightQuantLinearModule(weight, bias, name=None)           matmul.py:36-50
+      per-output-row symmetric int8 weight + float32 antiquant_scale [N]
+  * WeightQuantLinearModule.forward(x)                         matmul.py:52-66
+      fp32 input cast to bf16; per-token int8 quantization; int8 GEMM with exact
+      int32 accumulation; dequant acc * pertoken_scale * antiquant_scale + bias
+  * enable_weight_quant_linear(model, quant_config, dtype)     matmul.py:141-202
+
+The quantizer is the one the reference restates for the NPU path
+(npu_fusion/f2bc/op_kernel/f2bc_kernel.asc:89-107): scale = amax * fl(1/127),
+q = rint_half_even(x * fl(127/amax)); a zero row gives zeros and scale 0.
+"""
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from .. import _native as N
+from ..config import QuantLayerConfig
+from ..ops import xops
+
+
+def dynamic_quant(x: torch.Tensor):
+    """Per-row symmetric int8 quantization of [..., K] -> (int8 like x, float32 [rows])
+    (the role of torch_npu.npu_dynamic_quant, matmul.py:39,60)."""
+    return xops.quantize_rows(x, torch.int8)
+
+
+class WeightQuantLinearModule(nn.Module):
+    def __init__(self, weight, bias, name=None):
+        super().__init__()
+        w = weight.detach()
+        if w.ndim != 2:
+            raise ValueError("WeightQuantLinearModule requires a 2-D weight")
+        if w.dtype == torch.float32:
+            w = w.to(torch.bfloat16)
+        if not w.is_cuda:
+            if not torch.cuda.is_available():
+                raise RuntimeError("xgen_amd INT8 weight quantization requires a HIP device")
+            w = w.cuda()
+        quant_weight, weight_scale = dynamic_quant(w.contiguous())
+        self.register_parameter('weight', nn.Parameter(quant_weight, requires_grad=False))
+        self.register_parameter('antiquant_scale', nn.Parameter(weight_scale, requires_grad=False))
+        if bias is not None:
+            self.register_parameter('bias', nn.Parameter(bias.detach().to(quant_weight.device), requires_grad=False))
+        else:
+            self.register_parameter('bias', None)
+        self.out_features, self.in_features = quant_weight.shape
+        self.name = name
+
+    def forward(self, x):
+        ori_shape = x.shape
+        ori_dtype = x.dtype
+        x = x.reshape(-1, ori_shape[-1])
+        # the quantizer takes BF16/FP16 (as npu_dynamic_quant): FP32 is cast to BF16
+        if x.dtype == torch.float32:
+            x = x.to(torch.bfloat16)
+            ori_dtype = torch.bfloat16
+        x_int8, pertoken_scale = dynamic_quant(x)
+        out = quant_matmul_raw(x_int8, pertoken_scale, self, ori_dtype)
+        return out.reshape(*ori_shape[:-1], -1)
+
+
+def quant_matmul_raw(q, scale, linear, out_dtype=torch.bfloat16, activation=N.ACT_NONE):
+    """int8 GEMM of a pre-quantized activation against a WeightQuantLinearModule."""
+    out, _ = xops.scaled_mm(q.reshape(-1, q.shape[-1]), linear.weight, scale.reshape(-1),
+                            linear.antiquant_scale.reshape(-1), linear.bias, out_dtype, activation, False)
+    return out
+
+
+def enable_weight_quant_linear(model: nn.Module, quant_config: QuantLayerConfig, dtype: str = 'w8a8') -> nn.Module:
+    """Replace every selected nn.Linear by a WeightQuantLinearModule (matmul.py:141-202).
+
+    Selection is quant_config.should_quantize(name, layer); layers whose weight
+    was released are skipped; LoRA '.base_layer' suffixes are undone in the
+    replacement name.  Only W8A8 is provided (the reference's transformer path
+    builds the W8A8 module for every CLI value, matmul.py:183).
+    """
+    if dtype != 'w8a8':
+        raise ValueError("xgen_amd provides the W8A8 module only")
+    for name, layer in list(model.named_modules()):
+        if not quant_config.should_quantize(name, layer):
+            continue
+        if getattr(layer, 'weight', None) is None:
+            continue
+        clean_name = name.replace(".base_layer", "")
+        bias = layer.bias.data if getattr(layer, 'bias', None) is not None else None
+        quant_module = WeightQuantLinearModule(layer.weight.data, bias, clean_name)
+        if '.' in clean_name:
+            parent, leaf = clean_name.rsplit('.', 1)
+            setattr(model.get_submodule(parent), leaf, quant_module)
+        else:
+            setattr(model, clean_name, quant_module)
+    return model

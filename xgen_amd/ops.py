@@ -1,0 +1,242 @@
+"""torch.library operators over the xgen_amd C ABI (namespace ``xgen_amd``).
+
+Each operator has a CUDA-key implementation (PyTorch-ROCm exposes HIP devices
+under the CUDA key) that allocates its outputs with the caching allocator and
+launches on the current stream, and a Meta implementation with the same shape
+and dtype contract, so shapes are checkable without a GPU.  This mirrors the
+reference's TORCH_LIBRARY + device + Meta registrations
+(x_base/x_base/operator/npu_fusion/f2_nq2/op_extension/nq2_queued.asc:53-61).
+Contract violations raise RuntimeError before any launch.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _native as N
+
+NAMESPACE = "xgen_amd"
+_LIB = None
+
+SCHEMAS = {
+    "quantize_rows": "quantize_rows(Tensor x, ScalarType out_dtype) -> (Tensor, Tensor)",
+    "abs_peak": "abs_peak(Tensor x) -> Tensor",
+    "fp8_tensor_scale": "fp8_tensor_scale(Tensor x) -> Tensor",
+    "fp8_pack": "fp8_pack(Tensor x, Tensor scale) -> Tensor",
+    "norm_affine_quant": (
+        "norm_affine_quant(Tensor x, Tensor? weight, Tensor scale, Tensor shift, Tensor indices, "
+        "float eps, int norm_kind, ScalarType out_dtype, bool return_normed) -> (Tensor, Tensor, Tensor)"),
+    "scaled_mm": (
+        "scaled_mm(Tensor a, Tensor w, Tensor a_scale, Tensor w_scale, Tensor? bias, "
+        "ScalarType out_dtype, int activation, bool return_acc) -> (Tensor, Tensor)"),
+}
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _rows_view(x: torch.Tensor) -> torch.Tensor:
+    """[..., K] -> [M, K] with unit last stride (copies only if needed)."""
+    m = x.reshape(-1, x.shape[-1])
+    if m.stride(-1) != 1 or (m.shape[0] > 1 and m.stride(0) < m.shape[1]):
+        m = m.contiguous()
+    return m
+
+
+# --------------------------------------------------------------------------- meta
+def _quantize_rows_meta(x, out_dtype):
+    _require(x.dtype in (torch.bfloat16, torch.float16), "quantize_rows: BF16/F16 input required")
+    _require(out_dtype in (torch.float8_e4m3fn, torch.int8), "quantize_rows: out_dtype must be float8_e4m3fn or int8")
+    _require(x.dim() >= 1 and x.shape[-1] > 0, "quantize_rows: input needs a non-empty last dimension")
+    rows = x.numel() // x.shape[-1]
+    return torch.empty(x.shape, dtype=out_dtype, device=x.device), torch.empty((rows,), dtype=torch.float32, device=x.device)
+
+
+def _peak_meta(x):
+    _require(x.dtype in (torch.bfloat16, torch.float16), "abs_peak: BF16/F16 input required")
+    return torch.empty((), dtype=torch.float32, device=x.device)
+
+
+def _pack_meta(x, scale):
+    _require(x.dtype in (torch.bfloat16, torch.float16), "fp8_pack: BF16/F16 input required")
+    _require(scale.dtype == torch.float32 and scale.numel() == 1, "fp8_pack: one float32 scale required")
+    return torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=x.device)
+
+
+def _norm_check(x, weight, scale, shift, indices, eps, norm_kind, out_dtype):
+    _require(x.dim() == 3 and x.dtype == torch.bfloat16 and x.stride(2) == 1 and x.shape[2] > 0,
+             "norm_affine_quant: BF16 [B,S,H] with last stride 1 required")
+    H = x.shape[2]
+    _require(H <= 8192, "norm_affine_quant: H <= 8192 required")
+    _require(weight is None or (weight.dim() == 1 and weight.shape[0] == H and weight.is_contiguous()
+                                and weight.dtype in (torch.bfloat16, torch.float32)),
+             "norm_affine_quant: BF16/F32 norm weight [H] or None required")
+    _require(scale.dim() == 2 and scale.shape[0] > 0 and scale.shape[1] == H and shift.shape == scale.shape
+             and scale.dtype == torch.bfloat16 and shift.dtype == torch.bfloat16
+             and scale.stride(1) == 1 and shift.stride(1) == 1,
+             "norm_affine_quant: BF16 tables [T,H] with last stride 1 required")
+    _require(indices.dim() == 1 and indices.shape[0] == x.shape[1] and indices.dtype == torch.int64
+             and indices.is_contiguous(), "norm_affine_quant: contiguous INT64 indices [S] required")
+    _require(0 < eps < 1, "norm_affine_quant: eps must be in (0, 1)")
+    _require(norm_kind in (N.NORM_LAYER, N.NORM_RMS), "norm_affine_quant: norm_kind must be 0 (layer) or 1 (rms)")
+    _require(out_dtype in (torch.float8_e4m3fn, torch.int8), "norm_affine_quant: out_dtype must be float8_e4m3fn or int8")
+
+
+def _norm_meta(x, weight, scale, shift, indices, eps, norm_kind, out_dtype, return_normed):
+    _norm_check(x, weight, scale, shift, indices, eps, norm_kind, out_dtype)
+    rows = x.shape[0] * x.shape[1]
+    H = x.shape[2]
+    normed = x.new_empty((rows, H) if return_normed else (0,))
+    return (torch.empty((rows, H), dtype=out_dtype, device=x.device),
+            torch.empty((rows,), dtype=torch.float32, device=x.device), normed)
+
+
+def _mm_check(a, w, a_scale, w_scale, bias, out_dtype, activation):
+    _require(a.dtype in (torch.float8_e4m3fn, torch.int8) and w.dtype == a.dtype,
+             "scaled_mm: operands must both be float8_e4m3fn or both int8")
+    _require(a.dim() == 2 and w.dim() == 2 and a.shape[1] == w.shape[1],
+             "scaled_mm: a [M,K] and w [N,K] required")
+    M, K = a.shape
+    Nf = w.shape[0]
+    _require(a_scale.dtype == torch.float32 and a_scale.numel() in (1, M),
+             "scaled_mm: float32 activation scale with 1 or M elements required")
+    _require(w_scale.dtype == torch.float32 and w_scale.numel() in (1, Nf),
+             "scaled_mm: float32 weight scale with 1 or N elements required")
+    _require(bias is None or (bias.dim() == 1 and bias.shape[0] == Nf
+                              and bias.dtype in (torch.bfloat16, torch.float16, torch.float32)),
+             "scaled_mm: bias [N] of BF16/F16/F32 required")
+    _require(out_dtype in (torch.bfloat16, torch.float16), "scaled_mm: out_dtype must be bfloat16 or float16")
+    _require(activation in (N.ACT_NONE, N.ACT_GELU_TANH), "scaled_mm: activation must be 0 (none) or 1 (gelu_tanh)")
+    _require(K % 16 == 0 and Nf % 16 == 0, "scaled_mm: K and N must be multiples of 16")
+
+
+def _mm_meta(a, w, a_scale, w_scale, bias, out_dtype, activation, return_acc):
+    _mm_check(a, w, a_scale, w_scale, bias, out_dtype, activation)
+    M, Nf = a.shape[0], w.shape[0]
+    acc_dtype = torch.float32 if a.dtype == torch.float8_e4m3fn else torch.int32
+    acc = torch.empty((M, Nf) if return_acc else (0,), dtype=acc_dtype, device=a.device)
+    return torch.empty((M, Nf), dtype=out_dtype, device=a.device), acc
+
+
+# --------------------------------------------------------------------------- device
+def _on_gpu(*ts):
+    dev = ts[0].device
+    _require(dev.type == "cuda", "xgen_amd operators require tensors on a HIP (cuda) device")
+    for t in ts[1:]:
+        if t is not None:
+            _require(t.device == dev, "xgen_amd operators require all tensors on the same device")
+
+
+def _quantize_rows_gpu(x, out_dtype):
+    _on_gpu(x)
+    q, scale = _quantize_rows_meta(x, out_dtype)
+    if x.numel() == 0:
+        return q, scale
+    m = _rows_view(x)
+    L = N.lib()
+    st = L.xgen_quantize_rows(N.dtype_code(x.dtype), m.data_ptr(), m.shape[0], m.shape[1], m.stride(0),
+                              N.dtype_code(out_dtype), q.data_ptr(), m.shape[1], scale.data_ptr(), N.stream_of(x))
+    N.check(st, "xgen_quantize_rows")
+    return q, scale
+
+
+def _peak_common(x, fn):
+    _on_gpu(x)
+    out = _peak_meta(x)
+    _require(x.numel() > 0, f"{fn}: empty input")
+    xc = x.contiguous()
+    L = N.lib()
+    ws_bytes = L.xgen_abs_peak_workspace_bytes(xc.numel())
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=x.device)
+    st = getattr(L, fn)(N.dtype_code(x.dtype), xc.data_ptr(), xc.numel(), out.data_ptr(), ws.data_ptr(),
+                        ws_bytes, N.stream_of(x))
+    N.check(st, fn)
+    return out
+
+
+def _peak_gpu(x):
+    return _peak_common(x, "xgen_abs_peak")
+
+
+def _tensor_scale_gpu(x):
+    return _peak_common(x, "xgen_fp8_tensor_scale")
+
+
+def _pack_gpu(x, scale):
+    _on_gpu(x, scale)
+    q = _pack_meta(x, scale)
+    if x.numel() == 0:
+        return q
+    xc = x.contiguous()
+    st = N.lib().xgen_fp8_pack(N.dtype_code(x.dtype), xc.data_ptr(), xc.numel(), scale.data_ptr(), q.data_ptr(),
+                               N.stream_of(x))
+    N.check(st, "xgen_fp8_pack")
+    return q
+
+
+def _norm_gpu(x, weight, scale, shift, indices, eps, norm_kind, out_dtype, return_normed):
+    _on_gpu(x, weight, scale, shift, indices)
+    q, s, normed = _norm_meta(x, weight, scale, shift, indices, eps, norm_kind, out_dtype, return_normed)
+    if q.numel() == 0:
+        return q, s, normed
+    wcode = N.DTYPE_NONE if weight is None else N.dtype_code(weight.dtype)
+    st = N.lib().xgen_norm_affine_quant(
+        x.data_ptr(), x.shape[0], x.shape[1], x.shape[2], x.stride(0), x.stride(1), norm_kind,
+        N.ptr(weight), wcode, float(eps), scale.data_ptr(), scale.stride(0), shift.data_ptr(), shift.stride(0),
+        scale.shape[0], indices.data_ptr(), N.dtype_code(out_dtype), q.data_ptr(), s.data_ptr(),
+        normed.data_ptr() if return_normed else None, N.stream_of(x))
+    N.check(st, "xgen_norm_affine_quant")
+    return q, s, normed
+
+
+def _mm_gpu(a, w, a_scale, w_scale, bias, out_dtype, activation, return_acc):
+    _on_gpu(a, w, a_scale, w_scale, bias)
+    out, acc = _mm_meta(a, w, a_scale, w_scale, bias, out_dtype, activation, return_acc)
+    M, K = a.shape
+    Nf = w.shape[0]
+    if M == 0:
+        return out, acc
+    a = a if a.stride(1) == 1 else a.contiguous()
+    w = w if w.stride(1) == 1 else w.contiguous()
+    a_scale = a_scale.contiguous()
+    w_scale = w_scale.contiguous()
+    bias = None if bias is None else bias.contiguous()
+    sa_stride = 1 if a_scale.numel() == M and M > 1 else 0
+    sw_stride = 1 if w_scale.numel() == Nf and Nf > 1 else 0
+    fn = "xgen_scaled_mm_fp8" if a.dtype == torch.float8_e4m3fn else "xgen_quant_matmul_int8"
+    st = getattr(N.lib(), fn)(
+        a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0), M, Nf, K, a_scale.data_ptr(), sa_stride,
+        w_scale.data_ptr(), sw_stride, N.ptr(bias), N.DTYPE_NONE if bias is None else N.dtype_code(bias.dtype),
+        activation, out.data_ptr(), N.dtype_code(out_dtype), out.stride(0),
+        acc.data_ptr() if return_acc else None, N.stream_of(a))
+    N.check(st, fn)
+    return out, acc
+
+
+_IMPLS = {
+    "quantize_rows": (_quantize_rows_gpu, _quantize_rows_meta),
+    "abs_peak": (_peak_gpu, _peak_meta),
+    "fp8_tensor_scale": (_tensor_scale_gpu, _peak_meta),
+    "fp8_pack": (_pack_gpu, _pack_meta),
+    "norm_affine_quant": (_norm_gpu, _norm_meta),
+    "scaled_mm": (_mm_gpu, _mm_meta),
+}
+
+
+def register() -> None:
+    """Defines the xgen_amd operators (idempotent; does not load the HIP library)."""
+    global _LIB
+    if _LIB is not None:
+        return
+    lib = torch.library.Library(NAMESPACE, "DEF")
+    for name, schema in SCHEMAS.items():
+        lib.define(schema)
+        gpu, meta = _IMPLS[name]
+        lib.impl(name, gpu, "CUDA")
+        lib.impl(name, meta, "Meta")
+    _LIB = lib
+
+
+register()
+xops = getattr(torch.ops, NAMESPACE)
