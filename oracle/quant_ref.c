@@ -19,8 +19,8 @@
  *                            16-bit inputs the row quantizers can see, that the
  *                            HIP kernels' division by the row scale
  *                            (q0 = x*r; e = fma(-q0, s, x); q = fma(e, r, q0),
- *                            r = 1/s, for amax >= 2^-100) gives the same e4m3
- *                            byte as IEEE x / s.
+ *                            r = 1/s, sign of x restored, for amax >= 2^-100)
+ *                            gives the same e4m3 byte as IEEE x / s.
  *
  * NaN convention: any NaN byte is written as 0x7f (canonical positive NaN).
  * Build: oracle/build.py (gcc -O2, no fast-math: float division and fmaf are
@@ -142,14 +142,14 @@ void oracle_quant_rows_int8(int fmt, const uint16_t *x, int64_t rows, int64_t co
 static float fast_div(float x, float s, float r) {
   const float q0 = x * r;
   const float e = fmaf(-q0, s, x);
-  return fmaf(e, r, q0);
+  return copysignf(fmaf(e, r, q0), x);
 }
 
 /* Every positive finite amax bit pattern in [amax_lo, amax_hi] and every
- * non-negative finite x <= amax of format fmt: count of e4m3 bytes that differ
+ * finite x with |x| <= amax of format fmt (both signs, so signed zeros and
+ * underflowing negative quotients are covered): count of e4m3 bytes that differ
  * between IEEE x / s and the HIP row quantizers' division, which takes
- * fast_div when amax >= 2^-100 and IEEE division otherwise.  (Division is odd
- * in x and e4m3 is sign-magnitude, so negative x mirror the checked ones.) */
+ * fast_div when amax >= 2^-100 and IEEE division otherwise. */
 int64_t oracle_check_fast_division(int fmt, uint32_t amax_lo, uint32_t amax_hi) {
   int64_t bad = 0;
   for (uint32_t ab = amax_lo; ab <= amax_hi; ++ab) {
@@ -159,13 +159,15 @@ int64_t oracle_check_fast_division(int fmt, uint32_t amax_lo, uint32_t amax_hi) 
     if (s < FLT_MIN) s = FLT_MIN;
     const float r = 1.0f / s;
     const int fast = amax >= 0x1p-100f;
-    for (uint32_t xb = 0; xb <= ab; ++xb) {
-      const float x = oracle_half_to_f32(fmt, (uint16_t)xb);
-      float ref = x / s;
-      float got = fast ? fast_div(x, s, r) : x / s;
-      ref = ref > 448.0f ? 448.0f : ref;
-      got = got > 448.0f ? 448.0f : got;
-      if (oracle_e4m3_encode(ref) != oracle_e4m3_encode(got)) ++bad;
+    for (uint32_t mag = 0; mag <= ab; ++mag) {
+      for (uint32_t sign = 0; sign <= 0x8000u; sign += 0x8000u) {
+        const float x = oracle_half_to_f32(fmt, (uint16_t)(mag | sign));
+        float ref = x / s;
+        float got = fast ? fast_div(x, s, r) : x / s;
+        ref = ref > 448.0f ? 448.0f : (ref < -448.0f ? -448.0f : ref);
+        got = got > 448.0f ? 448.0f : (got < -448.0f ? -448.0f : got);
+        if (oracle_e4m3_encode(ref) != oracle_e4m3_encode(got)) ++bad;
+      }
     }
   }
   return bad;

@@ -1,6 +1,13 @@
-"""GPU parity of the W8A8 GEMMs: INT8 accumulators bit-exact, FP8 accumulators
-within the float32 summation bound of the exact sum, bf16 outputs within
-rel-L2 <= 1e-2 and cosine >= 0.9999 of the oracle (observed far tighter)."""
+"""GPU parity of the W8A8 GEMMs: INT8 accumulators bit-exact; FP8 accumulators
+within FP8_ACC_REL * sum|a*w| of the exact sum; bf16 outputs within rel-L2 <=
+1e-2 and cosine >= 0.9999 of the oracle (observed far tighter).
+
+gfx950's v_mfma_f32_32x32x64_f8f6f4 does not accumulate like IEEE float32:
+probes show a product sharing an 8-product group with a much larger one is
+truncated away (65536 + 63 x 1 -> 65592; 200704 + 63 x 2^-6 -> 200704.875),
+and the final sum is truncated rather than rounded.  Measured on seeded
+workloads: max |acc - exact| = 2^-13.5 * sum|a*w|.  The bound below keeps a
+4x margin over that; bf16 outputs are insensitive to it (2^-9 rounding)."""
 import pytest
 import torch
 
@@ -14,6 +21,7 @@ xops = torch.ops.xgen_amd
 
 REL_L2_MAX = 1e-2
 COS_MIN = 0.9999
+FP8_ACC_REL = 2.0 ** -11
 
 
 def quantized_operands(M, K, Nf, cuda, kind, seed=0, outliers=True):
@@ -22,6 +30,19 @@ def quantized_operands(M, K, Nf, cuda, kind, seed=0, outliers=True):
     qa, sa = xops.quantize_rows(inp.x.to(cuda), dt)
     qw, sw = xops.quantize_rows(inp.weight.to(cuda), dt)
     return qa, sa, qw, sw, inp.bias.to(cuda)
+
+
+def assert_within_rounding(out, ref, acc_abs, sa, sw, bias, acc_err=None):
+    """Per element: |out - ref| <= 1 bf16 rounding of each side + the float32
+    epilogue error (fma vs. separate multiply/add) + the accumulator error."""
+    out, ref = out.detach().cpu().double(), ref.detach().cpu().double()
+    scale = sa.detach().cpu().double().reshape(-1, 1) * sw.detach().cpu().double().reshape(1, -1)
+    y_abs = acc_abs * scale.abs() + (0 if bias is None else bias.detach().cpu().double().abs())
+    extra = 2.0 ** -22 * y_abs
+    if acc_err is not None:
+        extra = extra + acc_err * scale.abs()
+    bound = 2.0 ** -7 * torch.maximum(out.abs(), ref.abs()) + extra + 1e-30
+    assert ((out - ref).abs() <= bound).all()
 
 
 def check_close(out, ref, tight=1e-3):
@@ -40,10 +61,11 @@ def test_fp8_gemm_accumulators_and_output(cuda, M, K, Nf):
     exact = R.fp8_accumulate_exact(qa.cpu(), qw.cpu())
     mag = R.decode_fp8(qa.cpu()).abs() @ R.decode_fp8(qw.cpu()).abs().T
     err = (acc.cpu().double() - exact).abs()
-    assert (err <= 2 * K * 2.0 ** -24 * mag + 1e-30).all()
+    acc_bound = FP8_ACC_REL * mag
+    assert (err <= acc_bound + 1e-30).all()
     ref = R.w8a8_linear_fp8(qa.cpu(), sa.cpu(), qw.cpu(), sw.cpu(), bias.cpu())
     check_close(out, ref)
-    assert R.bf16_ulp_diff(out, ref).max() <= 2
+    assert_within_rounding(out, ref, exact.abs(), sa, sw, bias, acc_bound)
 
 
 @pytest.mark.parametrize("M,K,Nf", SHAPES)
@@ -54,7 +76,7 @@ def test_int8_gemm_accumulators_bit_exact(cuda, M, K, Nf):
     assert torch.equal(acc.cpu().long(), exact)
     ref = R.w8a8_linear_int8(qa.cpu(), sa.cpu(), qw.cpu(), sw.cpu(), bias.cpu())
     check_close(out, ref)
-    assert R.bf16_ulp_diff(out, ref).max() <= 1
+    assert_within_rounding(out, ref, exact.abs().double(), sa, sw, bias)
 
 
 @pytest.mark.parametrize("kind", ["fp8", "int8"])

@@ -1,8 +1,11 @@
 """GPU parity of the fused norm + AdaLN modulate + quantize kernel.
 
 Contract (the reductions of the norm are order-dependent in float32):
-  * pre-quant bf16 rows within 1 ulp of the oracle (float64 statistics, eager
-    bf16 modulation), >= 99.9% bit-identical;
+  * pre-quant bf16 rows m >= 99.9% bit-identical to the oracle (float64
+    statistics, eager bf16 modulation); elsewhere the difference is what one
+    bf16 ulp of the normalised value n can become after the modulation:
+    |dm| <= ulp(bf16(n*f)) + ulp(m) (bf16(n*f) + shift may cancel, so ulps of
+    m alone do not bound it);
   * quantized bytes and scales bit-exact given the kernel's own pre-quant rows.
 """
 import pytest
@@ -30,11 +33,16 @@ def inputs(B, S, H, T, seed, dev):
 
 
 def check(x, weight, scale, shift, idx, eps, norm, out, q, s, m):
-    qr, sr, mr = R.norm_affine_quant(x.cpu(), None if weight is None else weight.cpu(), scale.cpu(), shift.cpu(),
-                                     idx.cpu(), eps, norm, out)
+    w = None if weight is None else weight.cpu()
+    qr, sr, mr = R.norm_affine_quant(x.cpu(), w, scale.cpu(), shift.cpu(), idx.cpu(), eps, norm, out)
+    B, S, H = x.shape
+    n = (R.layer_norm_f64 if norm == "layer" else R.rms_norm_f64)(x.cpu().reshape(B * S, H), eps, w)
+    g = idx.cpu().long().repeat(B)
+    nf = n * (1.0 + scale.cpu()[g])  # eager bf16: bf16(n * bf16(1 + scale))
     ulps = R.bf16_ulp_diff(m.cpu(), mr)
-    assert ulps.max() <= 1
     assert (ulps == 0).float().mean() >= 0.999
+    bound = 2.0 ** -7 * (nf.double().abs() + mr.double().abs()) + 1e-30
+    assert ((m.cpu().double() - mr.double()).abs() <= bound).all()
     q2, s2 = (R.quantize_rows_fp8 if out == "fp8" else R.quantize_rows_int8)(m.cpu())
     if out == "fp8":
         assert torch.equal(q.cpu().view(torch.uint8), q2.view(torch.uint8))

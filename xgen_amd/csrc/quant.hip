@@ -204,7 +204,7 @@ __global__ __launch_bounds__(kThreads) void abs_peak_final_kernel(const uint32_t
     uint32_t r = red[0];
     for (int i = 1; i < 4; ++i) r = r > red[i] ? r : red[i];
     const float peak = Half2<DT>::from_absbits(r);
-    out[0] = mode == 0 ? peak : fp8_row_params(peak).s;
+    out[0] = mode == 0 ? canonical_nan(peak) : fp8_row_params(peak).s;
   }
 }
 

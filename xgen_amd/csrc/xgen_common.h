@@ -113,10 +113,12 @@ __device__ __forceinline__ float clamp448(float v) {
 // (Markstein's correction step).  With the amax gate of fp8_row_params the
 // e4m3 byte equals that of IEEE x / s for every (bf16|f16 x, amax) pair a row
 // quantizer can see (exhaustive oracle check).
+// The correction adds e = +0 to q0 = -0 for x = -0 (giving +0), so the sign
+// of x is restored: IEEE x / s keeps it for zero and underflowing quotients.
 __device__ __forceinline__ float div_by_scale(float x, float s, float r) {
   float q0 = x * r;
   float e = __builtin_fmaf(-q0, s, x);
-  return __builtin_fmaf(e, r, q0);
+  return __builtin_copysignf(__builtin_fmaf(e, r, q0), x);
 }
 
 // INT8 lane value: rint_half_even(x * alpha) as a byte.
@@ -143,6 +145,10 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
   return v;
 }
 
+// NaN results are stored as the canonical quiet NaN 0x7fc00000 (division
+// and conversions may produce other payloads).
+__device__ __forceinline__ float canonical_nan(float v) { return v == v ? v : __builtin_nanf(""); }
+
 // Per-row quantization parameters derived from the row's max |x| (as fp32).
 struct RowQuant {
   float s;      // stored scale
@@ -159,7 +165,7 @@ __device__ __forceinline__ RowQuant fp8_row_params(float amax) {
   RowQuant p;
   float s = amax / kE4M3Max;
   s = (s < kFltMin) ? kFltMin : s;  // clamp_min keeps NaN
-  p.s = s;
+  p.s = canonical_nan(s);
   p.mul = 1.0f / s;
   p.finite = __builtin_isfinite(s) && amax >= kFastDivMinAmax;
   return p;
@@ -167,7 +173,7 @@ __device__ __forceinline__ RowQuant fp8_row_params(float amax) {
 
 __device__ __forceinline__ RowQuant i8_row_params(float amax) {
   RowQuant p;
-  p.s = amax * kInv127;
+  p.s = canonical_nan(amax * kInv127);
   p.mul = 127.0f / amax;
   // amax == 0 (alpha = inf), inf or NaN: products may be NaN -> slow path.
   p.finite = amax > 0.0f && __builtin_isfinite(amax);
