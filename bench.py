@@ -43,7 +43,56 @@ def parse():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--only", default="", help="comma list of extra kernels to time (default all)")
+    p.add_argument("--kernels", default="",
+                   help="profiling mode: launch only these kernels (comma list of "
+                        f"{','.join(PROFILE_KERNELS)}) warmup+steps times each, print their timings, exit")
     return p.parse_args()
+
+
+PROFILE_KERNELS = ("gemm_fp8_qkv", "gemm_int8_qkv", "gemm_fp8_ffn_up_gelu", "gemm_fp8_ffn_down", "quant_rows_fp8",
+                   "front_end_ln_mod_quant_fp8", "copy_1gib")
+
+
+def profile_kernels(names, steps, warmup):
+    """Runs only the named kernels on the bench workload (for rocprofv3 --pmc /
+    --kernel-trace); copy_1gib is a plain 1 GiB device copy (reads and writes
+    2^30 bytes) used to calibrate the HBM byte counters."""
+    import torch
+    import xgen_amd  # noqa: F401
+    from xgen_amd import _native as N
+    from xgen_amd import workloads as W
+    xops = torch.ops.xgen_amd
+    fp8 = torch.float8_e4m3fn
+    dev = torch.device("cuda:0")
+    M, K = W.M_5S, W.D_MODEL
+    g = W.generator(0, dev)
+    x, _ = W.activations(M, K, g, dev)
+    out = {}
+    for name in names:
+        if name not in PROFILE_KERNELS:
+            raise SystemExit(f"unknown kernel {name}; choose from {PROFILE_KERNELS}")
+        if name.startswith("gemm"):
+            lin = {"gemm_fp8_qkv": "qkv", "gemm_int8_qkv": "qkv", "gemm_fp8_ffn_up_gelu": "ffn_up",
+                   "gemm_fp8_ffn_down": "ffn_down"}[name]
+            w, b = W.weight(lin, g, dev)
+            dt = torch.int8 if "int8" in name else fp8
+            a_in = x if lin != "ffn_down" else torch.randn((M, 4 * K), generator=g, device=dev).to(torch.bfloat16)
+            qa, sa = xops.quantize_rows(a_in, dt)
+            qw, sw = xops.quantize_rows(w, dt)
+            act = N.ACT_GELU_TANH if "gelu" in name else N.ACT_NONE
+            fn = lambda: xops.scaled_mm(qa, qw, sa, sw, b, torch.bfloat16, act, False)  # noqa: E731
+        elif name == "quant_rows_fp8":
+            fn = lambda: xops.quantize_rows(x, fp8)  # noqa: E731
+        elif name == "front_end_ln_mod_quant_fp8":
+            shift, scale = W.adaln_tables(20, K, g, dev)
+            idx = torch.randint(20, (M,), generator=g, device=dev)
+            fn = lambda: xops.norm_affine_quant(x[None], None, scale, shift, idx, 1e-6, N.NORM_LAYER, fp8, False)  # noqa: E731
+        else:
+            src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+            dst = torch.empty_like(src)
+            fn = lambda: dst.copy_(src)  # noqa: E731
+        out[name] = {"ms": timed(fn, steps, warmup)}
+    print(json.dumps({"profile_kernels": out}), flush=True)
 
 
 def timed(fn, iters, warmup):
@@ -85,6 +134,9 @@ def cpu_baseline(x_cpu, qw, sw, bias, flop_per_row, budget_s=12.0):
 
 def main():
     args = parse()
+    if args.kernels:
+        profile_kernels(args.kernels.split(","), args.steps, args.warmup)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
               "(the W8A8 linear path has no cross-GPU work at one SP rank's token share)", file=sys.stderr)
