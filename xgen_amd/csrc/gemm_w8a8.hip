@@ -8,13 +8,14 @@
 //
 // out[m, n] = act(cvt(acc[m, n] * (sa[m] * sw[n]) + bias[n])),  acc = sum_k a[m,k] w[n,k]
 //
-// Tiling: a 256x256 output tile per workgroup of 4 waves (2x2, 128x128 per
-// wave = 4x4 MFMA 32x32 blocks, accumulators in AGPRs), K in steps of 128
-// bytes, double-buffered in LDS (2 stages x (32 KB activations + 32 KB
-// weights)).  Global loads are bounds-checked buffer loads (rows past M/N read
-// as zero), staged through registers and written to LDS with the 16-byte chunk
-// index XOR-swizzled by (row & 7), so both the 128-bit LDS writes and the
-// 128-bit MFMA-operand reads are bank-conflict free.
+// Tiling: a 256x256 output tile per workgroup of WM x WN waves; each wave owns
+// a (256/WM) x (256/WN) block of 32x32 MFMA tiles with accumulators in AGPRs.
+// With 8 waves (2 per SIMD) one wave issues MFMAs while the other waits on
+// LDS or the barrier.  K advances in stages of 64 bytes through a ring of 4
+// LDS slots (4 x (16 KB activations + 16 KB weights)); operands go global ->
+// LDS by bounds-checked buffer loads on the LDS-DMA path (no VGPR staging;
+// rows past M/N and the K tail read as zero), issued 3 stages ahead of the
+// MFMAs that consume them, one barrier per stage.
 //
 // The MFMA's A operand is the weight tile and its B operand the activation
 // tile, so each lane's accumulator column is one token and its 4 consecutive
@@ -31,12 +32,17 @@ namespace xgen {
 
 namespace {
 
-constexpr int BM = 256, BN = 256, BK = 128;
-constexpr int kThreads = 256;
-constexpr int kTileBytes = 256 * BK;  // one operand tile per stage
+constexpr int BM = 256, BN = 256;
+constexpr int BK = 64;                        // K bytes per pipeline stage
+constexpr int kStages = 4;                    // LDS ring depth
+constexpr int kTileBytes = 256 * BK;          // one operand tile of one stage: 16 KB
+constexpr int kStageBytes = 2 * kTileBytes;   // activations + weights: 32 KB
 constexpr int kGroupM = 8;
 constexpr int kBufferFlags = 0x00020000;  // raw buffer, 32-bit dword format (gfx9)
 constexpr uint32_t kOutOfRange = 0x80000000u;
+
+// Waves per workgroup (along M and N) of the production configuration.
+constexpr int kWavesM = 2, kWavesN = 4;
 
 struct GemmArgs {
   const uint8_t *a;
@@ -56,6 +62,15 @@ struct GemmArgs {
   uint32_t a_bytes, w_bytes;
 };
 
+// LDS layout of one operand tile of one stage: 256 rows x 64 bytes (4 chunks
+// of 16 bytes).  Chunk c of row r is stored at chunk position c ^ ((r >> 2) & 3).
+// gfx950's LDS has 64 banks (256 bytes per cycle): the 16 lanes one 128-bit
+// access serves (rows r..r+15, one logical chunk) then hit 16 distinct 16-byte
+// bank groups.
+__device__ __forceinline__ int swz(int row, int chunk) {
+  return row * BK + ((chunk ^ ((row >> 2) & 3)) << 4);
+}
+
 template <bool FP8>
 struct Mfma;
 
@@ -63,12 +78,11 @@ template <>
 struct Mfma<true> {
   typedef f32x16 acc_t;
   typedef i32x8 frag_t;
-  static constexpr int kSteps = BK / 64;  // 32x32x64
+  static constexpr int kSteps = BK / 64;  // 32x32x64: one step per stage
   static __device__ __forceinline__ frag_t load(const uint8_t *tile, int row, int ks, int lane) {
     const int c0 = ks * 4 + (lane >> 5) * 2;
-    const int sw = lane & 7;
-    const u32x4 lo = *reinterpret_cast<const u32x4 *>(tile + row * BK + ((c0 ^ sw) << 4));
-    const u32x4 hi = *reinterpret_cast<const u32x4 *>(tile + row * BK + (((c0 + 1) ^ sw) << 4));
+    const u32x4 lo = *reinterpret_cast<const u32x4 *>(tile + swz(row, c0));
+    const u32x4 hi = *reinterpret_cast<const u32x4 *>(tile + swz(row, c0 + 1));
     return frag_t{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
   }
   static __device__ __forceinline__ acc_t mma(const frag_t &w, const frag_t &x, const acc_t &c) {
@@ -82,10 +96,10 @@ template <>
 struct Mfma<false> {
   typedef i32x16 acc_t;
   typedef i32x4 frag_t;
-  static constexpr int kSteps = BK / 32;  // 32x32x32
+  static constexpr int kSteps = BK / 32;  // 32x32x32: two steps per stage
   static __device__ __forceinline__ frag_t load(const uint8_t *tile, int row, int ks, int lane) {
     const int c = ks * 2 + (lane >> 5);
-    const u32x4 v = *reinterpret_cast<const u32x4 *>(tile + row * BK + ((c ^ (lane & 7)) << 4));
+    const u32x4 v = *reinterpret_cast<const u32x4 *>(tile + swz(row, c));
     return frag_t{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
   }
   static __device__ __forceinline__ acc_t mma(const frag_t &w, const frag_t &x, const acc_t &c) {
@@ -93,6 +107,23 @@ struct Mfma<false> {
   }
   static __device__ __forceinline__ float to_f32(int v) { return (float)v; }
 };
+
+// One 16-byte-per-lane buffer load on the LDS-DMA path: lane l's 16 bytes land
+// at lds + 16 * l.  (A plain device function: called directly from the kernel
+// template, the device-only builtin would keep the host pass from emitting the
+// kernel's launch stub.)
+__device__ __forceinline__ void dma_load16(__amdgpu_buffer_rsrc_t rsrc, uint8_t *lds, uint32_t offset) {
+  typedef __attribute__((address_space(3))) void *lds_ptr_t;
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr_t)lds, 16, offset, 0, 0, 0);
+}
+
+// s_waitcnt constraining only the vector-memory counter (gfx9 encoding: vmcnt
+// in bits [3:0] and [15:14]; expcnt [6:4] and lgkmcnt [11:8] left at max).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
 
 // GELU with the tanh approximation, via tanh(z) = 2*sigmoid(2z) - 1:
 // 0.5*x*(1 + tanh(z)) = x / (1 + exp(-2z)),  z = sqrt(2/pi) * (x + 0.044715 x^3).
@@ -132,149 +163,273 @@ __device__ __forceinline__ void load_bias4(const void *bias, int dtype, int n, f
   }
 }
 
-template <bool FP8, int ACT, int OUT_DT, bool ACC_OUT>
-__global__ __launch_bounds__(kThreads, 1) void gemm_w8a8_kernel(GemmArgs p) {
-  typedef Mfma<FP8> T;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * 2 * kTileBytes];
-
-  // --- tile selection (XCD-contiguous ranges, grouped rows) ----------------
-  const int bid = blockIdx.x;
-  const int pid = (bid & 7) * p.per_xcd + (bid >> 3);
-  if (pid >= p.tiles_m * p.tiles_n) return;
-  const int group_size = kGroupM * p.tiles_n;
+// Output tile -> (m0, n0): tiles are walked in groups of kGroupM tile-rows.
+__device__ __forceinline__ void tile_origin(int pid, int tiles_m, int tiles_n, int &m0, int &n0) {
+  const int group_size = kGroupM * tiles_n;
   const int group = pid / group_size;
   const int first_m = group * kGroupM;
-  const int gm = min(p.tiles_m - first_m, kGroupM);
+  const int gm = min(tiles_m - first_m, kGroupM);
   const int in_group = pid - group * group_size;
-  const int m0 = (first_m + in_group % gm) * BM;
-  const int n0 = (in_group / gm) * BN;
+  m0 = (first_m + in_group % gm) * BM;
+  n0 = (in_group / gm) * BN;
+}
+
+// Persistent kernel: one workgroup per CU.  The tiles of XCD x (workgroups
+// x, x+8, ... run there) are the contiguous range [x*per_xcd, (x+1)*per_xcd),
+// dealt round-robin to that XCD's workgroups, so the tiles running at once on
+// one XCD are neighbours in its L2.  The stage sequence of all of a
+// workgroup's tiles is one stream: the DMA ring runs across tile boundaries,
+// so a tile's epilogue overlaps the loads of the next tile's first stages.
+//
+// Epilogue.  gfx9 has a single in-order vector-memory counter, so a global
+// load in the epilogue would also wait for the DMA still in flight.  The
+// per-token scales, per-channel scales and bias of a tile therefore arrive in
+// LDS by the same DMA path, with the tile's first stage (kParamSets buffers,
+// indexed by tile), and are read with LDS loads.  Outputs are transposed
+// through the ring slot just consumed (free until the next barrier) so every
+// store writes full 128-byte row segments.
+constexpr int kParamBytes = 1024;  // 256 x 4 bytes: one parameter row of a tile
+constexpr int kParamSets = 4;      // tiles whose parameters may be in LDS at once
+constexpr int kLdsBytes = kStages * kStageBytes + kParamSets * 3 * kParamBytes;
+
+template <bool FP8, int ACT, int OUT_DT, bool ACC_OUT, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) {
+  typedef Mfma<FP8> T;
+  constexpr int kWaves = WM * WN;
+  constexpr int FM = BM / WM / 32;               // activation (token) fragments per wave
+  constexpr int FN = BN / WN / 32;               // weight (feature) fragments per wave
+  constexpr int kRowsPerWave = 256 / kWaves;     // DMA rows per operand per wave
+  constexpr int kWaveLoads = kRowsPerWave / 16;  // 1 KB DMA loads per operand per wave
+  constexpr int kLoadsPerStage = 2 * kWaveLoads; // per thread
+  static_assert(kRowsPerWave % 16 == 0, "DMA rows");
+  static_assert(FN * 32 * 2 == 128 && kWaves * 32 * 128 <= kStageBytes, "epilogue transpose layout");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kLdsBytes];
+
+  // --- this workgroup's tiles ------------------------------------------------
+  const int ntiles = p.tiles_m * p.tiles_n;
+  const int xcd = blockIdx.x & 7, local = blockIdx.x >> 3, wgs_per_xcd = gridDim.x >> 3;
+  const int t_first = xcd * p.per_xcd + local;
+  const int t_end = min((xcd + 1) * p.per_xcd, ntiles);
+  const int n_my = t_first < t_end ? (t_end - t_first + wgs_per_xcd - 1) / wgs_per_xcd : 0;
+  const int KT = (p.K + BK - 1) / BK;
+  const int G = n_my * KT;  // stages of all my tiles
+  if (G == 0) return;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wm = wave % WM, wn = wave / WM;
 
   const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t *>(p.a), (short)0, (int)p.a_bytes, kBufferFlags);
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t *>(p.w), (short)0, (int)p.w_bytes, kBufferFlags);
+  const int bias_elem = p.bias_dtype == XGEN_DTYPE_F32 ? 4 : 2;
+  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(p.sa), (short)0, p.M * 4, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(p.sw), (short)0, p.N * 4, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void *>(p.bias), (short)0, p.bias ? p.N * bias_elem : 0, kBufferFlags);
+  // per-tensor scales (stride 0): one uniform value each
+  const float sa0 = p.sa_stride ? 0.0f : p.sa[0];
+  const float sw0 = p.sw_stride ? 0.0f : p.sw[0];
 
-  // --- global -> LDS assignment: 8 rows x one 16-byte chunk per operand ---
-  const int lc = tid & 7, lr = tid >> 3;
-  uint32_t offa[8], offw[8];
+  // --- global -> LDS DMA ------------------------------------------------------
+  // A 16-byte DMA load writes LDS at (wave base + lane * 16), so one wave-load
+  // fills 1 KB = 16 rows x 64 bytes.  Wave w fills rows
+  // [w * kRowsPerWave, (w + 1) * kRowsPerWave) of both operand tiles; lane l
+  // lands on row base + (l >> 2), physical chunk l & 3, i.e. logical chunk
+  // (l & 3) ^ ((row >> 2) & 3) = (l & 3) ^ ((l >> 4) & 3), fetched from global.
+  const int dma_chunk = (lane & 3) ^ ((lane >> 4) & 3);
+  uint32_t offa[kWaveLoads], offw[kWaveLoads];
+  int dma_m0 = 0, dma_n0 = 0;
+  auto set_dma_tile = [&](int i) {  // row offsets of my i-th tile
+    tile_origin(t_first + i * wgs_per_xcd, p.tiles_m, p.tiles_n, dma_m0, dma_n0);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int ma = m0 + lr + 32 * i, nw = n0 + lr + 32 * i;
-    offa[i] = ma < p.M ? (uint32_t)ma * (uint32_t)p.lda + lc * 16 : kOutOfRange;
-    offw[i] = nw < p.N ? (uint32_t)nw * (uint32_t)p.ldw + lc * 16 : kOutOfRange;
-  }
-  const int lds_w = lr * BK + ((lc ^ (lr & 7)) << 4);  // + i * 32 * BK
-
-  u32x4 ga[8], gw[8];
-  auto load_global = [&](int k0) {
-    const bool kin = k0 + lc * 16 < p.K;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      ga[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, kin ? offa[i] + k0 : kOutOfRange, 0, 0);
-      gw[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, kin ? offw[i] + k0 : kOutOfRange, 0, 0);
+    for (int l = 0; l < kWaveLoads; ++l) {
+      const int r = wave * kRowsPerWave + l * 16 + (lane >> 2);
+      const int ma = dma_m0 + r, nw = dma_n0 + r;
+      offa[l] = ma < p.M ? (uint32_t)ma * (uint32_t)p.lda + dma_chunk * 16 : kOutOfRange;
+      offw[l] = nw < p.N ? (uint32_t)nw * (uint32_t)p.ldw + dma_chunk * 16 : kOutOfRange;
     }
   };
-  auto store_lds = [&](int stage) {
-    uint8_t *sa = smem + stage * 2 * kTileBytes;
-    uint8_t *sb = sa + kTileBytes;
+  int issue_g = 0, issue_kt = 0, issue_i = 0;  // next stage to load
+  auto issue_next = [&]() {
+    if (issue_g >= G) return;
+    const int k0 = issue_kt * BK;
+    const bool kin = k0 + dma_chunk * 16 < p.K;  // K tail: out of range -> zeros
+    uint8_t *base = smem + (issue_g % kStages) * kStageBytes + wave * kRowsPerWave * BK;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      *reinterpret_cast<u32x4 *>(sa + lds_w + i * 32 * BK) = ga[i];
-      *reinterpret_cast<u32x4 *>(sb + lds_w + i * 32 * BK) = gw[i];
+    for (int l = 0; l < kWaveLoads; ++l) {
+      dma_load16(ra, base + l * 16 * BK, kin ? offa[l] + k0 : kOutOfRange);
+      dma_load16(rw, base + kTileBytes + l * 16 * BK, kin ? offw[l] + k0 : kOutOfRange);
+    }
+    if (issue_kt == 0) {  // the tile's epilogue parameters ride with its first stage
+      uint8_t *prm = smem + kStages * kStageBytes + (issue_i % kParamSets) * 3 * kParamBytes;
+      if (wave == 0 && p.sa_stride) dma_load16(rsa, prm, (uint32_t)dma_m0 * 4 + lane * 16);
+      if (wave == 1 && p.sw_stride) dma_load16(rsw, prm + kParamBytes, (uint32_t)dma_n0 * 4 + lane * 16);
+      if (wave == 2 && p.bias) dma_load16(rb, prm + 2 * kParamBytes, (uint32_t)(dma_n0 * bias_elem) + lane * 16);
+    }
+    ++issue_g;
+    if (++issue_kt == KT) {
+      issue_kt = 0;
+      if (++issue_i < n_my) set_dma_tile(issue_i);
     }
   };
 
-  typename T::acc_t acc[4][4];
+  typename T::acc_t acc[FN][FM];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < FN; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = typename T::acc_t{};
+    for (int j = 0; j < FM; ++j) acc[i][j] = typename T::acc_t{};
 
-  const int row_x = wm * 128 + (lane & 31);
-  const int row_w = wn * 128 + (lane & 31);
-  const int KT = (p.K + BK - 1) / BK;
+  const int row_x = wm * (BM / WM) + (lane & 31);
+  const int row_w = wn * (BN / WN) + (lane & 31);
 
-  load_global(0);
-  store_lds(0);
-  __syncthreads();
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < KT) load_global((kt + 1) * BK);
-    const uint8_t *sx = smem + cur * 2 * kTileBytes;
+  set_dma_tile(0);
+#pragma unroll
+  for (int s = 0; s < kStages - 1; ++s) issue_next();
+
+  int tile_i = 0, kt = 0;
+  for (int g = 0; g < G; ++g) {
+    // this thread's loads of stage g (and, for a tile's first stage, its
+    // parameter row) are done once at most the loads of the stages issued
+    // after it remain outstanding
+    const int later = min(kStages - 2, G - 1 - g);
+    if (later >= 2) wait_vmcnt<2 * kLoadsPerStage>();
+    else if (later == 1) wait_vmcnt<kLoadsPerStage>();
+    else wait_vmcnt<0>();
+    // Every wave's share of stage g has landed and slot (g-1) % kStages is
+    // free.  A bare s_barrier: __syncthreads' fence would also wait for the
+    // loads still in flight for later stages.
+    __builtin_amdgcn_s_barrier();
+    issue_next();
+    uint8_t *sx = smem + (g % kStages) * kStageBytes;
     const uint8_t *sw = sx + kTileBytes;
 #pragma unroll
     for (int ks = 0; ks < T::kSteps; ++ks) {
-      typename T::frag_t fw[4], fx[4];
+      typename T::frag_t fw[FN], fx[FM];
 #pragma unroll
-      for (int f = 0; f < 4; ++f) {
-        fw[f] = T::load(sw, row_w + f * 32, ks, lane);
-        fx[f] = T::load(sx, row_x + f * 32, ks, lane);
-      }
+      for (int f = 0; f < FN; ++f) fw[f] = T::load(sw, row_w + f * 32, ks, lane);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int f = 0; f < FM; ++f) fx[f] = T::load(sx, row_x + f * 32, ks, lane);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = T::mma(fw[i], fx[j], acc[i][j]);
+      for (int j = 0; j < FM; ++j)
+#pragma unroll
+        for (int i = 0; i < FN; ++i) acc[i][j] = T::mma(fw[i], fx[j], acc[i][j]);
     }
-    if (kt + 1 < KT) store_lds(cur ^ 1);
-    __syncthreads();
-  }
+    if (++kt < KT) continue;
 
-  // --- epilogue -------------------------------------------------------------
-  // acc[i][j] element e: feature n = n0 + wn*128 + i*32 + (e/4)*8 + (lane/32)*4 + e%4,
-  //                      token   m = m0 + wm*128 + j*32 + lane%32.
+    // --- epilogue of my tile tile_i -------------------------------------------
+    // acc[i][j] element e: feature n = n0 + wn*(BN/WN) + i*32 + (e/4)*8 + (lane/32)*4 + e%4,
+    //                      token   m = m0 + wm*(BM/WM) + j*32 + lane%32.
+    int m0, n0;
+    tile_origin(t_first + tile_i * wgs_per_xcd, p.tiles_m, p.tiles_n, m0, n0);
+    const uint8_t *prm = smem + kStages * kStageBytes + (tile_i % kParamSets) * 3 * kParamBytes;
+    const float *psa = reinterpret_cast<const float *>(prm);
+    const float *psw = reinterpret_cast<const float *>(prm + kParamBytes);
+    const uint8_t *pb = prm + 2 * kParamBytes;
+    float swv[FN][4][4], bv[FN][4][4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int m = m0 + wm * 128 + j * 32 + (lane & 31);
-    if (m >= p.M) continue;
-    const float sam = p.sa[(int64_t)m * p.sa_stride];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < FN; ++i)
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq) {
-        const int n = n0 + wn * 128 + i * 32 + gq * 8 + (lane >> 5) * 4;
-        if (n >= p.N) continue;
-        float swv[4], bv[4] = {0.f, 0.f, 0.f, 0.f}, y[4];
+        const int nl = wn * (BN / WN) + i * 32 + gq * 8 + (lane >> 5) * 4;
         if (p.sw_stride) {
-          const f32x4 s4 = *reinterpret_cast<const f32x4 *>(p.sw + n);
-          swv[0] = s4.x; swv[1] = s4.y; swv[2] = s4.z; swv[3] = s4.w;
+          const f32x4 s4 = *reinterpret_cast<const f32x4 *>(psw + nl);
+          swv[i][gq][0] = s4.x; swv[i][gq][1] = s4.y; swv[i][gq][2] = s4.z; swv[i][gq][3] = s4.w;
         } else {
-          swv[0] = swv[1] = swv[2] = swv[3] = p.sw[0];
+          swv[i][gq][0] = swv[i][gq][1] = swv[i][gq][2] = swv[i][gq][3] = sw0;
         }
-        if (p.bias) load_bias4(p.bias, p.bias_dtype, n, bv);
+        if (p.bias) load_bias4(pb, p.bias_dtype, nl, bv[i][gq]);
+        else bv[i][gq][0] = bv[i][gq][1] = bv[i][gq][2] = bv[i][gq][3] = 0.0f;
+      }
+    // this wave's 4 KB transpose area in the slot of stage g; every wave must
+    // be done reading that slot's fragments first
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    uint8_t *xb = sx + wave * 32 * 128;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float a = T::to_f32(acc[i][j][gq * 4 + e]);
-          y[e] = __builtin_fmaf(a, sam * swv[e], bv[e]);
-          if constexpr (ACT == XGEN_ACT_GELU_TANH) y[e] = gelu_tanh(round_out<OUT_DT>(y[e]));
-        }
-        const u32x2 o = {pack_out<OUT_DT>(y[0], y[1]), pack_out<OUT_DT>(y[2], y[3])};
-        *reinterpret_cast<u32x2 *>(static_cast<uint16_t *>(p.out) + (int64_t)m * p.ldo + n) = o;
-        if constexpr (ACC_OUT) {
-          if constexpr (FP8) {
-            const f32x4 v = {acc[i][j][gq * 4 + 0], acc[i][j][gq * 4 + 1], acc[i][j][gq * 4 + 2],
-                             acc[i][j][gq * 4 + 3]};
-            *reinterpret_cast<f32x4 *>(static_cast<float *>(p.acc_out) + (int64_t)m * p.N + n) = v;
-          } else {
-            const i32x4 v = {acc[i][j][gq * 4 + 0], acc[i][j][gq * 4 + 1], acc[i][j][gq * 4 + 2],
-                             acc[i][j][gq * 4 + 3]};
-            *reinterpret_cast<i32x4 *>(static_cast<int32_t *>(p.acc_out) + (int64_t)m * p.N + n) = v;
+    for (int j = 0; j < FM; ++j) {
+      const int ml = wm * (BM / WM) + j * 32 + (lane & 31);
+      const float sam = p.sa_stride ? psa[ml] : sa0;
+      const int wrow = lane & 31;
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          float y[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float a = T::to_f32(acc[i][j][gq * 4 + e]);
+            y[e] = __builtin_fmaf(a, sam * swv[i][gq][e], bv[i][gq][e]);
+            if constexpr (ACT == XGEN_ACT_GELU_TANH) y[e] = gelu_tanh(round_out<OUT_DT>(y[e]));
+          }
+          // row wrow, 8-byte chunk c8 (4 outputs) of the wave's 128-byte row,
+          // XOR-swizzled by (row >> 1) & 15: conflict-free 64-bit writes
+          const int c8 = i * 8 + gq * 2 + (lane >> 5);
+          *reinterpret_cast<u32x2 *>(xb + wrow * 128 + ((c8 ^ ((wrow >> 1) & 15)) << 3)) =
+              u32x2{pack_out<OUT_DT>(y[0], y[1]), pack_out<OUT_DT>(y[2], y[3])};
+          if constexpr (ACC_OUT) {
+            const int m = m0 + ml;
+            const int n = n0 + wn * (BN / WN) + i * 32 + gq * 8 + (lane >> 5) * 4;
+            if (m < p.M && n < p.N) {
+              if constexpr (FP8) {
+                const f32x4 v = {acc[i][j][gq * 4 + 0], acc[i][j][gq * 4 + 1], acc[i][j][gq * 4 + 2],
+                                 acc[i][j][gq * 4 + 3]};
+                *reinterpret_cast<f32x4 *>(static_cast<float *>(p.acc_out) + (int64_t)m * p.N + n) = v;
+              } else {
+                const i32x4 v = {acc[i][j][gq * 4 + 0], acc[i][j][gq * 4 + 1], acc[i][j][gq * 4 + 2],
+                                 acc[i][j][gq * 4 + 3]};
+                *reinterpret_cast<i32x4 *>(static_cast<int32_t *>(p.acc_out) + (int64_t)m * p.N + n) = v;
+              }
+            }
           }
         }
+      // read back 8 rows x 128 bytes per instruction: 16 bytes per lane, stored
+      // as full row segments (LDS operations of a wave complete in order)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int row = q * 8 + (lane >> 3), c16 = lane & 7, sw4 = (row >> 1) & 15;
+        u32x4 v = *reinterpret_cast<const u32x4 *>(xb + row * 128 + ((c16 ^ (sw4 >> 1)) << 4));
+        if (sw4 & 1) v = u32x4{v.z, v.w, v.x, v.y};
+        const int m = m0 + wm * (BM / WM) + j * 32 + row;
+        const int n = n0 + wn * (BN / WN) + c16 * 8;
+        if (m < p.M && n < p.N)
+          *reinterpret_cast<u32x4 *>(static_cast<uint16_t *>(p.out) + (int64_t)m * p.ldo + n) = v;
       }
     }
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j) acc[i][j] = typename T::acc_t{};
+    kt = 0;
+    ++tile_i;
   }
+}
+
+int cu_count() {
+  static int cus = 0;  // per process; all devices of this build are MI355X (256 CUs)
+  if (cus == 0) {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+      cus = v;
+    else
+      cus = 256;
+  }
+  return cus;
 }
 
 template <bool FP8, int ACT, int OUT_DT>
 void launch_gemm(const GemmArgs &a, bool acc_out, hipStream_t stream) {
-  const int tiles = a.tiles_m * a.tiles_n;
-  const dim3 grid((unsigned)(a.per_xcd * 8)), block(kThreads);
-  (void)tiles;
-  if (acc_out) gemm_w8a8_kernel<FP8, ACT, OUT_DT, true><<<grid, block, 0, stream>>>(a);
-  else gemm_w8a8_kernel<FP8, ACT, OUT_DT, false><<<grid, block, 0, stream>>>(a);
+  // one persistent workgroup per CU (a multiple of the 8 XCDs), never more than the tiles need
+  const int ntiles = a.tiles_m * a.tiles_n;
+  int wgs = cu_count() / 8 * 8;
+  const int need = ((ntiles + 7) / 8) * 8;
+  if (wgs > need) wgs = need;
+  if (wgs < 8) wgs = 8;
+  const dim3 grid((unsigned)wgs), block(64 * kWavesM * kWavesN);
+  if (acc_out) gemm_w8a8_kernel<FP8, ACT, OUT_DT, true, kWavesM, kWavesN><<<grid, block, 0, stream>>>(a);
+  else gemm_w8a8_kernel<FP8, ACT, OUT_DT, false, kWavesM, kWavesN><<<grid, block, 0, stream>>>(a);
 }
 
 template <bool FP8>
@@ -300,11 +455,11 @@ int gemm_entry(const char *fn, const void *a, int64_t lda, const void *w, int64_
   if (K % 16 || N % 16) return fail(XGEN_ERR_UNSUPPORTED, "%s: K and N must be multiples of 16", fn);
   if (lda % 16 || ldw % 16 || !aligned16(a) || !aligned16(w))
     return fail(XGEN_ERR_UNSUPPORTED, "%s: operand rows must be 16-byte aligned", fn);
-  if (ldo % 4 || (reinterpret_cast<uintptr_t>(out) & 7u))
-    return fail(XGEN_ERR_UNSUPPORTED, "%s: output rows must be 8-byte aligned", fn);
-  if ((bias && (reinterpret_cast<uintptr_t>(bias) & 15u)) || (sw_stride && !aligned16(sw)) ||
+  if (ldo % 8 || !aligned16(out))
+    return fail(XGEN_ERR_UNSUPPORTED, "%s: output rows must be 16-byte aligned", fn);
+  if ((bias && !aligned16(bias)) || (sw_stride && !aligned16(sw)) || (sa_stride && !aligned16(sa)) ||
       (acc_out && !aligned16(acc_out)))
-    return fail(XGEN_ERR_UNSUPPORTED, "%s: bias, weight scale and accumulator buffers must be 16-byte aligned", fn);
+    return fail(XGEN_ERR_UNSUPPORTED, "%s: scale, bias and accumulator buffers must be 16-byte aligned", fn);
   const int64_t a_bytes = (M - 1) * lda + K, w_bytes = (N - 1) * ldw + K;
   if (a_bytes >= (int64_t)kOutOfRange || w_bytes >= (int64_t)kOutOfRange)
     return fail(XGEN_ERR_UNSUPPORTED, "%s: operands above 2 GiB", fn);
