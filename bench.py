@@ -95,12 +95,27 @@ def profile_kernels(names, steps, warmup):
     print(json.dumps({"profile_kernels": out}), flush=True)
 
 
-def timed(fn, iters, warmup):
-    """Average milliseconds per call of fn() over iters calls (HIP events on the current stream)."""
+MIN_WARM_S = 0.3  # the GPU's clocks take ~25 ms of sustained load to settle
+
+
+def warm(fn, warmup, min_s=MIN_WARM_S):
+    """At least `warmup` calls and at least min_s seconds of back-to-back calls,
+    so the timed region sees the steady-state clock, not the ramp out of idle."""
     import torch
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < min_s:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+
+
+def timed(fn, iters, warmup):
+    """Average milliseconds per call of fn() over iters calls (HIP events on the current stream)."""
+    import torch
+    warm(fn, warmup)
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(iters):
@@ -173,9 +188,7 @@ def main():
         return out
 
     # ---- whole step (quant + GEMM), the headline value
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    warm(step, args.warmup)
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(args.steps):

@@ -112,6 +112,24 @@ def test_gelu_epilogue(cuda, kind):
     assert (out.cpu()[~body].float() - g_ref[~body].float()).abs().max() <= 1e-3
 
 
+@pytest.mark.parametrize("K", [64, 128, 192])
+def test_many_tiles_per_workgroup_short_k(cuda, K):
+    """32 x 40 output tiles (at least 5 per persistent workgroup) with 1-3 K
+    stages per tile: each tile's scales and bias must reach its own epilogue
+    while the loads of the following tiles are already in flight.  The first
+    and last row of every 256-row block, all columns (every tile) checked."""
+    M, Nf = 8192, 10240
+    qa, sa, qw, sw, bias = quantized_operands(M, K, Nf, cuda, "fp8", seed=K)
+    out, _ = xops.scaled_mm(qa, qw, sa, sw, bias, torch.bfloat16, N.ACT_NONE, False)
+    rows = torch.tensor([r for b in range(0, M, 256) for r in (b, b + 255)])
+    rc = rows.to(cuda)
+    ref = R.w8a8_linear_fp8(qa[rc].cpu(), sa[rc].cpu(), qw.cpu(), sw.cpu(), bias.cpu())
+    check_close(out[rc], ref)
+    exact = R.fp8_accumulate_exact(qa[rc].cpu(), qw.cpu())
+    acc_bound = FP8_ACC_REL * (R.decode_fp8(qa[rc].cpu()).abs() @ R.decode_fp8(qw.cpu()).abs().T)
+    assert_within_rounding(out[rc], ref, exact.abs(), sa[rc], sw, bias, acc_bound)
+
+
 @pytest.mark.parametrize("kind", ["fp8", "int8"])
 def test_full_size_qkv_sampled_rows(cuda, kind):
     """C2 / C4 QKV at M=15,624: the whole GEMM on the GPU, 96 seeded rows checked."""

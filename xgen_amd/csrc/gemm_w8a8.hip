@@ -40,6 +40,8 @@ constexpr int kStageBytes = 2 * kTileBytes;   // activations + weights: 32 KB
 constexpr int kGroupM = 8;
 constexpr int kBufferFlags = 0x00020000;  // raw buffer, 32-bit dword format (gfx9)
 constexpr uint32_t kOutOfRange = 0x80000000u;
+// instruction classes of __builtin_amdgcn_sched_group_barrier
+constexpr int kMfma = 0x008, kVmemRead = 0x020, kDsRead = 0x100;
 
 // Waves per workgroup (along M and N) of the production configuration.
 constexpr int kWavesM = 2, kWavesN = 4;
@@ -79,6 +81,7 @@ struct Mfma<true> {
   typedef f32x16 acc_t;
   typedef i32x8 frag_t;
   static constexpr int kSteps = BK / 64;  // 32x32x64: one step per stage
+  static constexpr int kReads = 2;        // ds_read_b128 per fragment
   static __device__ __forceinline__ frag_t load(const uint8_t *tile, int row, int ks, int lane) {
     const int c0 = ks * 4 + (lane >> 5) * 2;
     const u32x4 lo = *reinterpret_cast<const u32x4 *>(tile + swz(row, c0));
@@ -97,6 +100,7 @@ struct Mfma<false> {
   typedef i32x16 acc_t;
   typedef i32x4 frag_t;
   static constexpr int kSteps = BK / 32;  // 32x32x32: two steps per stage
+  static constexpr int kReads = 1;        // ds_read_b128 per fragment
   static __device__ __forceinline__ frag_t load(const uint8_t *tile, int row, int ks, int lane) {
     const int c = ks * 2 + (lane >> 5);
     const u32x4 v = *reinterpret_cast<const u32x4 *>(tile + swz(row, c));
@@ -115,6 +119,17 @@ struct Mfma<false> {
 __device__ __forceinline__ void dma_load16(__amdgpu_buffer_rsrc_t rsrc, uint8_t *lds, uint32_t offset) {
   typedef __attribute__((address_space(3))) void *lds_ptr_t;
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr_t)lds, 16, offset, 0, 0, 0);
+}
+
+// Workgroup barrier that orders LDS accesses without waiting for the vector
+// memory counter: __syncthreads' fence would also wait for the DMA loads still
+// in flight for later stages.  The empty asm statements keep the compiler from
+// moving memory accesses across it; the caller waits lgkmcnt for its own LDS
+// accesses first.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 // s_waitcnt constraining only the vector-memory counter (gfx9 encoding: vmcnt
@@ -147,20 +162,11 @@ __device__ __forceinline__ uint32_t pack_out(float a, float b) {
   else return pack_f16x2(a, b);
 }
 
-__device__ __forceinline__ void load_bias4(const void *bias, int dtype, int n, float (&b)[4]) {
-  if (dtype == XGEN_DTYPE_F32) {
-    const f32x4 v = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(bias) + n);
-    b[0] = v.x; b[1] = v.y; b[2] = v.z; b[3] = v.w;
-  } else {
-    const u32x2 v = *reinterpret_cast<const u32x2 *>(static_cast<const uint16_t *>(bias) + n);
-    if (dtype == XGEN_DTYPE_BF16) {
-      b[0] = Half2<XGEN_DTYPE_BF16>::lo(v.x); b[1] = Half2<XGEN_DTYPE_BF16>::hi(v.x);
-      b[2] = Half2<XGEN_DTYPE_BF16>::lo(v.y); b[3] = Half2<XGEN_DTYPE_BF16>::hi(v.y);
-    } else {
-      b[0] = Half2<XGEN_DTYPE_F16>::lo(v.x); b[1] = Half2<XGEN_DTYPE_F16>::hi(v.x);
-      b[2] = Half2<XGEN_DTYPE_F16>::lo(v.y); b[3] = Half2<XGEN_DTYPE_F16>::hi(v.y);
-    }
-  }
+// Bias element n of a bf16 / f16 / f32 row, as float.
+__device__ __forceinline__ float bias_at(const uint8_t *bias, int dtype, int n) {
+  if (dtype == XGEN_DTYPE_F32) return reinterpret_cast<const float *>(bias)[n];
+  const uint16_t h = reinterpret_cast<const uint16_t *>(bias)[n];
+  return dtype == XGEN_DTYPE_BF16 ? Half2<XGEN_DTYPE_BF16>::lo(h) : Half2<XGEN_DTYPE_F16>::lo(h);
 }
 
 // Output tile -> (m0, n0): tiles are walked in groups of kGroupM tile-rows.
@@ -188,9 +194,15 @@ __device__ __forceinline__ void tile_origin(int pid, int tiles_m, int tiles_n, i
 // indexed by tile), and are read with LDS loads.  Outputs are transposed
 // through the ring slot just consumed (free until the next barrier) so every
 // store writes full 128-byte row segments.
+// One parameter set: [sa f32 x 256][sw f32 x 256][bias as loaded, <= 1 KB][bias f32 x 256].
 constexpr int kParamBytes = 1024;  // 256 x 4 bytes: one parameter row of a tile
-constexpr int kParamSets = 4;      // tiles whose parameters may be in LDS at once
-constexpr int kLdsBytes = kStages * kStageBytes + kParamSets * 3 * kParamBytes;
+constexpr int kParamSetBytes = 4 * kParamBytes;
+// A tile's parameters are loaded with its first stage, issued kStages stages
+// ahead, and read in its epilogue; the set is reloaded kParamSets tiles later.
+// With KT stages per tile that reload is issued after the epilogue when
+// (kParamSets - 1) * KT >= kStages, for every KT >= 1.
+constexpr int kParamSets = kStages + 1;
+constexpr int kLdsBytes = kStages * kStageBytes + kParamSets * kParamSetBytes;
 
 template <bool FP8, int ACT, int OUT_DT, bool ACC_OUT, int WM, int WN>
 __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) {
@@ -252,28 +264,64 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) 
       offw[l] = nw < p.N ? (uint32_t)nw * (uint32_t)p.ldw + dma_chunk * 16 : kOutOfRange;
     }
   };
-  int issue_g = 0, issue_kt = 0, issue_i = 0;  // next stage to load
-  auto issue_next = [&]() {
-    if (issue_g >= G) return;
+  // The load stream: the next stage to load is issue_g (slot issue_g %
+  // kStages), stage issue_kt of my tile issue_i.  Past my last stage the
+  // stream goes on with stages whose loads are all out of range: they write
+  // zeros into slots nothing reads, which keeps the stream free of branches.
+  int issue_g = 0, issue_kt = 0, issue_i = 0;
+  auto issue_params = [&]() {  // a tile's epilogue parameters ride with its first stage
+    if (issue_kt != 0 || issue_g >= G) return;
+    uint8_t *prm = smem + kStages * kStageBytes + (issue_i % kParamSets) * kParamSetBytes;
+    if (wave == 0 && p.sa_stride) dma_load16(rsa, prm, (uint32_t)dma_m0 * 4 + lane * 16);
+    if (wave == 1 && p.sw_stride) dma_load16(rsw, prm + kParamBytes, (uint32_t)dma_n0 * 4 + lane * 16);
+    if (wave == 2 && p.bias) dma_load16(rb, prm + 2 * kParamBytes, (uint32_t)(dma_n0 * bias_elem) + lane * 16);
+  };
+  // operand load q (0 .. kLoadsPerStage-1) of stage issue_g
+  struct Issue {
+    uint8_t *base;
+    int k0;
+    bool kin;
+  };
+  auto issue_setup = [&]() {
     const int k0 = issue_kt * BK;
-    const bool kin = k0 + dma_chunk * 16 < p.K;  // K tail: out of range -> zeros
-    uint8_t *base = smem + (issue_g % kStages) * kStageBytes + wave * kRowsPerWave * BK;
-#pragma unroll
-    for (int l = 0; l < kWaveLoads; ++l) {
-      dma_load16(ra, base + l * 16 * BK, kin ? offa[l] + k0 : kOutOfRange);
-      dma_load16(rw, base + kTileBytes + l * 16 * BK, kin ? offw[l] + k0 : kOutOfRange);
-    }
-    if (issue_kt == 0) {  // the tile's epilogue parameters ride with its first stage
-      uint8_t *prm = smem + kStages * kStageBytes + (issue_i % kParamSets) * 3 * kParamBytes;
-      if (wave == 0 && p.sa_stride) dma_load16(rsa, prm, (uint32_t)dma_m0 * 4 + lane * 16);
-      if (wave == 1 && p.sw_stride) dma_load16(rsw, prm + kParamBytes, (uint32_t)dma_n0 * 4 + lane * 16);
-      if (wave == 2 && p.bias) dma_load16(rb, prm + 2 * kParamBytes, (uint32_t)(dma_n0 * bias_elem) + lane * 16);
-    }
+    // K tail and the stages past my last: out of range -> zeros
+    return Issue{smem + (issue_g % kStages) * kStageBytes + wave * kRowsPerWave * BK, k0,
+                 issue_g < G && k0 + dma_chunk * 16 < p.K};
+  };
+  auto issue_load = [&](const Issue &is, int q) {
+    const int l = q >> 1;
+    if (q & 1)
+      dma_load16(rw, is.base + kTileBytes + l * 16 * BK, is.kin ? offw[l] + is.k0 : kOutOfRange);
+    else
+      dma_load16(ra, is.base + l * 16 * BK, is.kin ? offa[l] + is.k0 : kOutOfRange);
+  };
+  auto issue_advance = [&]() {
     ++issue_g;
     if (++issue_kt == KT) {
       issue_kt = 0;
       if (++issue_i < n_my) set_dma_tile(issue_i);
     }
+  };
+  auto issue_next = [&]() {  // a whole stage at once (prologue)
+    issue_params();
+    const Issue is = issue_setup();
+#pragma unroll
+    for (int q = 0; q < kLoadsPerStage; ++q) issue_load(is, q);
+    issue_advance();
+  };
+
+  typedef typename T::frag_t frag_t;
+  const int row_x = wm * (BM / WM) + (lane & 31);
+  const int row_w = wn * (BN / WN) + (lane & 31);
+  auto slot_of = [&](int stage) { return smem + (stage % kStages) * kStageBytes; };
+  // this thread's loads of stage h (and of the parameter row issued with it)
+  // are done once at most the loads of the stages issued after it remain
+  // outstanding (the parameter loads only make the count conservative)
+  auto wait_stage = [&](int h) {
+    const int later = issue_g - 1 - h;
+    if (later >= 2) wait_vmcnt<2 * kLoadsPerStage>();
+    else if (later == 1) wait_vmcnt<kLoadsPerStage>();
+    else wait_vmcnt<0>();
   };
 
   typename T::acc_t acc[FN][FM];
@@ -282,86 +330,102 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) 
 #pragma unroll
     for (int j = 0; j < FM; ++j) acc[i][j] = typename T::acc_t{};
 
-  const int row_x = wm * (BM / WM) + (lane & 31);
-  const int row_w = wn * (BN / WN) + (lane & 31);
-
-  set_dma_tile(0);
-#pragma unroll
-  for (int s = 0; s < kStages - 1; ++s) issue_next();
-
   int tile_i = 0, kt = 0;
-  for (int g = 0; g < G; ++g) {
-    // this thread's loads of stage g (and, for a tile's first stage, its
-    // parameter row) are done once at most the loads of the stages issued
-    // after it remain outstanding
-    const int later = min(kStages - 2, G - 1 - g);
-    if (later >= 2) wait_vmcnt<2 * kLoadsPerStage>();
-    else if (later == 1) wait_vmcnt<kLoadsPerStage>();
-    else wait_vmcnt<0>();
-    // Every wave's share of stage g has landed and slot (g-1) % kStages is
-    // free.  A bare s_barrier: __syncthreads' fence would also wait for the
-    // loads still in flight for later stages.
-    __builtin_amdgcn_s_barrier();
-    issue_next();
-    uint8_t *sx = smem + (g % kStages) * kStageBytes;
-    const uint8_t *sw = sx + kTileBytes;
+  // Operand fragments in registers: xf = activation fragments of the stage
+  // being multiplied; wf[c] = weight fragments of it, wf[c ^ 1] = those of the
+  // next stage.  Each activation fragment is refilled with the next stage's
+  // as soon as its last MFMA has been issued, so the LDS reads of stage g+1
+  // overlap the MFMAs of stage g within 64 fragment registers.
+  frag_t xf[T::kSteps][FM], wf[2][T::kSteps][FN];
+
+  // One stage.  The barrier at the top publishes every wave's DMA of stage
+  // g+1 and retires every wave's reads of slot g % kStages, which then takes
+  // the DMA of stage g + kStages.  (Past the last stage the reads of "stage
+  // g+1" fetch stale LDS that nothing uses.)
+  auto stage = [&](int g, int c) {
+    wait_stage(g + 1);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): my reads of slot g are done
+    lds_barrier();
+    issue_params();
+    const Issue is = issue_setup();
+    const uint8_t *nx = slot_of(g + 1), *nw = nx + kTileBytes;
 #pragma unroll
-    for (int ks = 0; ks < T::kSteps; ++ks) {
-      typename T::frag_t fw[FN], fx[FM];
+    for (int ks = 0; ks < T::kSteps; ++ks)
 #pragma unroll
-      for (int f = 0; f < FN; ++f) fw[f] = T::load(sw, row_w + f * 32, ks, lane);
+      for (int f = 0; f < FN; ++f) wf[c ^ 1][ks][f] = T::load(nw, row_w + f * 32, ks, lane);
+    // The operand loads of stage g + kStages are spread over the MFMAs: issued
+    // together, the workgroup's loads queue up in the address unit, and a wave
+    // whose load waits there cannot issue its MFMAs either.
+    constexpr int kSlots = T::kSteps * FM, kEvery = kSlots / kLoadsPerStage;
+    static_assert(kSlots % kLoadsPerStage == 0, "load spacing");
 #pragma unroll
-      for (int f = 0; f < FM; ++f) fx[f] = T::load(sx, row_x + f * 32, ks, lane);
+    for (int ks = 0; ks < T::kSteps; ++ks)
 #pragma unroll
-      for (int j = 0; j < FM; ++j)
+      for (int j = 0; j < FM; ++j) {
 #pragma unroll
-        for (int i = 0; i < FN; ++i) acc[i][j] = T::mma(fw[i], fx[j], acc[i][j]);
+        for (int i = 0; i < FN; ++i) acc[i][j] = T::mma(wf[c][ks][i], xf[ks][j], acc[i][j]);
+        xf[ks][j] = T::load(nx, row_x + j * 32, ks, lane);
+        const int slot = ks * FM + j;
+        if (slot % kEvery == 0) issue_load(is, slot / kEvery);
+      }
+    // Keep that order in the schedule: the weight reads, then per activation
+    // fragment its MFMAs, its refill and (every kEvery fragments) one load.
+    // (Left alone the scheduler issues most MFMAs first and the reads of the
+    // next stage too late.)
+    __builtin_amdgcn_sched_group_barrier(kDsRead, T::kReads * T::kSteps * FN, 0);
+#pragma unroll
+    for (int k = 0; k < kSlots; ++k) {
+      __builtin_amdgcn_sched_group_barrier(kMfma, FN, 0);
+      __builtin_amdgcn_sched_group_barrier(kDsRead, T::kReads, 0);
+      if (k % kEvery == 0) __builtin_amdgcn_sched_group_barrier(kVmemRead, 1, 0);
     }
-    if (++kt < KT) continue;
+    issue_advance();
+    if (++kt < KT) return;
 
     // --- epilogue of my tile tile_i -------------------------------------------
     // acc[i][j] element e: feature n = n0 + wn*(BN/WN) + i*32 + (e/4)*8 + (lane/32)*4 + e%4,
     //                      token   m = m0 + wm*(BM/WM) + j*32 + lane%32.
     int m0, n0;
     tile_origin(t_first + tile_i * wgs_per_xcd, p.tiles_m, p.tiles_n, m0, n0);
-    const uint8_t *prm = smem + kStages * kStageBytes + (tile_i % kParamSets) * 3 * kParamBytes;
-    const float *psa = reinterpret_cast<const float *>(prm);
-    const float *psw = reinterpret_cast<const float *>(prm + kParamBytes);
-    const uint8_t *pb = prm + 2 * kParamBytes;
-    float swv[FN][4][4], bv[FN][4][4];
-#pragma unroll
-    for (int i = 0; i < FN; ++i)
-#pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-        const int nl = wn * (BN / WN) + i * 32 + gq * 8 + (lane >> 5) * 4;
-        if (p.sw_stride) {
-          const f32x4 s4 = *reinterpret_cast<const f32x4 *>(psw + nl);
-          swv[i][gq][0] = s4.x; swv[i][gq][1] = s4.y; swv[i][gq][2] = s4.z; swv[i][gq][3] = s4.w;
-        } else {
-          swv[i][gq][0] = swv[i][gq][1] = swv[i][gq][2] = swv[i][gq][3] = sw0;
-        }
-        if (p.bias) load_bias4(pb, p.bias_dtype, nl, bv[i][gq]);
-        else bv[i][gq][0] = bv[i][gq][1] = bv[i][gq][2] = bv[i][gq][3] = 0.0f;
-      }
-    // this wave's 4 KB transpose area in the slot of stage g; every wave must
-    // be done reading that slot's fragments first
+    uint8_t *prm = smem + kStages * kStageBytes + (tile_i % kParamSets) * kParamSetBytes;
+    float *psa = reinterpret_cast<float *>(prm);
+    float *psw = reinterpret_cast<float *>(prm + kParamBytes);
+    float *pbf = reinterpret_cast<float *>(prm + 3 * kParamBytes);
+    // The transpose area: this wave's 4 KB of slot (g+1) % kStages, whose
+    // fragments every wave must have read first.  Its next DMA is issued after
+    // the barrier of stage g+1.
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
-    uint8_t *xb = sx + wave * 32 * 128;
+    lds_barrier();
+    // Parameters as float rows: per-tensor scales broadcast, bias converted
+    // (zeros without one), so the loops below read them without branches.
+    if (tid < 256) {
+      if (!p.sa_stride) psa[tid] = sa0;
+    } else {
+      const int t = tid - 256;
+      if (!p.sw_stride) psw[t] = sw0;
+      pbf[t] = p.bias ? bias_at(prm + 2 * kParamBytes, p.bias_dtype, t) : 0.0f;
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    lds_barrier();
+    uint8_t *xb = smem + ((g + 1) % kStages) * kStageBytes + wave * 32 * 128;
 #pragma unroll
     for (int j = 0; j < FM; ++j) {
       const int ml = wm * (BM / WM) + j * 32 + (lane & 31);
-      const float sam = p.sa_stride ? psa[ml] : sa0;
+      const float sam = psa[ml];
       const int wrow = lane & 31;
 #pragma unroll
       for (int i = 0; i < FN; ++i)
 #pragma unroll
         for (int gq = 0; gq < 4; ++gq) {
+          const int nl = wn * (BN / WN) + i * 32 + gq * 8 + (lane >> 5) * 4;
+          const f32x4 sw4 = *reinterpret_cast<const f32x4 *>(psw + nl);
+          const f32x4 b4 = *reinterpret_cast<const f32x4 *>(pbf + nl);
+          const float swv[4] = {sw4.x, sw4.y, sw4.z, sw4.w}, bv[4] = {b4.x, b4.y, b4.z, b4.w};
           float y[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float a = T::to_f32(acc[i][j][gq * 4 + e]);
-            y[e] = __builtin_fmaf(a, sam * swv[i][gq][e], bv[i][gq][e]);
+            y[e] = __builtin_fmaf(a, sam * swv[e], bv[e]);
             if constexpr (ACT == XGEN_ACT_GELU_TANH) y[e] = gelu_tanh(round_out<OUT_DT>(y[e]));
           }
           // row wrow, 8-byte chunk c8 (4 outputs) of the wave's 128-byte row,
@@ -370,8 +434,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) 
           *reinterpret_cast<u32x2 *>(xb + wrow * 128 + ((c8 ^ ((wrow >> 1) & 15)) << 3)) =
               u32x2{pack_out<OUT_DT>(y[0], y[1]), pack_out<OUT_DT>(y[2], y[3])};
           if constexpr (ACC_OUT) {
-            const int m = m0 + ml;
-            const int n = n0 + wn * (BN / WN) + i * 32 + gq * 8 + (lane >> 5) * 4;
+            const int m = m0 + ml, n = n0 + nl;
             if (m < p.M && n < p.N) {
               if constexpr (FP8) {
                 const f32x4 v = {acc[i][j][gq * 4 + 0], acc[i][j][gq * 4 + 1], acc[i][j][gq * 4 + 2],
@@ -404,7 +467,31 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) 
       for (int j = 0; j < FM; ++j) acc[i][j] = typename T::acc_t{};
     kt = 0;
     ++tile_i;
+  };
+
+  set_dma_tile(0);
+#pragma unroll
+  for (int s = 0; s < kStages - 1; ++s) issue_next();
+  wait_stage(0);
+  lds_barrier();
+  issue_next();
+  {
+    const uint8_t *sx = slot_of(0), *sw = sx + kTileBytes;
+#pragma unroll
+    for (int ks = 0; ks < T::kSteps; ++ks) {
+#pragma unroll
+      for (int f = 0; f < FN; ++f) wf[0][ks][f] = T::load(sw, row_w + f * 32, ks, lane);
+#pragma unroll
+      for (int f = 0; f < FM; ++f) xf[ks][f] = T::load(sx, row_x + f * 32, ks, lane);
+    }
   }
+  // two stages per trip so the weight-fragment buffers alternate without copies
+  for (int g = 0; g < G; g += 2) {
+    stage(g, 0);
+    if (g + 1 < G) stage(g + 1, 1);
+  }
+  // the loads of the stages past my last may still be writing LDS
+  wait_vmcnt<0>();
 }
 
 int cu_count() {
