@@ -2,6 +2,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <atomic>
+
 #include "xgen_common.h"
 
 namespace xgen {
@@ -25,6 +27,21 @@ int launch_status(const char *what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(XGEN_ERR_HIP, "%s: launch failed: %s", what, hipGetErrorString(e));
   return ok();
+}
+
+int device_cu_count() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cached[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  if (dev < kMaxDevices) {
+    const int c = cached[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int v = 0;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+  if (dev < kMaxDevices) cached[dev].store(v, std::memory_order_relaxed);
+  return v;
 }
 
 }  // namespace xgen

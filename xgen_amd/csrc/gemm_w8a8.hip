@@ -214,7 +214,14 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) 
   constexpr int kWaveLoads = kRowsPerWave / 16;  // 1 KB DMA loads per operand per wave
   constexpr int kLoadsPerStage = 2 * kWaveLoads; // per thread
   static_assert(kRowsPerWave % 16 == 0, "DMA rows");
-  static_assert(FN * 32 * 2 == 128 && kWaves * 32 * 128 <= kStageBytes, "epilogue transpose layout");
+  // epilogue transpose: one 32-row block of the wave's outputs, kRowBytes per row
+  constexpr int kRowBytes = FN * 32 * 2;
+  constexpr int kRowsPerLine = 256 / kRowBytes;      // rows sharing one 256-byte line of banks
+  constexpr int kChunks8 = kRowBytes / 8;            // 8-byte chunks per row
+  constexpr int kLanesPerRow = kRowBytes / 16;       // 16-byte chunks per row
+  constexpr int kRowsPerRead = 64 / kLanesPerRow;    // rows per 16-byte-per-lane read
+  static_assert((kRowBytes == 128 || kRowBytes == 256) && kWaves * 32 * kRowBytes <= kStageBytes,
+                "epilogue transpose layout");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kLdsBytes];
 
   // --- this workgroup's tiles ------------------------------------------------
@@ -356,8 +363,10 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) 
     // The operand loads of stage g + kStages are spread over the MFMAs: issued
     // together, the workgroup's loads queue up in the address unit, and a wave
     // whose load waits there cannot issue its MFMAs either.
-    constexpr int kSlots = T::kSteps * FM, kEvery = kSlots / kLoadsPerStage;
-    static_assert(kSlots % kLoadsPerStage == 0, "load spacing");
+    constexpr int kSlots = T::kSteps * FM;
+    constexpr int kEvery = kSlots >= kLoadsPerStage ? kSlots / kLoadsPerStage : 1;
+    constexpr int kPerSlot = kSlots >= kLoadsPerStage ? 1 : kLoadsPerStage / kSlots;
+    static_assert(kSlots % kLoadsPerStage == 0 || kLoadsPerStage % kSlots == 0, "load spacing");
 #pragma unroll
     for (int ks = 0; ks < T::kSteps; ++ks)
 #pragma unroll
@@ -366,7 +375,9 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) 
         for (int i = 0; i < FN; ++i) acc[i][j] = T::mma(wf[c][ks][i], xf[ks][j], acc[i][j]);
         xf[ks][j] = T::load(nx, row_x + j * 32, ks, lane);
         const int slot = ks * FM + j;
-        if (slot % kEvery == 0) issue_load(is, slot / kEvery);
+        if (slot % kEvery == 0)
+#pragma unroll
+          for (int u = 0; u < kPerSlot; ++u) issue_load(is, slot / kEvery * kPerSlot + u);
       }
     // Keep that order in the schedule: the weight reads, then per activation
     // fragment its MFMAs, its refill and (every kEvery fragments) one load.
@@ -377,7 +388,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) 
     for (int k = 0; k < kSlots; ++k) {
       __builtin_amdgcn_sched_group_barrier(kMfma, FN, 0);
       __builtin_amdgcn_sched_group_barrier(kDsRead, T::kReads, 0);
-      if (k % kEvery == 0) __builtin_amdgcn_sched_group_barrier(kVmemRead, 1, 0);
+      if (k % kEvery == 0) __builtin_amdgcn_sched_group_barrier(kVmemRead, kPerSlot, 0);
     }
     issue_advance();
     if (++kt < KT) return;
@@ -407,7 +418,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) 
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);
     lds_barrier();
-    uint8_t *xb = smem + ((g + 1) % kStages) * kStageBytes + wave * 32 * 128;
+    uint8_t *xb = smem + ((g + 1) % kStages) * kStageBytes + wave * 32 * kRowBytes;
 #pragma unroll
     for (int j = 0; j < FM; ++j) {
       const int ml = wm * (BM / WM) + j * 32 + (lane & 31);
@@ -428,10 +439,11 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) 
             y[e] = __builtin_fmaf(a, sam * swv[e], bv[e]);
             if constexpr (ACT == XGEN_ACT_GELU_TANH) y[e] = gelu_tanh(round_out<OUT_DT>(y[e]));
           }
-          // row wrow, 8-byte chunk c8 (4 outputs) of the wave's 128-byte row,
-          // XOR-swizzled by (row >> 1) & 15: conflict-free 64-bit writes
+          // row wrow, 8-byte chunk c8 (4 outputs) of the wave's row, XOR-swizzled
+          // by the row's index among the rows of its bank line: conflict-free
+          // 64-bit writes
           const int c8 = i * 8 + gq * 2 + (lane >> 5);
-          *reinterpret_cast<u32x2 *>(xb + wrow * 128 + ((c8 ^ ((wrow >> 1) & 15)) << 3)) =
+          *reinterpret_cast<u32x2 *>(xb + wrow * kRowBytes + ((c8 ^ ((wrow / kRowsPerLine) & (kChunks8 - 1))) << 3)) =
               u32x2{pack_out<OUT_DT>(y[0], y[1]), pack_out<OUT_DT>(y[2], y[3])};
           if constexpr (ACC_OUT) {
             const int m = m0 + ml, n = n0 + nl;
@@ -448,12 +460,13 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) 
             }
           }
         }
-      // read back 8 rows x 128 bytes per instruction: 16 bytes per lane, stored
-      // as full row segments (LDS operations of a wave complete in order)
+      // read back kRowsPerRead whole rows per instruction, 16 bytes per lane, and
+      // store them as full row segments (LDS operations of a wave complete in order)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int row = q * 8 + (lane >> 3), c16 = lane & 7, sw4 = (row >> 1) & 15;
-        u32x4 v = *reinterpret_cast<const u32x4 *>(xb + row * 128 + ((c16 ^ (sw4 >> 1)) << 4));
+      for (int q = 0; q < 32 / kRowsPerRead; ++q) {
+        const int row = q * kRowsPerRead + lane / kLanesPerRow, c16 = lane % kLanesPerRow;
+        const int sw4 = (row / kRowsPerLine) & (kChunks8 - 1);
+        u32x4 v = *reinterpret_cast<const u32x4 *>(xb + row * kRowBytes + ((c16 ^ (sw4 >> 1)) << 4));
         if (sw4 & 1) v = u32x4{v.z, v.w, v.x, v.y};
         const int m = m0 + wm * (BM / WM) + j * 32 + row;
         const int n = n0 + wn * (BN / WN) + c16 * 8;
@@ -494,23 +507,11 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) 
   wait_vmcnt<0>();
 }
 
-int cu_count() {
-  static int cus = 0;  // per process; all devices of this build are MI355X (256 CUs)
-  if (cus == 0) {
-    int dev = 0, v = 0;
-    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-      cus = v;
-    else
-      cus = 256;
-  }
-  return cus;
-}
-
 template <bool FP8, int ACT, int OUT_DT>
 void launch_gemm(const GemmArgs &a, bool acc_out, hipStream_t stream) {
   // one persistent workgroup per CU (a multiple of the 8 XCDs), never more than the tiles need
   const int ntiles = a.tiles_m * a.tiles_n;
-  int wgs = cu_count() / 8 * 8;
+  int wgs = device_cu_count() / 8 * 8;
   const int need = ((ntiles + 7) / 8) * 8;
   if (wgs > need) wgs = need;
   if (wgs < 8) wgs = 8;

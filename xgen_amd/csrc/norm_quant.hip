@@ -84,6 +84,10 @@ __device__ __forceinline__ void load_weight8(const void *w, int dtype, int ci, f
   }
 }
 
+// Streaming: a grid of as many workgroups as are resident walks the rows
+// (4 / WPR rows per workgroup per step; the walk is uniform over the
+// workgroup, so the cross-wave reductions stay in step); each wave loads its
+// next row and table index before it works on the current row.
 template <int NORM, int OUT, int WPR, int CH>
 __global__ __launch_bounds__(kThreads) void norm_affine_quant_kernel(NormArgs a) {
   constexpr int kRowsPerBlock = 4 / WPR;
@@ -91,136 +95,151 @@ __global__ __launch_bounds__(kThreads) void norm_affine_quant_kernel(NormArgs a)
   __shared__ uint32_t red_u[4];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + wave / WPR;
-  const bool row_ok = row < a.rows;
   const int lane_in_row = (wave % WPR) * 64 + lane;
   const int nchunks = a.width >> 3;
-  const int64_t r = row_ok ? row : 0;
-  const int64_t b = r / a.seq, s = r % a.seq;
-  const uint8_t *xr = a.x + b * a.xsb_bytes + s * a.xss_bytes;
+  const int64_t step = (int64_t)gridDim.x * kRowsPerBlock;
 
-  // 1. one read of the row
-  u32x4 c[CH];
-#pragma unroll
-  for (int j = 0; j < CH; ++j) {
-    const int ci = lane_in_row + j * 64 * WPR;
-    c[j] = (row_ok && ci < nchunks) ? *reinterpret_cast<const u32x4 *>(xr + (int64_t)ci * 16)
-                                    : u32x4{0, 0, 0, 0};
-  }
-  const int64_t g = row_ok ? a.indices[s] : 0;
-  const bool g_ok = g >= 0 && g < a.table_rows;
-
-  // 2. statistics (fp32, two passes over registers)
-  const float inv_w = 1.0f / (float)a.width;
-  float rstd, mean = 0.0f;
-  if constexpr (NORM == XGEN_NORM_LAYER) {
-    float acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < CH; ++j) {
-      float v[8];
-      unpack8<XGEN_DTYPE_BF16>(c[j], v);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc += v[i];
-    }
-    mean = row_sum<WPR>(acc, wave, lane, red_f) / (float)a.width;
-    float acc2 = 0.0f;
+  // one read of a row (zeros past the last row) and its table index
+  auto load_row = [&](int64_t row, u32x4 (&c)[CH], int64_t &g) {
+    const bool ok = row < a.rows;
+    const int64_t r = ok ? row : 0;
+    const int64_t b = r / a.seq, s = r % a.seq;
+    const uint8_t *xr = a.x + b * a.xsb_bytes + s * a.xss_bytes;
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
       const int ci = lane_in_row + j * 64 * WPR;
-      if (ci < nchunks) {
+      c[j] = (ok && ci < nchunks) ? *reinterpret_cast<const u32x4 *>(xr + (int64_t)ci * 16) : u32x4{0, 0, 0, 0};
+    }
+    g = ok ? a.indices[s] : 0;
+  };
+
+  u32x4 c[CH];
+  int64_t g;
+  int64_t base = (int64_t)blockIdx.x * kRowsPerBlock;
+  load_row(base + wave / WPR, c, g);
+  for (; base < a.rows; base += step) {
+    const int64_t row = base + wave / WPR;
+    const bool row_ok = row < a.rows;
+    u32x4 cn[CH];
+    int64_t gn;
+    load_row(row + step, cn, gn);
+    const bool g_ok = g >= 0 && g < a.table_rows;
+
+    // statistics (fp32, two passes over registers)
+    float rstd, mean = 0.0f;
+    if constexpr (NORM == XGEN_NORM_LAYER) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < CH; ++j) {
         float v[8];
         unpack8<XGEN_DTYPE_BF16>(c[j], v);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float d = v[i] - mean;
-          acc2 = __builtin_fmaf(d, d, acc2);
+        for (int i = 0; i < 8; ++i) acc += v[i];
+      }
+      mean = row_sum<WPR>(acc, wave, lane, red_f) / (float)a.width;
+      float acc2 = 0.0f;
+#pragma unroll
+      for (int j = 0; j < CH; ++j) {
+        const int ci = lane_in_row + j * 64 * WPR;
+        if (ci < nchunks) {
+          float v[8];
+          unpack8<XGEN_DTYPE_BF16>(c[j], v);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float d = v[i] - mean;
+            acc2 = __builtin_fmaf(d, d, acc2);
+          }
         }
       }
+      const float var = row_sum<WPR>(acc2, wave, lane, red_f) / (float)a.width;
+      rstd = 1.0f / __builtin_sqrtf(var + a.eps);
+    } else {
+      float acc2 = 0.0f;
+#pragma unroll
+      for (int j = 0; j < CH; ++j) {
+        float v[8];
+        unpack8<XGEN_DTYPE_BF16>(c[j], v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc2 = __builtin_fmaf(v[i], v[i], acc2);
+      }
+      const float ms = row_sum<WPR>(acc2, wave, lane, red_f) / (float)a.width;
+      rstd = 1.0f / __builtin_sqrtf(ms + a.eps);
     }
-    const float var = row_sum<WPR>(acc2, wave, lane, red_f) / (float)a.width;
-    rstd = 1.0f / __builtin_sqrtf(var + a.eps);
-  } else {
-    float acc2 = 0.0f;
+
+    // normalise, modulate with the table row, keep m as packed bf16 (in c)
+    const uint8_t *sr = a.scale_tab + (g_ok ? g : 0) * a.scale_stride_bytes;
+    const uint8_t *tr = a.shift_tab + (g_ok ? g : 0) * a.shift_stride_bytes;
+    u16x2 am = {0, 0};
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
-      float v[8];
-      unpack8<XGEN_DTYPE_BF16>(c[j], v);
+      const int ci = lane_in_row + j * 64 * WPR;
+      if (row_ok && g_ok && ci < nchunks) {
+        float v[8], sc[8], sh[8];
+        unpack8<XGEN_DTYPE_BF16>(c[j], v);
+        unpack8<XGEN_DTYPE_BF16>(*reinterpret_cast<const u32x4 *>(sr + (int64_t)ci * 16), sc);
+        unpack8<XGEN_DTYPE_BF16>(*reinterpret_cast<const u32x4 *>(tr + (int64_t)ci * 16), sh);
+        float n[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc2 = __builtin_fmaf(v[i], v[i], acc2);
-    }
-    const float ms = row_sum<WPR>(acc2, wave, lane, red_f) / (float)a.width;
-    rstd = 1.0f / __builtin_sqrtf(ms + a.eps);
-  }
-  (void)inv_w;
-
-  // 3. normalise, modulate with the table row, keep m as packed bf16
-  const uint8_t *sr = a.scale_tab + (g_ok ? g : 0) * a.scale_stride_bytes;
-  const uint8_t *tr = a.shift_tab + (g_ok ? g : 0) * a.shift_stride_bytes;
-  u32x4 mp[CH];
-  u16x2 am = {0, 0};
+        for (int i = 0; i < 8; ++i) n[i] = (NORM == XGEN_NORM_LAYER) ? (v[i] - mean) * rstd : v[i] * rstd;
+        if (a.weight_dtype != XGEN_DTYPE_NONE) {
+          float wv[8];
+          load_weight8(a.weight, a.weight_dtype, ci, wv);
 #pragma unroll
-  for (int j = 0; j < CH; ++j) {
-    const int ci = lane_in_row + j * 64 * WPR;
-    if (row_ok && g_ok && ci < nchunks) {
-      float v[8], sc[8], sh[8];
-      unpack8<XGEN_DTYPE_BF16>(c[j], v);
-      unpack8<XGEN_DTYPE_BF16>(*reinterpret_cast<const u32x4 *>(sr + (int64_t)ci * 16), sc);
-      unpack8<XGEN_DTYPE_BF16>(*reinterpret_cast<const u32x4 *>(tr + (int64_t)ci * 16), sh);
-      float n[8];
+          for (int i = 0; i < 8; ++i) n[i] *= wv[i];
+        }
+        uint32_t pk[4];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) n[i] = (NORM == XGEN_NORM_LAYER) ? (v[i] - mean) * rstd : v[i] * rstd;
-      if (a.weight_dtype != XGEN_DTYPE_NONE) {
-        float wv[8];
-        load_weight8(a.weight, a.weight_dtype, ci, wv);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) n[i] *= wv[i];
-      }
-      uint32_t pk[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float n0 = round_bf16(n[2 * i]), n1 = round_bf16(n[2 * i + 1]);
-        const float f0 = round_bf16(1.0f + sc[2 * i]), f1 = round_bf16(1.0f + sc[2 * i + 1]);
-        const float p0 = round_bf16(n0 * f0), p1 = round_bf16(n1 * f1);
-        pk[i] = pack_bf16x2(p0 + sh[2 * i], p1 + sh[2 * i + 1]);
-      }
-      mp[j] = u32x4{pk[0], pk[1], pk[2], pk[3]};
-      am = absmax_chunk<XGEN_DTYPE_BF16>(mp[j], am);
-    } else {
-      mp[j] = u32x4{0, 0, 0, 0};
-    }
-  }
-  const uint32_t amax_bits = row_max_u32<WPR>(hmax_u16x2(am), wave, lane, red_u);
-  if (!row_ok) return;
-
-  // 4. quantize from registers
-  const float amax = Half2<XGEN_DTYPE_BF16>::from_absbits(amax_bits);
-  RowQuant p = (OUT == XGEN_DTYPE_E4M3) ? fp8_row_params(amax) : i8_row_params(amax);
-  uint8_t *qr = a.q + row * (int64_t)a.width;
-  uint8_t *nr = a.normed ? a.normed + row * (int64_t)a.width * 2 : nullptr;
-#pragma unroll
-  for (int j = 0; j < CH; ++j) {
-    const int ci = lane_in_row + j * 64 * WPR;
-    if (ci < nchunks) {
-      u32x2 out;
-      if (g_ok) {
-        float v[8];
-        unpack8<XGEN_DTYPE_BF16>(mp[j], v);
-        out = quant8<OUT>(v, p);
+        for (int i = 0; i < 4; ++i) {
+          const float n0 = round_bf16(n[2 * i]), n1 = round_bf16(n[2 * i + 1]);
+          const float f0 = round_bf16(1.0f + sc[2 * i]), f1 = round_bf16(1.0f + sc[2 * i + 1]);
+          const float p0 = round_bf16(n0 * f0), p1 = round_bf16(n1 * f1);
+          pk[i] = pack_bf16x2(p0 + sh[2 * i], p1 + sh[2 * i + 1]);
+        }
+        c[j] = u32x4{pk[0], pk[1], pk[2], pk[3]};
+        am = absmax_chunk<XGEN_DTYPE_BF16>(c[j], am);
       } else {
-        out = (OUT == XGEN_DTYPE_E4M3) ? u32x2{0x7f7f7f7fu, 0x7f7f7f7fu} : u32x2{0u, 0u};
+        c[j] = u32x4{0, 0, 0, 0};
       }
-      *reinterpret_cast<u32x2 *>(qr + (int64_t)ci * 8) = out;
-      if (nr) *reinterpret_cast<u32x4 *>(nr + (int64_t)ci * 16) = mp[j];
     }
+    const uint32_t amax_bits = row_max_u32<WPR>(hmax_u16x2(am), wave, lane, red_u);
+
+    // quantize from registers
+    if (row_ok) {
+      const float amax = Half2<XGEN_DTYPE_BF16>::from_absbits(amax_bits);
+      const RowQuant p = (OUT == XGEN_DTYPE_E4M3) ? fp8_row_params(amax) : i8_row_params(amax);
+      uint8_t *qr = a.q + row * (int64_t)a.width;
+      uint8_t *nr = a.normed ? a.normed + row * (int64_t)a.width * 2 : nullptr;
+#pragma unroll
+      for (int j = 0; j < CH; ++j) {
+        const int ci = lane_in_row + j * 64 * WPR;
+        if (ci < nchunks) {
+          u32x2 out;
+          if (g_ok) {
+            float v[8];
+            unpack8<XGEN_DTYPE_BF16>(c[j], v);
+            out = quant8<OUT>(v, p);
+          } else {
+            out = (OUT == XGEN_DTYPE_E4M3) ? u32x2{0x7f7f7f7fu, 0x7f7f7f7fu} : u32x2{0u, 0u};
+          }
+          *reinterpret_cast<u32x2 *>(qr + (int64_t)ci * 8) = out;
+          if (nr) *reinterpret_cast<u32x4 *>(nr + (int64_t)ci * 16) = c[j];
+        }
+      }
+      if (lane_in_row == 0) a.token_scale[row] = g_ok ? p.s : __builtin_nanf("");
+    }
+#pragma unroll
+    for (int j = 0; j < CH; ++j) c[j] = cn[j];
+    g = gn;
   }
-  if (lane_in_row == 0) a.token_scale[row] = g_ok ? p.s : __builtin_nanf("");
 }
 
 template <int NORM, int OUT, int WPR, int CH>
 void launch(const NormArgs &a, hipStream_t stream) {
   constexpr int kRowsPerBlock = 4 / WPR;
-  const int64_t blocks = (a.rows + kRowsPerBlock - 1) / kRowsPerBlock;
-  norm_affine_quant_kernel<NORM, OUT, WPR, CH><<<dim3((unsigned)blocks), dim3(kThreads), 0, stream>>>(a);
+  static const int per_cu = resident_blocks_per_cu(norm_affine_quant_kernel<NORM, OUT, WPR, CH>, kThreads);
+  const int64_t need = (a.rows + kRowsPerBlock - 1) / kRowsPerBlock;
+  const int64_t cap = (int64_t)device_cu_count() * per_cu;
+  norm_affine_quant_kernel<NORM, OUT, WPR, CH><<<dim3((unsigned)(need < cap ? need : cap)), dim3(kThreads), 0, stream>>>(a);
 }
 
 template <int NORM, int OUT>

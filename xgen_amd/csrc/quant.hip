@@ -22,57 +22,72 @@ constexpr int kThreads = 256;  // 4 waves per workgroup
 
 // WPR waves per row, CH chunks of 8 elements per lane: one row covers up to
 // 512 * WPR * CH elements.  Requires cols % 8 == 0 and 16-byte aligned rows.
+//
+// Streaming: a grid of a few workgroups per CU walks the rows (4 / WPR rows
+// per workgroup per step); each wave loads its next row before it reduces and
+// stores the current one, so loads stay in flight through the reduction.
 template <int DT, int OUT, int WPR, int CH>
 __global__ __launch_bounds__(kThreads) void quant_rows_vec_kernel(
     const uint8_t *__restrict__ x, int64_t rows, int cols, int64_t ldx_bytes,
     uint8_t *__restrict__ q, int64_t ldq, float *__restrict__ scale) {
   constexpr int kRowsPerBlock = 4 / WPR;
+  __shared__ uint32_t red[2][4];  // cross-wave max, double-buffered by step parity
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int row_in_block = wave / WPR;
   const int wave_in_row = wave % WPR;
-  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + row_in_block;
-  const bool row_ok = row < rows;
   const int nchunks = cols >> 3;
   const int lane_in_row = wave_in_row * 64 + lane;
+  const int64_t step = (int64_t)gridDim.x * kRowsPerBlock;
 
-  const uint8_t *xr = x + (row_ok ? row : 0) * ldx_bytes;
+  auto load_row = [&](int64_t row, u32x4 (&c)[CH]) {
+    const bool ok = row < rows;
+    const uint8_t *xr = x + (ok ? row : 0) * ldx_bytes;
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int ci = lane_in_row + j * 64 * WPR;
+      c[j] = (ok && ci < nchunks) ? *reinterpret_cast<const u32x4 *>(xr + (int64_t)ci * 16) : u32x4{0, 0, 0, 0};
+    }
+  };
+
   u32x4 c[CH];
-  u16x2 m = {0, 0};
-#pragma unroll
-  for (int j = 0; j < CH; ++j) {
-    const int ci = lane_in_row + j * 64 * WPR;
-    if (row_ok && ci < nchunks) {
-      c[j] = *reinterpret_cast<const u32x4 *>(xr + (int64_t)ci * 16);
-    } else {
-      c[j] = u32x4{0, 0, 0, 0};
-    }
-    m = absmax_chunk<DT>(c[j], m);
-  }
-  uint32_t amax_bits = wave_max_u32(hmax_u16x2(m));
-  if constexpr (WPR > 1) {
-    __shared__ uint32_t red[4];
-    if (lane == 0) red[wave] = amax_bits;
-    __syncthreads();
-    const int w0 = row_in_block * WPR;
-#pragma unroll
-    for (int i = 0; i < WPR; ++i) amax_bits = amax_bits > red[w0 + i] ? amax_bits : red[w0 + i];
-  }
-  if (!row_ok) return;
-  const float amax = Half2<DT>::from_absbits(amax_bits);
-  const RowQuant p = (OUT == XGEN_DTYPE_E4M3) ? fp8_row_params(amax) : i8_row_params(amax);
+  int parity = 0;
+  int64_t base = (int64_t)blockIdx.x * kRowsPerBlock;  // uniform over the workgroup
+  load_row(base + row_in_block, c);
+  for (; base < rows; base += step, parity ^= 1) {
+    const int64_t row = base + row_in_block;
+    u32x4 cn[CH];
+    load_row(row + step, cn);
 
-  uint8_t *qr = q + row * ldq;
+    u16x2 m = {0, 0};
 #pragma unroll
-  for (int j = 0; j < CH; ++j) {
-    const int ci = lane_in_row + j * 64 * WPR;
-    if (ci < nchunks) {
-      float v[8];
-      unpack8<DT>(c[j], v);
-      *reinterpret_cast<u32x2 *>(qr + (int64_t)ci * 8) = quant8<OUT>(v, p);
+    for (int j = 0; j < CH; ++j) m = absmax_chunk<DT>(c[j], m);
+    uint32_t amax_bits = wave_max_u32(hmax_u16x2(m));
+    if constexpr (WPR > 1) {
+      if (lane == 0) red[parity][wave] = amax_bits;
+      __syncthreads();
+      const int w0 = row_in_block * WPR;
+#pragma unroll
+      for (int i = 0; i < WPR; ++i) amax_bits = amax_bits > red[parity][w0 + i] ? amax_bits : red[parity][w0 + i];
     }
+    if (row < rows) {
+      const float amax = Half2<DT>::from_absbits(amax_bits);
+      const RowQuant p = (OUT == XGEN_DTYPE_E4M3) ? fp8_row_params(amax) : i8_row_params(amax);
+      uint8_t *qr = q + row * ldq;
+#pragma unroll
+      for (int j = 0; j < CH; ++j) {
+        const int ci = lane_in_row + j * 64 * WPR;
+        if (ci < nchunks) {
+          float v[8];
+          unpack8<DT>(c[j], v);
+          *reinterpret_cast<u32x2 *>(qr + (int64_t)ci * 8) = quant8<OUT>(v, p);
+        }
+      }
+      if (lane_in_row == 0) scale[row] = p.s;
+    }
+#pragma unroll
+    for (int j = 0; j < CH; ++j) c[j] = cn[j];
   }
-  if (lane_in_row == 0) scale[row] = p.s;
 }
 
 // Any width / alignment: one workgroup per row, two passes over global memory.
@@ -116,7 +131,11 @@ template <int DT, int OUT, int WPR, int CH>
 void launch_vec(const void *x, int64_t rows, int64_t cols, int64_t ldx, void *q, int64_t ldq,
                 float *scale, hipStream_t stream) {
   constexpr int kRowsPerBlock = 4 / WPR;
-  const int64_t blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+  // as many workgroups as are resident at once (a streaming grid must not queue)
+  static const int per_cu = resident_blocks_per_cu(quant_rows_vec_kernel<DT, OUT, WPR, CH>, kThreads);
+  const int64_t need = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+  const int64_t cap = (int64_t)device_cu_count() * per_cu;
+  const int64_t blocks = need < cap ? need : cap;
   quant_rows_vec_kernel<DT, OUT, WPR, CH><<<dim3((unsigned)blocks), dim3(kThreads), 0, stream>>>(
       static_cast<const uint8_t *>(x), rows, (int)cols, ldx * 2, static_cast<uint8_t *>(q), ldq,
       scale);

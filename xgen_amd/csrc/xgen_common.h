@@ -16,6 +16,15 @@ int fail(int status, const char *fmt, ...) __attribute__((format(printf, 2, 3)))
 int ok();
 // Maps the result of the launch just made to XGEN_OK / XGEN_ERR_HIP.
 int launch_status(const char *what);
+// Compute units of the current device (cached per device; 256 on MI355X).
+int device_cu_count();
+// Workgroups of `threads` threads of `kernel` resident on one CU at once (>= 1).
+template <typename K>
+int resident_blocks_per_cu(K kernel, int threads) {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0) != hipSuccess || n < 1) n = 1;
+  return n;
+}
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool is_input_dtype(int dt) { return dt == XGEN_DTYPE_BF16 || dt == XGEN_DTYPE_F16; }
