@@ -271,6 +271,38 @@ def main():
         kernels["gemm_int8_qkv"] = {"ms": ms_i8, "tops": flop / (ms_i8 * 1e-3) / 1e12,
                                     "frac_of_peak": flop / (ms_i8 * 1e-3) / 1e12 / PEAK_INT8_TOPS}
 
+    # ---- C5 chain at a 10 s clip's share (M=31,248): front end -> QKV -> out -> up(+GELU) -> down
+    if want("c5"):
+        from xgen_amd.operator.dit_chain import DiTLinearChain
+        M5 = W.M_10S
+        g5 = W.generator(5, dev)
+        x5 = torch.cat([W.activations(M5 // 2, K, g5, dev)[0] for _ in range(2)])[None]
+        sh5, sc5 = W.adaln_tables(20, K, g5, dev)
+        idx5 = torch.randint(20, (M5,), generator=g5, device=dev)
+        chain = DiTLinearChain(*[t for n in ("qkv", "out", "ffn_up", "ffn_down") for t in W.weight(n, g5, dev)])
+        ms_chain = timed(lambda: chain(x5, sc5, sh5, idx5), max(5, args.steps // 5), args.warmup)
+        chain_flop = 2.0 * M5 * K * (3 * K + K + 4 * K + 4 * K)
+        qkv5, o5, h5, _ = chain(x5, sc5, sh5, idx5)
+        qa5, sa5 = xops.quantize_rows(o5.reshape(M5, K), fp8)
+        qh5, sh5_ = xops.quantize_rows(h5.reshape(M5, 4 * K), fp8)
+        qv5, sv5 = xops.quantize_rows(qkv5.reshape(M5, 3 * K)[:, 2 * K:], fp8)
+        stages = {"front_end": timed(lambda: xops.norm_affine_quant(x5, None, sc5, sh5, idx5, 1e-6, N.NORM_LAYER,
+                                                                    fp8, False), args.steps, args.warmup)}
+        qf5, sf5, _ = xops.norm_affine_quant(x5, None, sc5, sh5, idx5, 1e-6, N.NORM_LAYER, fp8, False)
+        stages["qkv"] = timed(lambda: chain.qkv.forward_quantized(qf5, sf5), args.steps, args.warmup)
+        stages["requant_v"] = timed(lambda: xops.quantize_rows(qkv5.reshape(M5, 3 * K)[:, 2 * K:], fp8),
+                                    args.steps, args.warmup)
+        stages["out"] = timed(lambda: chain.out.forward_quantized(qv5, sv5), args.steps, args.warmup)
+        stages["requant_o"] = timed(lambda: xops.quantize_rows(o5.reshape(M5, K), fp8), args.steps, args.warmup)
+        stages["ffn_up_gelu"] = timed(lambda: chain.ff_up.forward_quantized(qa5, sa5), args.steps, args.warmup)
+        stages["requant_h"] = timed(lambda: xops.quantize_rows(h5.reshape(M5, 4 * K), fp8), args.steps,
+                                    args.warmup)
+        stages["ffn_down"] = timed(lambda: chain.ff_down.forward_quantized(qh5, sh5_), args.steps, args.warmup)
+        kernels["c5_chain_m31248"] = {"ms": ms_chain, "gemm_flop": chain_flop,
+                                      "tflops": chain_flop / (ms_chain * 1e-3) / 1e12,
+                                      "stages_ms": stages}
+        del chain, x5, qkv5, o5, h5, qa5, qh5, qv5, qf5
+
     # ---- CPU baseline (oracle fake-quant path) on a bounded sample
     cpu = None
     if not args.no_cpu_baseline:

@@ -255,6 +255,27 @@ def w8a8_linear_int8(qa, sa, qw, sw, bias, out_dtype=torch.bfloat16, activation=
     return dequant_epilogue(int8_accumulate_exact(qa, qw).double(), sa, sw, bias, out_dtype, activation)
 
 
+def dit_chain_fp8(x, scale_tab, shift_tab, indices, weights, eps=1e-6):
+    """C5 composite: LayerNorm + AdaLN modulation + per-token FP8 quant (A10/A11), then QKV,
+    out-projection on the V third (attention stand-in), FFN up with GELU-tanh (A12) and FFN down,
+    each later projection quantizing its own bf16 input per token.  `weights` maps
+    qkv/out/ffn_up/ffn_down to (bf16 W [N,K], bf16 bias [N]); weights are quantized per channel.
+    Returns (qkv, out, hidden, y) as bf16 [B*S, N]."""
+    q, s, _ = norm_affine_quant(x, None, scale_tab, shift_tab, indices, eps, "layer", "fp8")
+    packed = {k: quantize_rows_fp8(w) + (b.detach().cpu(),) for k, (w, b) in weights.items()}
+    d = x.shape[-1]
+
+    def lin(qa, sa, name, act=None):
+        qw, sw, b = packed[name]
+        return w8a8_linear_fp8(qa, sa, qw, sw, b, torch.bfloat16, act)
+
+    qkv = lin(q, s, "qkv")
+    o = lin(*quantize_rows_fp8(qkv[:, 2 * d:].contiguous()), "out")
+    h = lin(*quantize_rows_fp8(o), "ffn_up", "gelu_tanh")
+    y = lin(*quantize_rows_fp8(h), "ffn_down")
+    return qkv, o, h, y
+
+
 def cpu_fake_quant_linear_fp8(x: torch.Tensor, qw: torch.Tensor, sw: torch.Tensor, bias) -> torch.Tensor:
     """CPU quantize-dequantize W8A8 linear (the reported CPU baseline): per-token FP8
     quantization, dequantize to fp32, F.linear in fp32, + bias, bf16."""

@@ -1,0 +1,63 @@
+"""The quantized linears of one DiT block in execution order, on the HIP kernels.
+
+The reference runs them as separate eager steps around its attention
+(x_diffusers/x_diffusers/framework/transformer/hunyuan.py:390-400 for the FFN
+half: norm2 -> modulate -> ff; h3_npu_fusion.py:74-119 for the fused front end
+and the shared-QKV projection).  Here the front end is one kernel
+(LayerNorm + AdaLN-table modulation + per-token quantization), its quantized
+activation is shared by the Q, K and V columns of one [3d, d] projection, and
+every later projection quantizes its own input per token:
+
+    q, s = norm_affine_quant(x, tables, indices)        # fused front end
+    qkv  = QKV(q, s)                                     # [M, 3d]
+    a    = attention(qkv)                                # caller's (default: the V third)
+    o    = out_proj(a)                                   # [M, d]
+    h    = ff_up(o)  with the GELU-tanh epilogue         # [M, 4d]
+    y    = ff_down(h)                                    # [M, d]
+
+Attention is outside this path; without a callable the V third of the QKV
+output stands in for it (the out-projection then sees a real [M, d] bf16
+activation of the right statistics).  Residual adds and gates are left to the
+caller, as in the reference block.
+"""
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from .h3_fp8 import H3FP8Linear
+from .nq2 import norm_affine_quant
+
+
+class DiTLinearChain(nn.Module):
+    """QKV, out-projection, FFN up (GELU-tanh) and FFN down as W8A8 FP8
+    linears with per-channel weight and per-token activation scales."""
+
+    def __init__(self, w_qkv, b_qkv, w_out, b_out, w_up, b_up, w_down, b_down, *, eps: float = 1e-6):
+        super().__init__()
+        opts = dict(weight_scaling="channel", activation_scaling="token")
+        self.qkv = H3FP8Linear(w_qkv, b_qkv, **opts)
+        self.out = H3FP8Linear(w_out, b_out, **opts)
+        self.ff_up = H3FP8Linear(w_up, b_up, activation="gelu_tanh", **opts)
+        self.ff_down = H3FP8Linear(w_down, b_down, **opts)
+        self.eps = float(eps)
+        d = self.qkv.in_features
+        if self.qkv.out_features != 3 * d or self.out.in_features != d or self.ff_up.in_features != d \
+                or self.ff_down.in_features != self.ff_up.out_features or self.ff_down.out_features != d:
+            raise ValueError("DiTLinearChain: inconsistent projection shapes")
+
+    def forward(self, x, scale_table, shift_table, indices, attention=None):
+        """x bf16 [B, S, d]; scale/shift tables bf16 [T, d]; indices int64 [S].
+        Returns (qkv [B,S,3d], out-proj [B,S,d], FFN hidden after GELU [B,S,4d],
+        FFN output [B,S,d]), all bf16."""
+        if x.dim() != 3:
+            raise ValueError("DiTLinearChain expects x of shape [B, S, d]")
+        B, S, d = x.shape
+        q, s = norm_affine_quant(x, None, scale_table, shift_table, indices, eps=self.eps, norm="layer",
+                                 out_dtype=torch.float8_e4m3fn)
+        qkv = self.qkv.forward_quantized(q, s).reshape(B, S, 3 * d)
+        a = attention(qkv) if attention is not None else qkv[..., 2 * d:]
+        o = self.out(a)
+        h = self.ff_up(o)
+        y = self.ff_down(h)
+        return qkv, o, h, y
