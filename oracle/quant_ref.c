@@ -14,7 +14,9 @@
  *  oracle_quant_rows_int8    the per-row int8 quantizer the reference restates in
  *                            npu_fusion/f2bc/op_kernel/f2bc_kernel.asc:89-107:
  *                            s = amax * fl(1/127); alpha = fl(127 / amax);
- *                            q = rint_half_even(fl(x * alpha)), NaN -> 0.
+ *                            q = rint_half_even(fl(x * alpha)); a non-finite
+ *                            product (NaN, or inf when 127 / amax overflows for
+ *                            a subnormal amax) -> 0, as for a flushed zero row.
  *  oracle_check_fast_division   exhaustive check, for every (x, amax) pair of
  *                            16-bit inputs the row quantizers can see, that the
  *                            HIP kernels' division by the row scale
@@ -134,7 +136,7 @@ void oracle_quant_rows_int8(int fmt, const uint16_t *x, int64_t rows, int64_t co
     scale[r] = amax * inv127;
     for (int64_t c = 0; c < cols; ++c) {
       const float y = oracle_half_to_f32(fmt, xr[c]) * alpha;
-      q[r * cols + c] = isnan(y) ? 0 : (int8_t)nearbyintf(y);
+      q[r * cols + c] = isfinite(y) ? (int8_t)nearbyintf(y) : 0;
     }
   }
 }

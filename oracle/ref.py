@@ -122,14 +122,15 @@ def quantize_rows_fp8(x: torch.Tensor):
 
 
 def quantize_rows_int8(x: torch.Tensor):
-    """f2bc_kernel.asc:89-107: scale = amax*fl(1/127), q = rint(x*fl(127/amax)), NaN -> 0."""
+    """f2bc_kernel.asc:89-107: scale = amax*fl(1/127), q = rint(x*fl(127/amax)); a
+    non-finite product (NaN, or inf when 127/amax overflows for a subnormal amax) -> 0."""
     v = x.detach().cpu().float().reshape(-1, x.shape[-1])
     amax = v.abs().amax(dim=-1)
     inv127 = torch.tensor(1.0, dtype=torch.float32) / 127.0
     scale = amax * inv127
     alpha = torch.tensor(127.0, dtype=torch.float32) / amax
     y = v * alpha[:, None]
-    q = torch.where(torch.isnan(y), torch.zeros_like(y), torch.round(y)).to(torch.int8)
+    q = torch.where(torch.isfinite(y), torch.round(y), torch.zeros_like(y)).to(torch.int8)
     return q.reshape(x.shape), scale
 
 

@@ -64,3 +64,21 @@ def test_scale_uses_reciprocal_multiplier():
     _, s = R.quantize_rows_int8(x.to(torch.bfloat16))
     a = x[:, 0].to(torch.bfloat16).float()
     assert torch.equal(s, a * (torch.tensor(1.0) / 127.0))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_subnormal_amax_row_quantizes_to_zeros(dtype):
+    """127/amax overflows for a subnormal amax: every product is non-finite or
+    -0 * inf = NaN, and the row comes out as zeros (the flushed-zero-row rule),
+    in the torch and the C restatement alike."""
+    tiny = 2.0 ** -130 if dtype == torch.bfloat16 else 2.0 ** -24
+    x = torch.zeros(2, 64)
+    x[0, :] = -0.0
+    x[0, 3] = tiny
+    x[1, 5] = -tiny
+    x = x.to(dtype)
+    q, s = R.quantize_rows_int8(x)
+    qc, sc = R.quantize_rows_c(x, "int8")
+    if dtype == torch.bfloat16:   # f16's smallest subnormal still gives a finite 127/amax
+        assert (q == 0).all()
+    assert torch.equal(q, qc) and torch.equal(s.view(torch.int32), sc.view(torch.int32))

@@ -184,16 +184,16 @@ __device__ __forceinline__ RowQuant i8_row_params(float amax) {
   RowQuant p;
   p.s = canonical_nan(amax * kInv127);
   p.mul = 127.0f / amax;
-  // amax == 0 (alpha = inf), inf or NaN: products may be NaN -> slow path.
-  p.finite = amax > 0.0f && __builtin_isfinite(amax);
+  // amax == 0 or subnormal (alpha = inf), inf or NaN: products may be non-finite -> slow path.
+  p.finite = amax > 0.0f && __builtin_isfinite(amax) && __builtin_isfinite(p.mul);
   return p;
 }
 
-// Slow per-element INT8 path (zero or non-finite amax): a NaN product gives 0,
-// so a zero row quantizes to zeros (swiglu_quant_kernel.asc:72-75).
+// Slow per-element INT8 path (zero, subnormal or non-finite amax): a non-finite
+// product gives 0, so a zero row quantizes to zeros (swiglu_quant_kernel.asc:72-75).
 __device__ __forceinline__ uint32_t i8_slow_byte(float x, float alpha) {
   float y = x * alpha;
-  y = (y == y) ? __builtin_rintf(y) : 0.0f;
+  y = __builtin_isfinite(y) ? __builtin_rintf(y) : 0.0f;
   return (uint32_t)(int32_t)y & 0xffu;
 }
 
