@@ -33,6 +33,9 @@ sys.path.insert(0, str(ROOT))
 PEAK_FP8_TFLOPS = 5000.0   # MI355X dense FP8 MFMA
 PEAK_INT8_TOPS = 5000.0    # MI355X dense INT8 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+# HBM (fabric) bytes per launch of the QKV GEMM, from rocprofv3 FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000
+# (copy-kernel calibration); profiles/hbm_traffic_c2_qkv_gemm_quant_front_end.md holds the counts.
+QKV_GEMM_TRAFFIC_BYTES = (403504 * 2.0 + 281232 * 1.0) * 1024
 METRIC = "FP8 W8A8 linear TFLOP/s (% MFMA peak) + quant GB/s, M=15.6k d=3072, 1 GPU"
 
 
@@ -329,7 +332,7 @@ def main():
         "config": {"workload": "c2_qkv: per-token FP8 quant + FP8 W8A8 GEMM, M=15624 K=3072 N=9216, bf16 out",
                    "M": M, "K": K, "N": Nf, "weight_scaling": "per-channel", "activation_scaling": "per-token"},
         "roofline": {"bound": "mfma", "achieved": gemm_tflops, "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
-                     "frac": gemm_tflops / PEAK_FP8_TFLOPS, "traffic": None,
+                     "frac": gemm_tflops / PEAK_FP8_TFLOPS, "traffic": QKV_GEMM_TRAFFIC_BYTES,
                      "kernel": "gemm_w8a8_kernel<fp8> (QKV)", "flop_per_launch": flop},
         "quant": {"gbs": quant_gbs, "frac_of_hbm": quant_gbs / PEAK_HBM_GBS},
         "kernels": kernels,
