@@ -20,8 +20,9 @@
  *  oracle_check_fast_division   exhaustive check, for every (x, amax) pair of
  *                            16-bit inputs the row quantizers can see, that the
  *                            HIP kernels' division by the row scale
- *                            (q0 = x*r; e = fma(-q0, s, x); q = fma(e, r, q0),
- *                            r = 1/s, sign of x restored, for amax >= 2^-100)
+ *                            (a = |x|; q0 = a*r; e = fma(-q0, s, a);
+ *                            q = fma(e, r, q0), r = 1/s, sign of x restored,
+ *                            for amax >= 2^-100)
  *                            gives the same e4m3 byte as IEEE x / s.
  *
  * NaN convention: any NaN byte is written as 0x7f (canonical positive NaN).
@@ -141,9 +142,11 @@ void oracle_quant_rows_int8(int fmt, const uint16_t *x, int64_t rows, int64_t co
   }
 }
 
+/* The kernels divide the magnitude and copy the input's sign bit into the byte. */
 static float fast_div(float x, float s, float r) {
-  const float q0 = x * r;
-  const float e = fmaf(-q0, s, x);
+  const float a = fabsf(x);
+  const float q0 = a * r;
+  const float e = fmaf(-q0, s, a);
   return copysignf(fmaf(e, r, q0), x);
 }
 

@@ -10,7 +10,7 @@
 // with every intermediate rounded to bf16 as the eager bf16 ops round it
 // (x_base/x_base/operator/h3_indexed_affine.py:22-28).
 //
-// Layout: one row per wave (two waves per row above 4096 columns).  The row
+// Layout: one to four waves per row (at most 4 chunks of 8 per lane).  The row
 // stays in registers from the single HBM read to the single quantized write;
 // mean / variance / max |m| are wave reductions (plus an LDS exchange when a
 // row spans two waves).  The two table rows come from L2 (the table is small).
@@ -88,7 +88,9 @@ __device__ __forceinline__ void load_weight8(const void *w, int dtype, int ci, f
 // (4 / WPR rows per workgroup per step; the walk is uniform over the
 // workgroup, so the cross-wave reductions stay in step); each wave loads its
 // next row and table index before it works on the current row.
-template <int NORM, int OUT, int WPR, int CH>
+// FULL: the row is exactly CH chunks per lane (width == 512 * WPR * CH), so
+// no chunk needs a bounds check.
+template <int NORM, int OUT, int WPR, int CH, bool FULL>
 __global__ __launch_bounds__(kThreads) void norm_affine_quant_kernel(NormArgs a) {
   constexpr int kRowsPerBlock = 4 / WPR;
   __shared__ float red_f[4];
@@ -98,6 +100,7 @@ __global__ __launch_bounds__(kThreads) void norm_affine_quant_kernel(NormArgs a)
   const int lane_in_row = (wave % WPR) * 64 + lane;
   const int nchunks = a.width >> 3;
   const int64_t step = (int64_t)gridDim.x * kRowsPerBlock;
+  auto chunk_ok = [&](int j) { return FULL || lane_in_row + j * 64 * WPR < nchunks; };
 
   // one read of a row (zeros past the last row) and its table index
   auto load_row = [&](int64_t row, u32x4 (&c)[CH], int64_t &g) {
@@ -108,7 +111,7 @@ __global__ __launch_bounds__(kThreads) void norm_affine_quant_kernel(NormArgs a)
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
       const int ci = lane_in_row + j * 64 * WPR;
-      c[j] = (ok && ci < nchunks) ? *reinterpret_cast<const u32x4 *>(xr + (int64_t)ci * 16) : u32x4{0, 0, 0, 0};
+      c[j] = (ok && chunk_ok(j)) ? *reinterpret_cast<const u32x4 *>(xr + (int64_t)ci * 16) : u32x4{0, 0, 0, 0};
     }
     g = ok ? a.indices[s] : 0;
   };
@@ -125,8 +128,9 @@ __global__ __launch_bounds__(kThreads) void norm_affine_quant_kernel(NormArgs a)
     load_row(row + step, cn, gn);
     const bool g_ok = g >= 0 && g < a.table_rows;
 
-    // statistics (fp32, two passes over registers)
-    float rstd, mean = 0.0f;
+    // statistics (fp32, two passes over the packed row; chunks past the row's
+    // end are zeros and must stay out of the variance)
+    float rstd, nmr = 0.0f;  // n = x * rstd + nmr
     if constexpr (NORM == XGEN_NORM_LAYER) {
       float acc = 0.0f;
 #pragma unroll
@@ -136,12 +140,11 @@ __global__ __launch_bounds__(kThreads) void norm_affine_quant_kernel(NormArgs a)
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc += v[i];
       }
-      mean = row_sum<WPR>(acc, wave, lane, red_f) / (float)a.width;
+      const float mean = row_sum<WPR>(acc, wave, lane, red_f) / (float)a.width;
       float acc2 = 0.0f;
 #pragma unroll
       for (int j = 0; j < CH; ++j) {
-        const int ci = lane_in_row + j * 64 * WPR;
-        if (ci < nchunks) {
+        if (chunk_ok(j)) {
           float v[8];
           unpack8<XGEN_DTYPE_BF16>(c[j], v);
 #pragma unroll
@@ -153,6 +156,7 @@ __global__ __launch_bounds__(kThreads) void norm_affine_quant_kernel(NormArgs a)
       }
       const float var = row_sum<WPR>(acc2, wave, lane, red_f) / (float)a.width;
       rstd = 1.0f / __builtin_sqrtf(var + a.eps);
+      nmr = -mean * rstd;
     } else {
       float acc2 = 0.0f;
 #pragma unroll
@@ -166,66 +170,80 @@ __global__ __launch_bounds__(kThreads) void norm_affine_quant_kernel(NormArgs a)
       rstd = 1.0f / __builtin_sqrtf(ms + a.eps);
     }
 
-    // normalise, modulate with the table row, keep m as packed bf16 (in c)
-    const uint8_t *sr = a.scale_tab + (g_ok ? g : 0) * a.scale_stride_bytes;
-    const uint8_t *tr = a.shift_tab + (g_ok ? g : 0) * a.shift_stride_bytes;
+    // normalise, modulate with the table row, keep m as packed bf16 (in c);
+    // bf16 roundings two at a time (one conversion per pair)
     u16x2 am = {0, 0};
+    if (row_ok && g_ok) {  // uniform over the wave (one row per wave)
+      const uint8_t *sr = a.scale_tab + g * a.scale_stride_bytes;
+      const uint8_t *tr = a.shift_tab + g * a.shift_stride_bytes;
 #pragma unroll
-    for (int j = 0; j < CH; ++j) {
-      const int ci = lane_in_row + j * 64 * WPR;
-      if (row_ok && g_ok && ci < nchunks) {
-        float v[8], sc[8], sh[8];
-        unpack8<XGEN_DTYPE_BF16>(c[j], v);
-        unpack8<XGEN_DTYPE_BF16>(*reinterpret_cast<const u32x4 *>(sr + (int64_t)ci * 16), sc);
-        unpack8<XGEN_DTYPE_BF16>(*reinterpret_cast<const u32x4 *>(tr + (int64_t)ci * 16), sh);
-        float n[8];
+      for (int j = 0; j < CH; ++j) {
+        const int ci = lane_in_row + j * 64 * WPR;
+        if (chunk_ok(j)) {
+          const u32x4 scw = *reinterpret_cast<const u32x4 *>(sr + (int64_t)ci * 16);
+          const u32x4 shw = *reinterpret_cast<const u32x4 *>(tr + (int64_t)ci * 16);
+          float n[8];
+          unpack8<XGEN_DTYPE_BF16>(c[j], n);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) n[i] = (NORM == XGEN_NORM_LAYER) ? (v[i] - mean) * rstd : v[i] * rstd;
-        if (a.weight_dtype != XGEN_DTYPE_NONE) {
-          float wv[8];
-          load_weight8(a.weight, a.weight_dtype, ci, wv);
+          for (int i = 0; i < 8; ++i) n[i] = __builtin_fmaf(n[i], rstd, nmr);
+          if (a.weight_dtype != XGEN_DTYPE_NONE) {
+            float wv[8];
+            load_weight8(a.weight, a.weight_dtype, ci, wv);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) n[i] *= wv[i];
+            for (int i = 0; i < 8; ++i) n[i] *= wv[i];
+          }
+          const uint32_t scp[4] = {scw.x, scw.y, scw.z, scw.w}, shp[4] = {shw.x, shw.y, shw.z, shw.w};
+          uint32_t pk[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float n0 = n[2 * i], n1 = n[2 * i + 1];
+            round_bf16x2(n0, n1);
+            float f0 = 1.0f + Half2<XGEN_DTYPE_BF16>::lo(scp[i]), f1 = 1.0f + Half2<XGEN_DTYPE_BF16>::hi(scp[i]);
+            round_bf16x2(f0, f1);
+            float p0 = n0 * f0, p1 = n1 * f1;
+            round_bf16x2(p0, p1);
+            pk[i] = pack_bf16x2(p0 + Half2<XGEN_DTYPE_BF16>::lo(shp[i]), p1 + Half2<XGEN_DTYPE_BF16>::hi(shp[i]));
+          }
+          c[j] = u32x4{pk[0], pk[1], pk[2], pk[3]};
+          am = absmax_chunk<XGEN_DTYPE_BF16>(c[j], am);
+        } else {
+          c[j] = u32x4{0, 0, 0, 0};
         }
-        uint32_t pk[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float n0 = round_bf16(n[2 * i]), n1 = round_bf16(n[2 * i + 1]);
-          const float f0 = round_bf16(1.0f + sc[2 * i]), f1 = round_bf16(1.0f + sc[2 * i + 1]);
-          const float p0 = round_bf16(n0 * f0), p1 = round_bf16(n1 * f1);
-          pk[i] = pack_bf16x2(p0 + sh[2 * i], p1 + sh[2 * i + 1]);
-        }
-        c[j] = u32x4{pk[0], pk[1], pk[2], pk[3]};
-        am = absmax_chunk<XGEN_DTYPE_BF16>(c[j], am);
-      } else {
-        c[j] = u32x4{0, 0, 0, 0};
       }
     }
     const uint32_t amax_bits = row_max_u32<WPR>(hmax_u16x2(am), wave, lane, red_u);
 
     // quantize from registers
     if (row_ok) {
+      uint8_t *qr = a.q + row * (int64_t)a.width;
       const float amax = Half2<XGEN_DTYPE_BF16>::from_absbits(amax_bits);
       const RowQuant p = (OUT == XGEN_DTYPE_E4M3) ? fp8_row_params(amax) : i8_row_params(amax);
-      uint8_t *qr = a.q + row * (int64_t)a.width;
-      uint8_t *nr = a.normed ? a.normed + row * (int64_t)a.width * 2 : nullptr;
+      if (g_ok) {
+        uint8_t *nr = a.normed ? a.normed + row * (int64_t)a.width * 2 : nullptr;
 #pragma unroll
-      for (int j = 0; j < CH; ++j) {
-        const int ci = lane_in_row + j * 64 * WPR;
-        if (ci < nchunks) {
-          u32x2 out;
-          if (g_ok) {
+        for (int j = 0; j < CH; ++j) {
+          const int ci = lane_in_row + j * 64 * WPR;
+          if (chunk_ok(j)) {
             float v[8];
             unpack8<XGEN_DTYPE_BF16>(c[j], v);
-            out = quant8<OUT>(v, p);
-          } else {
-            out = (OUT == XGEN_DTYPE_E4M3) ? u32x2{0x7f7f7f7fu, 0x7f7f7f7fu} : u32x2{0u, 0u};
+            *reinterpret_cast<u32x2 *>(qr + (int64_t)ci * 8) = quant8<OUT>(c[j], v, p);
+            if (nr) *reinterpret_cast<u32x4 *>(nr + (int64_t)ci * 16) = c[j];
           }
-          *reinterpret_cast<u32x2 *>(qr + (int64_t)ci * 8) = out;
-          if (nr) *reinterpret_cast<u32x4 *>(nr + (int64_t)ci * 16) = c[j];
         }
+        if (lane_in_row == 0) a.token_scale[row] = p.s;
+      } else {  // index outside the table: a poisoned row (NaN scale; NaN bytes or zeros)
+        const u32x2 bad = (OUT == XGEN_DTYPE_E4M3) ? u32x2{0x7f7f7f7fu, 0x7f7f7f7fu} : u32x2{0u, 0u};
+        uint8_t *nr = a.normed ? a.normed + row * (int64_t)a.width * 2 : nullptr;
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+          const int ci = lane_in_row + j * 64 * WPR;
+          if (chunk_ok(j)) {
+            *reinterpret_cast<u32x2 *>(qr + (int64_t)ci * 8) = bad;
+            if (nr) *reinterpret_cast<u32x4 *>(nr + (int64_t)ci * 16) = u32x4{0, 0, 0, 0};
+          }
+        }
+        if (lane_in_row == 0) a.token_scale[row] = __builtin_nanf("");
       }
-      if (lane_in_row == 0) a.token_scale[row] = g_ok ? p.s : __builtin_nanf("");
     }
 #pragma unroll
     for (int j = 0; j < CH; ++j) c[j] = cn[j];
@@ -233,24 +251,34 @@ __global__ __launch_bounds__(kThreads) void norm_affine_quant_kernel(NormArgs a)
   }
 }
 
-template <int NORM, int OUT, int WPR, int CH>
-void launch(const NormArgs &a, hipStream_t stream) {
+template <int NORM, int OUT, int WPR, int CH, bool FULL>
+void launch_kernel(const NormArgs &a, hipStream_t stream) {
   constexpr int kRowsPerBlock = 4 / WPR;
-  static const int per_cu = resident_blocks_per_cu(norm_affine_quant_kernel<NORM, OUT, WPR, CH>, kThreads);
+  static const int per_cu = resident_blocks_per_cu(norm_affine_quant_kernel<NORM, OUT, WPR, CH, FULL>, kThreads);
   const int64_t need = (a.rows + kRowsPerBlock - 1) / kRowsPerBlock;
   const int64_t cap = (int64_t)device_cu_count() * per_cu;
-  norm_affine_quant_kernel<NORM, OUT, WPR, CH><<<dim3((unsigned)(need < cap ? need : cap)), dim3(kThreads), 0, stream>>>(a);
+  norm_affine_quant_kernel<NORM, OUT, WPR, CH, FULL>
+      <<<dim3((unsigned)(need < cap ? need : cap)), dim3(kThreads), 0, stream>>>(a);
 }
 
+template <int NORM, int OUT, int WPR, int CH>
+void launch(const NormArgs &a, hipStream_t stream) {
+  if (a.width == 512 * WPR * CH) launch_kernel<NORM, OUT, WPR, CH, true>(a, stream);
+  else launch_kernel<NORM, OUT, WPR, CH, false>(a, stream);
+}
+
+// Waves per row and chunks per lane by width: at most 4 chunks (32 values) per
+// lane keeps a wave's registers at occupancy >= 3; the row's reductions are
+// DPP shuffles plus one LDS exchange between the row's waves.
 template <int NORM, int OUT>
 void dispatch_width(const NormArgs &a, hipStream_t stream) {
   const int w = a.width;
   if (w <= 1024) launch<NORM, OUT, 1, 2>(a, stream);
-  else if (w <= 2048) launch<NORM, OUT, 1, 4>(a, stream);
-  else if (w <= 3072) launch<NORM, OUT, 1, 6>(a, stream);
-  else if (w <= 4096) launch<NORM, OUT, 1, 8>(a, stream);
-  else if (w <= 6144) launch<NORM, OUT, 2, 6>(a, stream);
-  else launch<NORM, OUT, 2, 8>(a, stream);
+  else if (w <= 2048) launch<NORM, OUT, 2, 2>(a, stream);
+  else if (w <= 3072) launch<NORM, OUT, 2, 3>(a, stream);
+  else if (w <= 4096) launch<NORM, OUT, 2, 4>(a, stream);
+  else if (w <= 6144) launch<NORM, OUT, 4, 3>(a, stream);
+  else launch<NORM, OUT, 4, 4>(a, stream);
 }
 
 }  // namespace

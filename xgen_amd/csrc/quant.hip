@@ -80,7 +80,7 @@ __global__ __launch_bounds__(kThreads) void quant_rows_vec_kernel(
         if (ci < nchunks) {
           float v[8];
           unpack8<DT>(c[j], v);
-          *reinterpret_cast<u32x2 *>(qr + (int64_t)ci * 8) = quant8<OUT>(v, p);
+          *reinterpret_cast<u32x2 *>(qr + (int64_t)ci * 8) = quant8<OUT>(c[j], v, p);
         }
       }
       if (lane_in_row == 0) scale[row] = p.s;
@@ -146,19 +146,21 @@ int quantize_rows_typed(const void *x, int64_t rows, int64_t cols, int64_t ldx, 
                         int64_t ldq, float *scale, hipStream_t stream) {
   const bool vec = (cols % 8 == 0) && (ldx % 8 == 0) && (ldq % 8 == 0) && aligned16(x) &&
                    ((reinterpret_cast<uintptr_t>(q) & 7u) == 0);
-  // Smallest (waves per row, chunks per lane) that covers the row.
+  // (waves per row, chunks per lane) covering the row with at most 4 chunks
+  // (32 values) per lane where 4 waves suffice (register budget of the
+  // streaming kernel, which holds the current and the next row).
   if (vec && cols <= 512 * 2) {
     launch_vec<DT, OUT, 1, 2>(x, rows, cols, ldx, q, ldq, scale, stream);
   } else if (vec && cols <= 512 * 4) {
     launch_vec<DT, OUT, 1, 4>(x, rows, cols, ldx, q, ldq, scale, stream);
-  } else if (vec && cols <= 512 * 6) {
-    launch_vec<DT, OUT, 1, 6>(x, rows, cols, ldx, q, ldq, scale, stream);
-  } else if (vec && cols <= 512 * 8) {
-    launch_vec<DT, OUT, 1, 8>(x, rows, cols, ldx, q, ldq, scale, stream);
-  } else if (vec && cols <= 1024 * 6) {
-    launch_vec<DT, OUT, 2, 6>(x, rows, cols, ldx, q, ldq, scale, stream);
-  } else if (vec && cols <= 1024 * 8) {
-    launch_vec<DT, OUT, 2, 8>(x, rows, cols, ldx, q, ldq, scale, stream);
+  } else if (vec && cols <= 1024 * 3) {
+    launch_vec<DT, OUT, 2, 3>(x, rows, cols, ldx, q, ldq, scale, stream);
+  } else if (vec && cols <= 1024 * 4) {
+    launch_vec<DT, OUT, 2, 4>(x, rows, cols, ldx, q, ldq, scale, stream);
+  } else if (vec && cols <= 2048 * 3) {
+    launch_vec<DT, OUT, 4, 3>(x, rows, cols, ldx, q, ldq, scale, stream);
+  } else if (vec && cols <= 2048 * 4) {
+    launch_vec<DT, OUT, 4, 4>(x, rows, cols, ldx, q, ldq, scale, stream);
   } else if (vec && cols <= 2048 * 6) {
     launch_vec<DT, OUT, 4, 6>(x, rows, cols, ldx, q, ldq, scale, stream);
   } else if (vec && cols <= 2048 * 8) {
@@ -245,7 +247,7 @@ __global__ __launch_bounds__(kThreads) void fp8_pack_kernel(const uint8_t *__res
     const u32x4 c = *reinterpret_cast<const u32x4 *>(x + ci * 16);
     float v[8];
     unpack8<DT>(c, v);
-    *reinterpret_cast<u32x2 *>(q + ci * 8) = quant8<XGEN_DTYPE_E4M3>(v, p);
+    *reinterpret_cast<u32x2 *>(q + ci * 8) = quant8<XGEN_DTYPE_E4M3>(c, v, p);
   }
   if (blockIdx.x == 0) {
     const uint16_t *xs = reinterpret_cast<const uint16_t *>(x);

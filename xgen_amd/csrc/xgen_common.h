@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "xgen_amd.h"
 
 namespace xgen {
@@ -103,6 +105,13 @@ __device__ __forceinline__ float round_bf16(float x) {
   return __uint_as_float(pack_bf16x2(x, 0.0f) << 16);
 }
 
+// Rounds two floats to bf16 (RNE) with one conversion.
+__device__ __forceinline__ void round_bf16x2(float &a, float &b) {
+  const uint32_t w = pack_bf16x2(a, b);
+  a = __uint_as_float(w << 16);
+  b = __uint_as_float(w & 0xffff0000u);
+}
+
 // --- OCP e4m3fn packing -----------------------------------------------------
 // v_cvt_pk_fp8_f32 rounds to nearest even into e4m3fn (gfx950: OCP format).
 // Inputs here are always finite and within [-448, 448].
@@ -130,6 +139,21 @@ __device__ __forceinline__ float div_by_scale(float x, float s, float r) {
   return __builtin_copysignf(__builtin_fmaf(e, r, q0), x);
 }
 
+// The same division of a magnitude a >= 0 (result >= 0).  With round-to-
+// nearest-even each step commutes with negation, so div_by_scale(x) ==
+// copysign(div_by_scale_abs(|x|), x) bit for bit.
+__device__ __forceinline__ float div_by_scale_abs(float a, float s, float r) {
+  float q0 = a * r;
+  float e = __builtin_fmaf(-q0, s, a);
+  return __builtin_fmaf(e, r, q0);
+}
+
+// Sign bits of four 16-bit floats (bf16 or f16: bit 15 of each half of w0, w1)
+// placed at bit 7 of bytes 0..3: v_perm_b32 picks bytes 1, 3 of w0 and 1, 3 of w1.
+__device__ __forceinline__ uint32_t sign_bytes4(uint32_t w0, uint32_t w1) {
+  return __builtin_amdgcn_perm(w1, w0, 0x07050301u) & 0x80808080u;
+}
+
 // INT8 lane value: rint_half_even(x * alpha) as a byte.
 __device__ __forceinline__ uint32_t q_i8(float x, float alpha) {
   float y = __builtin_rintf(x * alpha);
@@ -140,18 +164,38 @@ __device__ __forceinline__ uint32_t pack_i8x4(float a, float b, float c, float d
 }
 
 // --- wave64 reductions ---------------------------------------------------------
+// Wave64 reductions with DPP lane shuffles (no LDS round trips): quad
+// permutes [1,0,3,2] and [2,3,0,1], half-row and row mirrors give every lane
+// its 16-lane row's result; row_bcast15 / row_bcast31 (gfx9) fold rows 0-1
+// into 1 and 0-2 into 3; lane 63 then holds the wave's result, read back as a
+// wave-uniform value.
+constexpr int kDppQuad1032 = 0xB1, kDppQuad2301 = 0x4E, kDppRowMirror = 0x140, kDppRowHalfMirror = 0x141,
+              kDppRowBcast15 = 0x142, kDppRowBcast31 = 0x143;
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t old, uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, ROW_MASK, 0xf, false);
+}
+__device__ __forceinline__ uint32_t max_u32(uint32_t a, uint32_t b) { return a > b ? a : b; }
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    uint32_t o = __shfl_xor(v, off, 64);
-    v = v > o ? v : o;
-  }
-  return v;
+  v = max_u32(v, dpp_u32<kDppQuad1032>(0, v));
+  v = max_u32(v, dpp_u32<kDppQuad2301>(0, v));
+  v = max_u32(v, dpp_u32<kDppRowHalfMirror>(0, v));
+  v = max_u32(v, dpp_u32<kDppRowMirror>(0, v));
+  v = max_u32(v, dpp_u32<kDppRowBcast15, 0xa>(0, v));
+  v = max_u32(v, dpp_u32<kDppRowBcast31, 0xc>(0, v));
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 __device__ __forceinline__ float wave_sum_f32(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+  auto sh = [](float x, auto ctrl_tag) {
+    return __uint_as_float(dpp_u32<decltype(ctrl_tag)::value>(0, __float_as_uint(x)));
+  };
+  v += sh(v, std::integral_constant<int, kDppQuad1032>{});
+  v += sh(v, std::integral_constant<int, kDppQuad2301>{});
+  v += sh(v, std::integral_constant<int, kDppRowHalfMirror>{});
+  v += sh(v, std::integral_constant<int, kDppRowMirror>{});
+  v += __uint_as_float(dpp_u32<kDppRowBcast15, 0xa>(0, __float_as_uint(v)));
+  v += __uint_as_float(dpp_u32<kDppRowBcast31, 0xc>(0, __float_as_uint(v)));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 // NaN results are stored as the canonical quiet NaN 0x7fc00000 (division
@@ -205,17 +249,21 @@ __device__ __forceinline__ uint32_t e4m3_slow_byte(float x, float s) {
   return pack_e4m3x4(clamp448(v), 0.0f, 0.0f, 0.0f) & 0xffu;
 }
 
-// Quantizes 8 fp32 values (one 16-byte input chunk) into 8 bytes.
+// Quantizes one 16-byte chunk c of 8 bf16/f16 values (v = the same values as
+// fp32) into 8 bytes.  E4M3: the magnitude is divided and clamped to 448 and
+// the sign bit is copied from the 16-bit input (so -0 and negative values that
+// round to zero keep their sign, as IEEE x / s does).
 template <int OUT>
-__device__ __forceinline__ u32x2 quant8(const float (&v)[8], const RowQuant &p) {
+__device__ __forceinline__ u32x2 quant8(const u32x4 &c, const float (&v)[8], const RowQuant &p) {
   u32x2 r;
   if constexpr (OUT == XGEN_DTYPE_E4M3) {
     if (p.finite) {
       float q[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) q[i] = clamp448(div_by_scale(v[i], p.s, p.mul));
-      r.x = pack_e4m3x4(q[0], q[1], q[2], q[3]);
-      r.y = pack_e4m3x4(q[4], q[5], q[6], q[7]);
+      for (int i = 0; i < 8; ++i)
+        q[i] = __builtin_fminf(div_by_scale_abs(__builtin_fabsf(v[i]), p.s, p.mul), kE4M3Max);
+      r.x = pack_e4m3x4(q[0], q[1], q[2], q[3]) | sign_bytes4(c.x, c.y);
+      r.y = pack_e4m3x4(q[4], q[5], q[6], q[7]) | sign_bytes4(c.z, c.w);
     } else {
       uint32_t b[8];
 #pragma unroll
