@@ -274,6 +274,28 @@ def main():
         kernels["gemm_int8_qkv"] = {"ms": ms_i8, "tops": flop / (ms_i8 * 1e-3) / 1e12,
                                     "frac_of_peak": flop / (ms_i8 * 1e-3) / 1e12 / PEAK_INT8_TOPS}
 
+    # ---- gated residual: standalone (HBM) and fused into the out-projection's epilogue
+    if want("gate"):
+        wo, bo = W.weight("out", g, dev)
+        qo, so = xops.quantize_rows(wo, fp8)
+        res = torch.randn((1, M, K), generator=g, device=dev).to(torch.bfloat16)
+        gt = (torch.randn((20, K), generator=g, device=dev) * 0.1).to(torch.bfloat16)
+        gi = torch.randint(20, (M,), generator=g, device=dev)
+        yb = torch.randn((1, M, K), generator=g, device=dev).to(torch.bfloat16)
+        gate_bytes = 3 * M * K * 2
+        ms_gate = timed(lambda: xops.gate_residual(res, yb, gt, gi), args.steps, args.warmup)
+        ms_fused = timed(lambda: xops.scaled_mm_gate_residual(qa0, qo, sa0, so, bo, res[0], gt, gi), args.steps,
+                         args.warmup)
+        ms_plain = timed(lambda: xops.scaled_mm(qa0, qo, sa0, so, bo, torch.bfloat16, N.ACT_NONE, False),
+                         args.steps, args.warmup)
+        f_out = 2.0 * M * K * K
+        kernels["gate_residual_op"] = {"ms": ms_gate, "gbs": gate_bytes / (ms_gate * 1e-3) / 1e9,
+                                       "frac_of_hbm": gate_bytes / (ms_gate * 1e-3) / 1e9 / PEAK_HBM_GBS}
+        kernels["out_proj_gate_residual_fused"] = {
+            "ms": ms_fused, "tflops": f_out / (ms_fused * 1e-3) / 1e12,
+            "unfused_ms": ms_plain + ms_gate, "gemm_alone_ms": ms_plain}
+        del wo, qo, res, yb
+
     # ---- C5 chain at a 10 s clip's share (M=31,248): front end -> QKV -> out -> up(+GELU) -> down
     if want("c5"):
         from xgen_amd.operator.dit_chain import DiTLinearChain

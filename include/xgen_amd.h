@@ -171,6 +171,45 @@ int xgen_quant_matmul_int8(const void *a, int64_t lda, const void *w, int64_t ld
                            int activation, void *out, int out_dtype, int64_t ldo,
                            int32_t *acc_out, hipStream_t stream);
 
+/*
+ * Gated residual with an indexed gate table
+ * (torch.ops.h3_phaa_gate_residual.gate_residual,
+ *  x_base/x_base/operator/npu_fusion/f2a/op_extension/gate_residual_queued.asc:33-35, kernel
+ *  f2a/op_kernel/gate_residual_kernel.asc:57-67; eager form x_base/x_base/operator/h3_indexed_affine.py:47):
+ *   out[b,s,c] = bf16(residual[b,s,c] + bf16(branch[b,s,c] * gate_table[indices[s], c]))
+ * multiply, round, add, round (no fused multiply-add).  residual / branch: BF16
+ * [batch, seq, width] with the given batch / seq strides (elements, last stride
+ * 1); gate_table BF16 [gate_rows, width], rows gate_row_stride apart; indices
+ * int64 [seq]; out BF16 [batch, seq, width] contiguous.  An index outside
+ * [0, gate_rows) writes a NaN row.  width and strides multiples of 8 elements.
+ */
+int xgen_gate_residual(const void *residual, int64_t res_stride_batch, int64_t res_stride_seq,
+                       const void *branch, int64_t br_stride_batch, int64_t br_stride_seq,
+                       const void *gate_table, int64_t gate_row_stride, int64_t gate_rows,
+                       const int64_t *indices, int64_t batch, int64_t seq, int64_t width, void *out,
+                       hipStream_t stream);
+
+/*
+ * W8A8 GEMM whose bf16 output feeds the gated residual in the same epilogue:
+ * the out-projection / FFN-down of a DiT block followed by
+ * `residual + gate[idx] * y` (x_base/x_base/operator/h3_indexed_affine.py:58-61;
+ * x_diffusers/x_diffusers/framework/transformer/hunyuan.py:387,400):
+ *   y[m,n]   = bf16(acc * (a_scale[m*a_scale_stride] * w_scale[n*w_scale_stride]) + bias[n])
+ *              (xgen_scaled_mm_fp8 for in_dtype E4M3, xgen_quant_matmul_int8 for I8)
+ *   out[m,n] = bf16(residual[m,n] + bf16(y[m,n] * gate_table[indices[m % seq], n]))
+ * residual BF16 [M, N] (leading dimension ld_residual); gate_table BF16
+ * [gate_rows, N] rows gate_row_stride apart; indices int64 [seq] with M a
+ * multiple of seq; out BF16 [M, N] (ldo).  Equal bit for bit to
+ * xgen_scaled_mm_fp8 / xgen_quant_matmul_int8 (BF16 out) followed by
+ * xgen_gate_residual.  Operand requirements as those entry points.
+ */
+int xgen_w8a8_gate_residual(int in_dtype, const void *a, int64_t lda, const void *w, int64_t ldw,
+                            int64_t M, int64_t N, int64_t K, const float *a_scale, int64_t a_scale_stride,
+                            const float *w_scale, int64_t w_scale_stride, const void *bias, int bias_dtype,
+                            const void *residual, int64_t ld_residual, const void *gate_table,
+                            int64_t gate_row_stride, int64_t gate_rows, const int64_t *indices, int64_t seq,
+                            void *out, int64_t ldo, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

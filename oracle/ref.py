@@ -208,6 +208,25 @@ def norm_affine_quant(x, weight, scale_tab, shift_tab, indices, eps, norm="layer
     return q, s, m
 
 
+def gate_residual(residual, branch, gate_table, indices):
+    """Gated residual out = bf16(residual + bf16(branch * gate[g])) with g = indices[r % S] for row
+    r = b*S + s (npu_fusion/f2a/op_kernel/gate_residual_kernel.asc:57-67: multiply, round, add, round,
+    no FMA; the eager form `residual + gate.index_select(0, indices) * x` of
+    x_base/x_base/operator/h3_indexed_affine.py:47 and tests/test_h3_indexed_affine.py:21-22).
+    [B, S, H] bf16 in and out."""
+    r = residual.detach().cpu()
+    b = branch.detach().cpu()
+    g = gate_table.detach().cpu().index_select(0, indices.detach().cpu().long())
+    return r + g[None] * b
+
+
+def gate_residual_np(residual: np.ndarray, branch: np.ndarray, gate_rows: np.ndarray) -> np.ndarray:
+    """The same with explicit RNE bf16 rounding after each fp32 operation (float32 arrays of
+    bf16 values in, float32 array of bf16 values out); gate_rows already indexed [.., S, H]."""
+    prod = round_bf16_np(branch.astype(np.float32) * gate_rows.astype(np.float32))
+    return round_bf16_np(residual.astype(np.float32) + prod)
+
+
 def gelu_tanh_bf16(y: torch.Tensor) -> torch.Tensor:
     """diffusers GELU(approximate='tanh') on a bf16 tensor (hunyuan.py:358)."""
     return F.gelu(y.detach().cpu(), approximate="tanh")

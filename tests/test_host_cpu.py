@@ -134,3 +134,29 @@ def test_scaled_mm_meta():
 
 def test_meta_checks_leave_device_uninitialized():
     assert not torch.cuda.is_initialized()
+
+
+def test_gate_residual_meta():
+    m = torch.device("meta")
+    r = torch.empty(2, 5, 64, dtype=torch.bfloat16, device=m)
+    g = torch.empty(3, 64, dtype=torch.bfloat16, device=m)
+    i = torch.empty(5, dtype=torch.int64, device=m)
+    out = xops.gate_residual(r, r, g, i)
+    assert out.shape == (2, 5, 64) and out.dtype == torch.bfloat16
+    with pytest.raises(RuntimeError):
+        xops.gate_residual(r, r, g[:, :32], i)
+    with pytest.raises(RuntimeError):
+        xops.gate_residual(r, r, g, i.to(torch.int32))
+
+
+def test_scaled_mm_gate_residual_meta():
+    m = torch.device("meta")
+    a = torch.empty(10, 64, dtype=torch.float8_e4m3fn, device=m)
+    w = torch.empty(32, 64, dtype=torch.float8_e4m3fn, device=m)
+    sa, sw = torch.empty(10, device=m), torch.empty(32, device=m)
+    res = torch.empty(10, 32, dtype=torch.bfloat16, device=m)
+    g = torch.empty(4, 32, dtype=torch.bfloat16, device=m)
+    out = xops.scaled_mm_gate_residual(a, w, sa, sw, None, res, g, torch.empty(5, dtype=torch.int64, device=m))
+    assert out.shape == (10, 32) and out.dtype == torch.bfloat16
+    with pytest.raises(RuntimeError):   # M not a multiple of S
+        xops.scaled_mm_gate_residual(a, w, sa, sw, None, res, g, torch.empty(3, dtype=torch.int64, device=m))

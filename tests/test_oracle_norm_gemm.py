@@ -146,3 +146,20 @@ def test_cpu_fake_quant_path_equals_oracle_linear():
     a = R.cpu_fake_quant_linear_fp8(x, qw, sw, b)
     ref = R.w8a8_linear_fp8(qa, sa, qw, sw, b)
     assert R.rel_l2(a, ref) < 1e-2 and R.cosine(a, ref) > 0.9999
+
+
+def test_gate_residual_eager_equals_explicit_rounding():
+    """The reference's bitwise check of its gated residual against eager bf16
+    (x_base/tests/test_h3_indexed_affine.py:21-22): multiply, round, add, round."""
+    g = torch.Generator().manual_seed(42)
+    x = torch.randn((2, 37, 128), generator=g, dtype=torch.bfloat16)
+    residual = torch.randn(x.shape, generator=g, dtype=torch.bfloat16)
+    tables = torch.randn((7, 6 * 128), generator=g, dtype=torch.bfloat16)
+    _, _, gate, *_ = tables.chunk(6, dim=-1)
+    idx = torch.randint(7, (37,), generator=g)
+    eager = R.gate_residual(residual, x, gate, idx)
+    explicit = R.gate_residual_np(R.bf16_to_np(residual), R.bf16_to_np(x), R.bf16_to_np(gate.index_select(0, idx))[None])
+    assert np.array_equal(eager.float().numpy().view(np.uint32), explicit.view(np.uint32))
+    # and it is not the fused multiply-add: some elements differ from a single rounding
+    fused = (residual.float() + gate.index_select(0, idx).float()[None] * x.float()).to(torch.bfloat16)
+    assert not torch.equal(fused, eager)

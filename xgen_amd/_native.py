@@ -58,6 +58,12 @@ SIGNATURES = {
     "xgen_quant_matmul_int8": (_c_int, [
         _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64,
         _c_ptr, _c_int, _c_int, _c_ptr, _c_int, _c_i64, _c_ptr, _c_ptr]),
+    "xgen_gate_residual": (_c_int, [
+        _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64,
+        _c_ptr, _c_ptr]),
+    "xgen_w8a8_gate_residual": (_c_int, [
+        _c_int, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64,
+        _c_ptr, _c_int, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr]),
 }
 
 

@@ -62,6 +62,14 @@ struct GemmArgs {
   void *acc_out;
   int tiles_m, tiles_n, per_xcd;
   uint32_t a_bytes, w_bytes;
+  // gated residual epilogue (GATED kernels only)
+  const uint8_t *residual;
+  int64_t ld_residual;  // elements
+  const uint8_t *gate;
+  int64_t gate_stride;  // elements
+  int64_t gate_rows;
+  const int64_t *indices;
+  uint32_t seq;
 };
 
 // LDS layout of one operand tile of one stage: 256 rows x 64 bytes (4 chunks
@@ -204,7 +212,8 @@ constexpr int kParamSetBytes = 4 * kParamBytes;
 constexpr int kParamSets = kStages + 1;
 constexpr int kLdsBytes = kStages * kStageBytes + kParamSets * kParamSetBytes;
 
-template <bool FP8, int ACT, int OUT_DT, bool ACC_OUT, int WM, int WN>
+// GATED: the bf16 output y feeds out = bf16(residual + bf16(y * gate[indices[m % seq]])).
+template <bool FP8, int ACT, int OUT_DT, bool ACC_OUT, int WM, int WN, bool GATED = false>
 __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) {
   typedef Mfma<FP8> T;
   constexpr int kWaves = WM * WN;
@@ -470,8 +479,19 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) 
         if (sw4 & 1) v = u32x4{v.z, v.w, v.x, v.y};
         const int m = m0 + wm * (BM / WM) + j * 32 + row;
         const int n = n0 + wn * (BN / WN) + c16 * 8;
-        if (m < p.M && n < p.N)
+        if (m < p.M && n < p.N) {
+          if constexpr (GATED) {
+            const int64_t gi = p.indices[(uint32_t)m % p.seq];
+            if (gi >= 0 && gi < p.gate_rows) {
+              const u32x4 r = *reinterpret_cast<const u32x4 *>(p.residual + ((int64_t)m * p.ld_residual + n) * 2);
+              const u32x4 t = *reinterpret_cast<const u32x4 *>(p.gate + (gi * p.gate_stride + n) * 2);
+              v = gate_residual8(r, v, t);
+            } else {
+              v = u32x4{0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};  // index outside the table: NaN
+            }
+          }
           *reinterpret_cast<u32x4 *>(static_cast<uint16_t *>(p.out) + (int64_t)m * p.ldo + n) = v;
+        }
       }
     }
 #pragma unroll
@@ -507,24 +527,45 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) 
   wait_vmcnt<0>();
 }
 
-template <bool FP8, int ACT, int OUT_DT>
-void launch_gemm(const GemmArgs &a, bool acc_out, hipStream_t stream) {
-  // one persistent workgroup per CU (a multiple of the 8 XCDs), never more than the tiles need
+// one persistent workgroup per CU (a multiple of the 8 XCDs), never more than the tiles need
+dim3 gemm_grid(const GemmArgs &a) {
   const int ntiles = a.tiles_m * a.tiles_n;
   int wgs = device_cu_count() / 8 * 8;
   const int need = ((ntiles + 7) / 8) * 8;
   if (wgs > need) wgs = need;
   if (wgs < 8) wgs = 8;
-  const dim3 grid((unsigned)wgs), block(64 * kWavesM * kWavesN);
+  return dim3((unsigned)wgs);
+}
+
+template <bool FP8, int ACT, int OUT_DT>
+void launch_gemm(const GemmArgs &a, bool acc_out, hipStream_t stream) {
+  const dim3 grid = gemm_grid(a), block(64 * kWavesM * kWavesN);
   if (acc_out) gemm_w8a8_kernel<FP8, ACT, OUT_DT, true, kWavesM, kWavesN><<<grid, block, 0, stream>>>(a);
   else gemm_w8a8_kernel<FP8, ACT, OUT_DT, false, kWavesM, kWavesN><<<grid, block, 0, stream>>>(a);
 }
 
 template <bool FP8>
+void launch_gemm_gated(const GemmArgs &a, hipStream_t stream) {
+  gemm_w8a8_kernel<FP8, XGEN_ACT_NONE, XGEN_DTYPE_BF16, false, kWavesM, kWavesN, true>
+      <<<gemm_grid(a), dim3(64 * kWavesM * kWavesN), 0, stream>>>(a);
+}
+
+struct GateParams {  // the gated residual epilogue's inputs (null residual: plain GEMM)
+  const void *residual = nullptr;
+  int64_t ld_residual = 0;
+  const void *gate = nullptr;
+  int64_t gate_stride = 0, gate_rows = 0;
+  const int64_t *indices = nullptr;
+  int64_t seq = 0;
+};
+
+template <bool FP8>
 int gemm_entry(const char *fn, const void *a, int64_t lda, const void *w, int64_t ldw, int64_t M,
                int64_t N, int64_t K, const float *sa, int64_t sa_stride, const float *sw,
                int64_t sw_stride, const void *bias, int bias_dtype, int activation, void *out,
-               int out_dtype, int64_t ldo, void *acc_out, hipStream_t stream) {
+               int out_dtype, int64_t ldo, void *acc_out, hipStream_t stream,
+               const GateParams &gp = GateParams()) {
+  const bool gated = gp.residual != nullptr;
   if (M < 0 || N <= 0 || K <= 0)
     return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: bad shape M=%lld N=%lld K=%lld", fn, (long long)M,
                 (long long)N, (long long)K);
@@ -548,6 +589,14 @@ int gemm_entry(const char *fn, const void *a, int64_t lda, const void *w, int64_
   if ((bias && !aligned16(bias)) || (sw_stride && !aligned16(sw)) || (sa_stride && !aligned16(sa)) ||
       (acc_out && !aligned16(acc_out)))
     return fail(XGEN_ERR_UNSUPPORTED, "%s: scale, bias and accumulator buffers must be 16-byte aligned", fn);
+  if (gated) {
+    if (!gp.gate || !gp.indices) return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+    if (gp.seq <= 0 || M % gp.seq || gp.gate_rows <= 0 || gp.ld_residual < N || gp.gate_stride < N)
+      return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: bad gated residual shape (M %% seq, gate rows, strides)", fn);
+    if (gp.ld_residual % 8 || gp.gate_stride % 8 || !aligned16(gp.residual) || !aligned16(gp.gate))
+      return fail(XGEN_ERR_UNSUPPORTED, "%s: residual and gate rows must be 16-byte aligned", fn);
+    if (M >= 0x7fffffffLL) return fail(XGEN_ERR_UNSUPPORTED, "%s: too many rows", fn);
+  }
   const int64_t a_bytes = (M - 1) * lda + K, w_bytes = (N - 1) * ldw + K;
   if (a_bytes >= (int64_t)kOutOfRange || w_bytes >= (int64_t)kOutOfRange)
     return fail(XGEN_ERR_UNSUPPORTED, "%s: operands above 2 GiB", fn);
@@ -574,8 +623,17 @@ int gemm_entry(const char *fn, const void *a, int64_t lda, const void *w, int64_
   g.per_xcd = (g.tiles_m * g.tiles_n + 7) / 8;
   g.a_bytes = (uint32_t)a_bytes;
   g.w_bytes = (uint32_t)w_bytes;
+  g.residual = static_cast<const uint8_t *>(gp.residual);
+  g.ld_residual = gp.ld_residual;
+  g.gate = static_cast<const uint8_t *>(gp.gate);
+  g.gate_stride = gp.gate_stride;
+  g.gate_rows = gp.gate_rows;
+  g.indices = gp.indices;
+  g.seq = (uint32_t)gp.seq;
   const bool with_acc = acc_out != nullptr;
-  if (activation == XGEN_ACT_NONE) {
+  if (gated) {
+    launch_gemm_gated<FP8>(g, stream);
+  } else if (activation == XGEN_ACT_NONE) {
     if (out_dtype == XGEN_DTYPE_BF16) launch_gemm<FP8, XGEN_ACT_NONE, XGEN_DTYPE_BF16>(g, with_acc, stream);
     else launch_gemm<FP8, XGEN_ACT_NONE, XGEN_DTYPE_F16>(g, with_acc, stream);
   } else {
@@ -610,4 +668,30 @@ extern "C" int xgen_quant_matmul_int8(const void *a, int64_t lda, const void *w,
   return gemm_entry<false>("xgen_quant_matmul_int8", a, lda, w, ldw, M, N, K, pertoken_scale,
                            pertoken_scale_stride, w_scale, w_scale_stride, bias, bias_dtype,
                            activation, out, out_dtype, ldo, acc_out, stream);
+}
+
+extern "C" int xgen_w8a8_gate_residual(int in_dtype, const void *a, int64_t lda, const void *w, int64_t ldw,
+                                       int64_t M, int64_t N, int64_t K, const float *a_scale,
+                                       int64_t a_scale_stride, const float *w_scale, int64_t w_scale_stride,
+                                       const void *bias, int bias_dtype, const void *residual,
+                                       int64_t ld_residual, const void *gate_table, int64_t gate_row_stride,
+                                       int64_t gate_rows, const int64_t *indices, int64_t seq, void *out,
+                                       int64_t ldo, hipStream_t stream) {
+  const char *fn = "xgen_w8a8_gate_residual";
+  if (in_dtype != XGEN_DTYPE_E4M3 && in_dtype != XGEN_DTYPE_I8)
+    return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: operand dtype must be E4M3 or I8", fn);
+  if (M > 0 && !residual) return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+  GateParams gp;
+  gp.residual = residual;
+  gp.ld_residual = ld_residual;
+  gp.gate = gate_table;
+  gp.gate_stride = gate_row_stride;
+  gp.gate_rows = gate_rows;
+  gp.indices = indices;
+  gp.seq = seq;
+  if (in_dtype == XGEN_DTYPE_E4M3)
+    return gemm_entry<true>(fn, a, lda, w, ldw, M, N, K, a_scale, a_scale_stride, w_scale, w_scale_stride, bias,
+                            bias_dtype, XGEN_ACT_NONE, out, XGEN_DTYPE_BF16, ldo, nullptr, stream, gp);
+  return gemm_entry<false>(fn, a, lda, w, ldw, M, N, K, a_scale, a_scale_stride, w_scale, w_scale_stride, bias,
+                           bias_dtype, XGEN_ACT_NONE, out, XGEN_DTYPE_BF16, ldo, nullptr, stream, gp);
 }

@@ -105,11 +105,29 @@ __device__ __forceinline__ float round_bf16(float x) {
   return __uint_as_float(pack_bf16x2(x, 0.0f) << 16);
 }
 
+// Gated residual of one 16-byte chunk (8 bf16 values each of residual r,
+// branch y and gate t): bf16(r + bf16(y * t)), multiply, round, add, round.
+__device__ __forceinline__ void round_bf16x2(float &a, float &b);
+__device__ __forceinline__ u32x4 gate_residual8(const u32x4 &r, const u32x4 &y, const u32x4 &t);
+
 // Rounds two floats to bf16 (RNE) with one conversion.
 __device__ __forceinline__ void round_bf16x2(float &a, float &b) {
   const uint32_t w = pack_bf16x2(a, b);
   a = __uint_as_float(w << 16);
   b = __uint_as_float(w & 0xffff0000u);
+}
+
+__device__ __forceinline__ u32x4 gate_residual8(const u32x4 &r, const u32x4 &y, const u32x4 &t) {
+  const uint32_t rw[4] = {r.x, r.y, r.z, r.w}, yw[4] = {y.x, y.y, y.z, y.w}, tw[4] = {t.x, t.y, t.z, t.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float p0 = __uint_as_float(yw[i] << 16) * __uint_as_float(tw[i] << 16);
+    float p1 = __uint_as_float(yw[i] & 0xffff0000u) * __uint_as_float(tw[i] & 0xffff0000u);
+    round_bf16x2(p0, p1);
+    o[i] = pack_bf16x2(__uint_as_float(rw[i] << 16) + p0, __uint_as_float(rw[i] & 0xffff0000u) + p1);
+  }
+  return u32x4{o[0], o[1], o[2], o[3]};
 }
 
 // --- OCP e4m3fn packing -----------------------------------------------------

@@ -112,6 +112,21 @@ class H3FP8Linear(nn.Module):
         self.calls += 1
         return out
 
+    def forward_gate_residual(self, x, residual, gate_table, indices):
+        """`residual + bf16(gate_table[indices] * self(x))` with the gated residual in the GEMM's
+        epilogue (the out-projection / FFN-down of a DiT block followed by
+        x_base/x_base/operator/h3_indexed_affine.py:58-61).  x: bf16/fp16 [B, S, K]; residual bf16
+        [B, S, N]; gate_table bf16 [T, N]; indices int64 [S].  Per-token activation scaling only."""
+        if self.activation_scaling != "token" or _ACTIVATIONS[self.activation] != N.ACT_NONE:
+            raise ValueError("forward_gate_residual needs activation_scaling='token' and no activation")
+        if x.dim() != 3 or residual.shape != (*x.shape[:-1], self.out_features):
+            raise ValueError("forward_gate_residual: x [B,S,K] and residual [B,S,N] required")
+        packed, scale = self.quantize_input(x.reshape(-1, x.shape[-1]))
+        out = xops.scaled_mm_gate_residual(packed, self.weight, scale, self.weight_scale.reshape(-1), self.bias,
+                                           residual.reshape(-1, self.out_features), gate_table, indices)
+        self.calls += 1
+        return out.reshape(residual.shape)
+
     def _local_forward(self, x, bias):
         if not x.is_cuda or x.dtype not in (torch.bfloat16, torch.float16):
             raise ValueError("H3 FP8 Linear requires CUDA BF16/FP16 input")

@@ -62,6 +62,20 @@ class WeightQuantLinearModule(nn.Module):
         out = quant_matmul_raw(x_int8, pertoken_scale, self, ori_dtype)
         return out.reshape(*ori_shape[:-1], -1)
 
+    def forward_gate_residual(self, x, residual, gate_table, indices):
+        """`residual + bf16(gate_table[indices] * self(x))` with the gated residual in the INT8 GEMM's
+        epilogue (x_base/x_base/operator/npu_fusion/gate_residual.py:9-14 after npu_quant_matmul).
+        x: [B, S, K]; residual bf16 [B, S, N]; gate_table bf16 [T, N]; indices int64 [S]."""
+        if x.dim() != 3 or residual.shape != (*x.shape[:-1], self.weight.shape[0]):
+            raise ValueError("forward_gate_residual: x [B,S,K] and residual [B,S,N] required")
+        m = x.reshape(-1, x.shape[-1])
+        if m.dtype == torch.float32:
+            m = m.to(torch.bfloat16)
+        q, s = dynamic_quant(m)
+        out = xops.scaled_mm_gate_residual(q, self.weight, s.reshape(-1), self.antiquant_scale.reshape(-1), self.bias,
+                                           residual.reshape(-1, residual.shape[-1]), gate_table, indices)
+        return out.reshape(residual.shape)
+
 
 def quant_matmul_raw(q, scale, linear, out_dtype=torch.bfloat16, activation=N.ACT_NONE):
     """int8 GEMM of a pre-quantized activation against a WeightQuantLinearModule."""

@@ -28,6 +28,10 @@ SCHEMAS = {
     "scaled_mm": (
         "scaled_mm(Tensor a, Tensor w, Tensor a_scale, Tensor w_scale, Tensor? bias, "
         "ScalarType out_dtype, int activation, bool return_acc) -> (Tensor, Tensor)"),
+    "gate_residual": "gate_residual(Tensor residual, Tensor branch, Tensor gate_table, Tensor indices) -> Tensor",
+    "scaled_mm_gate_residual": (
+        "scaled_mm_gate_residual(Tensor a, Tensor w, Tensor a_scale, Tensor w_scale, Tensor? bias, "
+        "Tensor residual, Tensor gate_table, Tensor indices) -> Tensor"),
 }
 
 
@@ -117,6 +121,37 @@ def _mm_meta(a, w, a_scale, w_scale, bias, out_dtype, activation, return_acc):
     acc_dtype = torch.float32 if a.dtype == torch.float8_e4m3fn else torch.int32
     acc = torch.empty((M, Nf) if return_acc else (0,), dtype=acc_dtype, device=a.device)
     return torch.empty((M, Nf), dtype=out_dtype, device=a.device), acc
+
+
+def _gate_check(residual, branch, gate_table, indices, what="gate_residual"):
+    _require(residual.dim() == 3 and branch.shape == residual.shape and residual.shape[2] > 0,
+             f"{what}: residual/branch [B,S,H] shapes must match")
+    _require(gate_table.dim() == 2 and gate_table.shape[0] > 0 and gate_table.shape[1] == residual.shape[2],
+             f"{what}: gate_table [T,H] required")
+    _require(indices.dim() == 1 and indices.shape[0] == residual.shape[1] and indices.dtype == torch.int64,
+             f"{what}: int64 indices [S] required")
+    _require(residual.dtype == branch.dtype == gate_table.dtype == torch.bfloat16, f"{what}: BF16 inputs required")
+
+
+def _gate_meta(residual, branch, gate_table, indices):
+    _gate_check(residual, branch, gate_table, indices)
+    return torch.empty(residual.shape, dtype=torch.bfloat16, device=residual.device)
+
+
+def _mm_gate_check(a, w, a_scale, w_scale, bias, residual, gate_table, indices):
+    _mm_check(a, w, a_scale, w_scale, bias, torch.bfloat16, N.ACT_NONE)
+    M, Nf = a.shape[0], w.shape[0]
+    _require(residual.dim() == 2 and tuple(residual.shape) == (M, Nf) and residual.dtype == torch.bfloat16,
+             "scaled_mm_gate_residual: residual BF16 [M, N] required")
+    _require(gate_table.dim() == 2 and gate_table.shape[1] == Nf and gate_table.shape[0] > 0
+             and gate_table.dtype == torch.bfloat16, "scaled_mm_gate_residual: gate_table BF16 [T, N] required")
+    _require(indices.dim() == 1 and indices.dtype == torch.int64 and indices.shape[0] > 0
+             and M % indices.shape[0] == 0, "scaled_mm_gate_residual: int64 indices [S] with M % S == 0 required")
+
+
+def _mm_gate_meta(a, w, a_scale, w_scale, bias, residual, gate_table, indices):
+    _mm_gate_check(a, w, a_scale, w_scale, bias, residual, gate_table, indices)
+    return torch.empty((a.shape[0], w.shape[0]), dtype=torch.bfloat16, device=a.device)
 
 
 # --------------------------------------------------------------------------- device
@@ -214,6 +249,48 @@ def _mm_gpu(a, w, a_scale, w_scale, bias, out_dtype, activation, return_acc):
     return out, acc
 
 
+def _gate_gpu(residual, branch, gate_table, indices):
+    _on_gpu(residual, branch, gate_table, indices)
+    out = _gate_meta(residual, branch, gate_table, indices)
+    if out.numel() == 0:
+        return out
+    residual = residual if residual.stride(2) == 1 else residual.contiguous()
+    branch = branch if branch.stride(2) == 1 else branch.contiguous()
+    gate_table = gate_table if gate_table.stride(1) == 1 else gate_table.contiguous()
+    indices = indices.contiguous()
+    B, S, H = residual.shape
+    st = N.lib().xgen_gate_residual(
+        residual.data_ptr(), residual.stride(0), residual.stride(1), branch.data_ptr(), branch.stride(0),
+        branch.stride(1), gate_table.data_ptr(), gate_table.stride(0), gate_table.shape[0], indices.data_ptr(),
+        B, S, H, out.data_ptr(), N.stream_of(residual))
+    N.check(st, "xgen_gate_residual")
+    return out
+
+
+def _mm_gate_gpu(a, w, a_scale, w_scale, bias, residual, gate_table, indices):
+    _on_gpu(a, w, a_scale, w_scale, bias, residual, gate_table, indices)
+    out = _mm_gate_meta(a, w, a_scale, w_scale, bias, residual, gate_table, indices)
+    M, K = a.shape
+    Nf = w.shape[0]
+    if M == 0:
+        return out
+    a = a if a.stride(1) == 1 else a.contiguous()
+    w = w if w.stride(1) == 1 else w.contiguous()
+    a_scale, w_scale = a_scale.contiguous(), w_scale.contiguous()
+    bias = None if bias is None else bias.contiguous()
+    residual = residual if residual.stride(1) == 1 else residual.contiguous()
+    gate_table = gate_table if gate_table.stride(1) == 1 else gate_table.contiguous()
+    indices = indices.contiguous()
+    st = N.lib().xgen_w8a8_gate_residual(
+        N.dtype_code(a.dtype), a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0), M, Nf, K, a_scale.data_ptr(),
+        1 if a_scale.numel() == M and M > 1 else 0, w_scale.data_ptr(), 1 if w_scale.numel() == Nf and Nf > 1 else 0,
+        N.ptr(bias), N.DTYPE_NONE if bias is None else N.dtype_code(bias.dtype), residual.data_ptr(),
+        residual.stride(0), gate_table.data_ptr(), gate_table.stride(0), gate_table.shape[0], indices.data_ptr(),
+        indices.shape[0], out.data_ptr(), out.stride(0), N.stream_of(a))
+    N.check(st, "xgen_w8a8_gate_residual")
+    return out
+
+
 _IMPLS = {
     "quantize_rows": (_quantize_rows_gpu, _quantize_rows_meta),
     "abs_peak": (_peak_gpu, _peak_meta),
@@ -221,6 +298,8 @@ _IMPLS = {
     "fp8_pack": (_pack_gpu, _pack_meta),
     "norm_affine_quant": (_norm_gpu, _norm_meta),
     "scaled_mm": (_mm_gpu, _mm_meta),
+    "gate_residual": (_gate_gpu, _gate_meta),
+    "scaled_mm_gate_residual": (_mm_gate_gpu, _mm_gate_meta),
 }
 
 
