@@ -296,6 +296,17 @@ def main():
             "unfused_ms": ms_plain + ms_gate, "gemm_alone_ms": ms_plain}
         del wo, qo, res, yb
 
+    # ---- H3 FFN activation: SwiGLU + per-token INT8 / FP8 requant at F = 14,336 (u is 896 MB)
+    if want("swiglu"):
+        F3 = 14336
+        u3 = torch.randn((1, M, 2 * F3), generator=g, device=dev).to(torch.bfloat16)
+        sw_bytes = M * 2 * F3 * 2 + M * F3 + 4 * M
+        for name, dt in (("swiglu_quant_int8_h3", torch.int8), ("swiglu_quant_fp8_h3", fp8)):
+            ms_sw = timed(lambda: xops.swiglu_quant(u3, False, dt, 1, False), args.steps, args.warmup)
+            kernels[name] = {"ms": ms_sw, "gbs": sw_bytes / (ms_sw * 1e-3) / 1e9,
+                             "frac_of_hbm": sw_bytes / (ms_sw * 1e-3) / 1e9 / PEAK_HBM_GBS, "bytes": sw_bytes}
+        del u3
+
     # ---- C5 chain at a 10 s clip's share (M=31,248): front end -> QKV -> out -> up(+GELU) -> down
     if want("c5"):
         from xgen_amd.operator.dit_chain import DiTLinearChain

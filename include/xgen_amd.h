@@ -44,6 +44,9 @@ extern "C" {
 #define XGEN_DTYPE_I32 5
 #define XGEN_DTYPE_NONE (-1)
 
+/* widest SwiGLU half (F) of xgen_swiglu_quant: H3's F = 14,336 fits */
+#define XGEN_SWIGLU_MAX_HALF 16384
+
 /* normalisation kinds for xgen_norm_affine_quant */
 #define XGEN_NORM_LAYER 0 /* (x - mean) * rsqrt(var + eps), biased variance */
 #define XGEN_NORM_RMS 1   /* x * rsqrt(mean(x^2) + eps) */
@@ -209,6 +212,24 @@ int xgen_w8a8_gate_residual(int in_dtype, const void *a, int64_t lda, const void
                             const void *residual, int64_t ld_residual, const void *gate_table,
                             int64_t gate_row_stride, int64_t gate_rows, const int64_t *indices, int64_t seq,
                             void *out, int64_t ldo, hipStream_t stream);
+
+/*
+ * SwiGLU + per-row quantization (the H3 FFN's activation and the requant before
+ * its down-projection; torch.ops.h3_phaa_fusion_quant_reuse.swiglu_quantize,
+ * x_base/x_base/operator/npu_fusion/f1b/op_extension/swiglu_quant_reuse_queued.asc:33-35,
+ * kernel f1b/op_kernel/swiglu_quant_reuse_kernel.asc:36-105; gate-first layout of
+ * x_base/x_base/operator/h3_swiglu.py:15-29):
+ *   u: BF16 [batch, seq, 2F], row (b, s) at u + b*u_stride_batch + s*u_stride_seq (elements);
+ *      gate_first 0: [hidden | gate] (the NPU kernel), 1: [gate | hidden] (h3_swiglu.py)
+ *   a = bf16(silu(gate)) with silu(g) = g / (1 + exp(-g)); v = bf16(hidden * a)
+ *   q, scale = per-row quantization of v: E4M3 as xgen_quantize_rows, or I8 with
+ *   scale_mode 1: scale = amax * fl(1/127), 0: scale = 1 / fl(127/amax).
+ * q: [batch*seq, F] contiguous; scale float32 [batch*seq]; act_out NULL or BF16
+ * [batch*seq, F] receiving v.  F <= XGEN_SWIGLU_MAX_HALF, F and strides multiples of 8.
+ */
+int xgen_swiglu_quant(const void *u, int64_t batch, int64_t seq, int64_t half_width, int64_t u_stride_batch,
+                      int64_t u_stride_seq, int gate_first, int out_dtype, int scale_mode, void *q, float *scale,
+                      void *act_out, hipStream_t stream);
 
 #ifdef __cplusplus
 }

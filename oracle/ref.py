@@ -227,6 +227,30 @@ def gate_residual_np(residual: np.ndarray, branch: np.ndarray, gate_rows: np.nda
     return round_bf16_np(residual.astype(np.float32) + prod)
 
 
+def swiglu_quant(u, gate_first=False, out="int8", scale_mode=1):
+    """SwiGLU + per-row quantization (npu_fusion/f1b/op_kernel/swiglu_quant_reuse_kernel.asc:36-105;
+    gate-first layout of x_base/x_base/operator/h3_swiglu.py:15-29): u bf16 [B, S, 2F] split into
+    hidden | gate (gate | hidden when gate_first); a = bf16(gate / (1 + exp(-gate))) (IEEE division,
+    h3_swiglu.py:22), v = bf16(hidden * a) (kernel :48-55), then the row quantizer of v: FP8 as
+    quantize_rows_fp8, INT8 as quantize_rows_int8 with scale_mode 1 (amax * fl(1/127)) or 0
+    (1 / fl(127/amax)) (kernel :80-89).  Returns (q [B*S, F], scale [B*S], v [B*S, F])."""
+    t = u.detach().cpu()
+    F = t.shape[-1] // 2
+    first, second = t[..., :F].float(), t[..., F:].float()
+    gate, hidden = (first, second) if gate_first else (second, first)
+    a = (gate / (1.0 + torch.exp(-gate))).to(torch.bfloat16).float()
+    v = (hidden * a).to(torch.bfloat16).reshape(-1, F)
+    if out == "fp8":
+        q, s = quantize_rows_fp8(v)
+    else:
+        q, s = quantize_rows_int8(v)
+        if scale_mode == 0:
+            amax = v.float().abs().amax(dim=-1)
+            alpha = torch.tensor(127.0, dtype=torch.float32) / amax
+            s = torch.tensor(1.0, dtype=torch.float32) / alpha
+    return q, s, v
+
+
 def gelu_tanh_bf16(y: torch.Tensor) -> torch.Tensor:
     """diffusers GELU(approximate='tanh') on a bf16 tensor (hunyuan.py:358)."""
     return F.gelu(y.detach().cpu(), approximate="tanh")

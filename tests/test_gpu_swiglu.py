@@ -1,0 +1,83 @@
+"""GPU parity of the fused SwiGLU + per-row quantization (H3's FFN activation
+and requant).  Contract (exp and the row reductions are not bit-reproducible
+across libraries): the bf16 activation v is >= 99.9% bit-identical to the
+oracle's and elsewhere within 1 bf16 ulp; quantized bytes and scales are
+bit-exact given the kernel's own v (returned with return_act)."""
+import pytest
+import torch
+
+import oracle.ref as R
+import xgen_amd  # noqa: F401
+from xgen_amd.operator.matmul import WeightQuantLinearModule
+from xgen_amd.operator.swiglu_quant import swiglu_quant, swiglu_quantize_reuse
+
+pytestmark = pytest.mark.gpu
+xops = torch.ops.xgen_amd
+
+
+def u_input(B, S, F, seed, dev):
+    g = torch.Generator().manual_seed(seed)
+    u = (torch.randn((B, S, 2 * F), generator=g) * 2).to(torch.bfloat16)
+    u[..., 5] = (u[..., 5].float() * 40).to(torch.bfloat16)
+    return u.to(dev)
+
+
+def check(u, gate_first, out, scale_mode, q, s, v):
+    qr, sr, vr = R.swiglu_quant(u, gate_first, "fp8" if out == torch.float8_e4m3fn else "int8", scale_mode)
+    ulps = R.bf16_ulp_diff(v.cpu(), vr)
+    assert (ulps == 0).float().mean() >= 0.999 and ulps.max() <= 1
+    if out == torch.float8_e4m3fn:
+        q2, s2 = R.quantize_rows_fp8(v.cpu())
+        assert torch.equal(q.cpu().view(torch.uint8), q2.view(torch.uint8))
+    else:
+        q2, s2 = R.quantize_rows_int8(v.cpu())
+        assert torch.equal(q.cpu(), q2)
+        if scale_mode == 0:
+            amax = v.cpu().float().abs().amax(dim=-1)
+            s2 = torch.tensor(1.0) / (torch.tensor(127.0) / amax)
+    assert torch.equal(s.cpu().view(torch.int32), s2.view(torch.int32))
+
+
+@pytest.mark.parametrize("gate_first", [False, True])
+@pytest.mark.parametrize("out", [torch.float8_e4m3fn, torch.int8])
+@pytest.mark.parametrize("B,S,F", [(2, 37, 128), (1, 300, 3072), (3, 5, 1000), (1, 20, 14336), (1, 9, 16384)])
+def test_matches_oracle(cuda, gate_first, out, B, S, F):
+    u = u_input(B, S, F, seed=F + S, dev=cuda)
+    q, s, v = swiglu_quant(u, gate_first=gate_first, out_dtype=out, return_act=True)
+    assert q.shape == (B * S, F) and s.shape == (B * S,)
+    check(u, gate_first, out, 1, q, s, v)
+
+
+def test_scale_mode_zero_and_strided_rows(cuda):
+    big = u_input(2, 11, 512, seed=4, dev=cuda)
+    u = big[..., 128:128 + 2 * 192]      # row stride 1024, F = 192
+    q, s, v = swiglu_quant(u, scale_mode=0, return_act=True)
+    check(u, False, torch.int8, 0, q, s, v)
+
+
+def test_reference_surface(cuda):
+    u = u_input(1, 8, 256, seed=5, dev=cuda)
+    q, s = swiglu_quantize_reuse(u)
+    assert q.dtype == torch.int8 and q.shape == (8, 256) and s.shape == (8,)
+    with pytest.raises(ValueError):
+        swiglu_quantize_reuse(u.float().requires_grad_().to(torch.bfloat16))
+    with pytest.raises(RuntimeError):
+        swiglu_quantize_reuse(u, tile=5376)
+    with pytest.raises(RuntimeError):
+        swiglu_quantize_reuse(u[..., :255])
+
+
+def test_h3_ffn_int8(cuda):
+    """H3 geometry at reduced M: up [2F, d] -> SwiGLU + INT8 requant -> down [d, F] (h3_npu_fusion.py:33-54)."""
+    g = torch.Generator().manual_seed(6)
+    M, d, F = 96, 5376, 14336
+    x = torch.randn((1, M, d), generator=g).to(torch.bfloat16).to(cuda)
+    wu = (torch.randn((2 * F, d), generator=g) * 0.02).to(torch.bfloat16)
+    wd = (torch.randn((d, F), generator=g) * 0.02).to(torch.bfloat16)
+    up, down = WeightQuantLinearModule(wu, None), WeightQuantLinearModule(wd, None)
+    u = up(x)
+    q, s = swiglu_quantize_reuse(u)
+    y, _ = xops.scaled_mm(q, down.weight, s, down.antiquant_scale, None, torch.bfloat16, 0, False)
+    qr, sr, _ = R.swiglu_quant(u, False, "int8", 1)
+    yr = R.w8a8_linear_int8(qr, sr, down.weight.cpu(), down.antiquant_scale.cpu(), None)
+    assert R.rel_l2(y, yr) <= 1e-2 and R.cosine(y, yr) >= 0.9999

@@ -163,3 +163,32 @@ def test_gate_residual_eager_equals_explicit_rounding():
     # and it is not the fused multiply-add: some elements differ from a single rounding
     fused = (residual.float() + gate.index_select(0, idx).float()[None] * x.float()).to(torch.bfloat16)
     assert not torch.equal(fused, eager)
+
+
+def test_swiglu_oracle_layouts_scale_modes_and_closed_form():
+    g = torch.Generator().manual_seed(8)
+    F = 64
+    u = (torch.randn((2, 9, 2 * F), generator=g) * 3).to(torch.bfloat16)
+    q1, s1, v1 = R.swiglu_quant(u, gate_first=False, out="int8", scale_mode=1)
+    # layout: [hidden | gate] vs [gate | hidden] are the same op on swapped halves
+    swapped = torch.cat([u[..., F:], u[..., :F]], dim=-1)
+    _, _, v2 = R.swiglu_quant(swapped, gate_first=True)
+    assert torch.equal(v1, v2)
+    # a = bf16(silu(gate)) against the float64 closed form; v = bf16(hidden * a)
+    hidden, gate = u[..., :F].double(), u[..., F:].double()
+    a64 = (gate / (1 + torch.exp(-gate))).float().to(torch.bfloat16).double()
+    v64 = (hidden * a64).float().to(torch.bfloat16)
+    assert (v64.reshape(-1, F) == v1).float().mean() >= 0.999
+    # eager torch (the reference's fallback `hidden * F.silu(gate)` in bf16)
+    eager = (u[..., :F] * torch.nn.functional.silu(u[..., F:])).reshape(-1, F)
+    assert (eager == v1).float().mean() >= 0.999
+    # scale modes: amax * fl(1/127) vs 1 / fl(127 / amax), same bytes
+    q0, s0, _ = R.swiglu_quant(u, scale_mode=0)
+    assert torch.equal(q0, q1)
+    amax = v1.float().abs().amax(dim=-1)
+    assert torch.equal(s1, amax * (torch.tensor(1.0) / 127.0))
+    assert torch.equal(s0, torch.tensor(1.0) / (torch.tensor(127.0) / amax))
+    # FP8 form: the row quantizer of v
+    qf, sf, _ = R.swiglu_quant(u, out="fp8")
+    qr, sr = R.quantize_rows_fp8(v1)
+    assert torch.equal(qf.view(torch.uint8), qr.view(torch.uint8)) and torch.equal(sf, sr)

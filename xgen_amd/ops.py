@@ -29,6 +29,9 @@ SCHEMAS = {
         "scaled_mm(Tensor a, Tensor w, Tensor a_scale, Tensor w_scale, Tensor? bias, "
         "ScalarType out_dtype, int activation, bool return_acc) -> (Tensor, Tensor)"),
     "gate_residual": "gate_residual(Tensor residual, Tensor branch, Tensor gate_table, Tensor indices) -> Tensor",
+    "swiglu_quant": (
+        "swiglu_quant(Tensor u, bool gate_first, ScalarType out_dtype, int scale_mode, bool return_act) "
+        "-> (Tensor, Tensor, Tensor)"),
     "scaled_mm_gate_residual": (
         "scaled_mm_gate_residual(Tensor a, Tensor w, Tensor a_scale, Tensor w_scale, Tensor? bias, "
         "Tensor residual, Tensor gate_table, Tensor indices) -> Tensor"),
@@ -136,6 +139,22 @@ def _gate_check(residual, branch, gate_table, indices, what="gate_residual"):
 def _gate_meta(residual, branch, gate_table, indices):
     _gate_check(residual, branch, gate_table, indices)
     return torch.empty(residual.shape, dtype=torch.bfloat16, device=residual.device)
+
+
+SWIGLU_MAX_HALF = 16384
+
+
+def _swiglu_meta(u, gate_first, out_dtype, scale_mode, return_act):
+    _require(u.dim() == 3 and u.shape[2] > 0 and u.shape[2] % 2 == 0 and u.shape[2] <= 2 * SWIGLU_MAX_HALF,
+             f"swiglu_quant: [B,S,2F], 1<=F<={SWIGLU_MAX_HALF} required")
+    _require(u.dtype == torch.bfloat16, "swiglu_quant: BF16 input required")
+    _require(out_dtype in (torch.float8_e4m3fn, torch.int8), "swiglu_quant: out_dtype must be float8_e4m3fn or int8")
+    _require(scale_mode in (0, 1), "swiglu_quant: scale_mode must be 0 or 1")
+    rows, F = u.shape[0] * u.shape[1], u.shape[2] // 2
+    q = torch.empty((rows, F), dtype=out_dtype, device=u.device)
+    s = torch.empty((rows,), dtype=torch.float32, device=u.device)
+    act = torch.empty((rows, F) if return_act else (0,), dtype=torch.bfloat16, device=u.device)
+    return q, s, act
 
 
 def _mm_gate_check(a, w, a_scale, w_scale, bias, residual, gate_table, indices):
@@ -267,6 +286,20 @@ def _gate_gpu(residual, branch, gate_table, indices):
     return out
 
 
+def _swiglu_gpu(u, gate_first, out_dtype, scale_mode, return_act):
+    _on_gpu(u)
+    q, s, act = _swiglu_meta(u, gate_first, out_dtype, scale_mode, return_act)
+    if q.numel() == 0:
+        return q, s, act
+    u = u if u.stride(2) == 1 else u.contiguous()
+    st = N.lib().xgen_swiglu_quant(
+        u.data_ptr(), u.shape[0], u.shape[1], u.shape[2] // 2, u.stride(0), u.stride(1), int(bool(gate_first)),
+        N.dtype_code(out_dtype), scale_mode, q.data_ptr(), s.data_ptr(), act.data_ptr() if return_act else None,
+        N.stream_of(u))
+    N.check(st, "xgen_swiglu_quant")
+    return q, s, act
+
+
 def _mm_gate_gpu(a, w, a_scale, w_scale, bias, residual, gate_table, indices):
     _on_gpu(a, w, a_scale, w_scale, bias, residual, gate_table, indices)
     out = _mm_gate_meta(a, w, a_scale, w_scale, bias, residual, gate_table, indices)
@@ -299,6 +332,7 @@ _IMPLS = {
     "norm_affine_quant": (_norm_gpu, _norm_meta),
     "scaled_mm": (_mm_gpu, _mm_meta),
     "gate_residual": (_gate_gpu, _gate_meta),
+    "swiglu_quant": (_swiglu_gpu, _swiglu_meta),
     "scaled_mm_gate_residual": (_mm_gate_gpu, _mm_gate_meta),
 }
 
