@@ -53,7 +53,33 @@ def parse():
 
 
 PROFILE_KERNELS = ("gemm_fp8_qkv", "gemm_int8_qkv", "gemm_fp8_ffn_up_gelu", "gemm_fp8_ffn_down", "quant_rows_fp8",
-                   "front_end_ln_mod_quant_fp8", "copy_1gib")
+                   "front_end_ln_mod_quant_fp8", "wire_encode_h3", "wire_decode_h3", "copy_1gib")
+
+
+def wire_setup(M, g, dev):
+    """The FP8 wire codec workload: Q/K/V of two rotating fused [M, 9216] bf16 projection outputs as
+    [8 peers, M, 1, 3 heads, 128] views, one padded wire buffer, contiguous bf16 outputs.
+    Returns (encode(), decode(), bytes_encode, bytes_decode)."""
+    import torch
+    from xgen_amd import workloads as W
+    from xgen_amd.phaa import fp8_transport as T
+    fused = [torch.randn((M, 3 * W.HEADS * W.HEAD_DIM), generator=g, device=dev).to(torch.bfloat16)
+             for _ in range(2)]
+    views = [W.qkv_head_views(f) for f in fused]
+    wire, pad = T.encode_wire(views[0], W.HEAD_DIM, W.SP_PEERS, align16=True)
+    rows = M * W.HEADS
+    outs = tuple(torch.empty((rows, W.HEAD_DIM), dtype=torch.bfloat16, device=dev) for _ in range(3))
+    state = {"i": 0}
+
+    def encode():
+        state["i"] += 1
+        T.encode_wire(views[state["i"] & 1], W.HEAD_DIM, W.SP_PEERS, align16=True, out=wire)
+
+    def decode():
+        T.decode_wire(wire, outs, W.HEAD_DIM, W.SP_PEERS, pad)
+
+    values = 3 * rows * W.HEAD_DIM
+    return encode, decode, values * 2 + wire.numel(), wire.numel() + values * 2
 
 
 def profile_kernels(names, steps, warmup):
@@ -94,6 +120,10 @@ def profile_kernels(names, steps, warmup):
             fn = lambda: xops.scaled_mm(qa, qw, sa, sw, b, torch.bfloat16, act, False)  # noqa: E731
         elif name == "quant_rows_fp8":
             fn = lambda: xops.quantize_rows(nxt(), fp8)  # noqa: E731
+        elif name.startswith("wire_"):
+            enc, dec, _, _ = wire_setup(M, g, dev)
+            enc()
+            fn = enc if name == "wire_encode_h3" else dec
         elif name == "front_end_ln_mod_quant_fp8":
             shift, scale = W.adaln_tables(20, K, g, dev)
             idx = torch.randint(20, (M,), generator=g, device=dev)
@@ -306,6 +336,18 @@ def main():
             kernels[name] = {"ms": ms_sw, "gbs": sw_bytes / (ms_sw * 1e-3) / 1e9,
                              "frac_of_hbm": sw_bytes / (ms_sw * 1e-3) / 1e9 / PEAK_HBM_GBS, "bytes": sw_bytes}
         del u3
+
+    # ---- FP8 wire codec of the head-parallel attention exchange (Q/K/V at M=15,624, 24 x 128, 8 peers)
+    if want("wire"):
+        enc, dec, enc_bytes, dec_bytes = wire_setup(M, g, dev)
+        ms_enc = timed(enc, args.steps, args.warmup)
+        ms_dec = timed(dec, args.steps, args.warmup)
+        kernels["wire_encode_h3"] = {"ms": ms_enc, "gbs": enc_bytes / (ms_enc * 1e-3) / 1e9,
+                                     "frac_of_hbm": enc_bytes / (ms_enc * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                                     "bytes": enc_bytes}
+        kernels["wire_decode_h3"] = {"ms": ms_dec, "gbs": dec_bytes / (ms_dec * 1e-3) / 1e9,
+                                     "frac_of_hbm": dec_bytes / (ms_dec * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                                     "bytes": dec_bytes}
 
     # ---- C5 chain at a 10 s clip's share (M=31,248): front end -> QKV -> out -> up(+GELU) -> down
     if want("c5"):

@@ -47,6 +47,9 @@ extern "C" {
 /* widest SwiGLU half (F) of xgen_swiglu_quant: H3's F = 14,336 fits */
 #define XGEN_SWIGLU_MAX_HALF 16384
 
+/* widest row (head_dim) of the FP8 wire codec (the reference takes any multiple of 4) */
+#define XGEN_WIRE_MAX_WIDTH 1024
+
 /* normalisation kinds for xgen_norm_affine_quant */
 #define XGEN_NORM_LAYER 0 /* (x - mean) * rsqrt(var + eps), biased variance */
 #define XGEN_NORM_RMS 1   /* x * rsqrt(mean(x^2) + eps) */
@@ -230,6 +233,44 @@ int xgen_w8a8_gate_residual(int in_dtype, const void *a, int64_t lda, const void
 int xgen_swiglu_quant(const void *u, int64_t batch, int64_t seq, int64_t half_width, int64_t u_stride_batch,
                       int64_t u_stride_seq, int gate_first, int out_dtype, int scale_mode, void *q, float *scale,
                       void *act_out, hipStream_t stream);
+
+/*
+ * Per-row FP8 wire codec of the head-parallel attention exchange: the encode
+ * and decode kernels around the byte all-to-all of
+ * x_base/x_base/phaa/fp8_transport.py:26-78 (_encode / _decode, launched at
+ * :137-144 by fp8_all_to_all_many, :85).  Each row of `width` values travels as
+ * `width` e4m3fn bytes then its float32 scale (width + 4 bytes):
+ *   scale = max(max|v| / 448, 1e-12);  byte = e4m3fn(clamp(v / scale, +-448));
+ *   decoded = out_dtype(fl32(e4m3(byte) * scale)).
+ * Rows of `streams` (1, or 3 for Q/K/V) inputs of `peers * peer_rows` rows each
+ * are ordered [peer][stream][peer row]; each peer block is followed by
+ * peer_padding zero bytes.  width: multiple of 4, <= XGEN_WIRE_MAX_WIDTH;
+ * streams * peers * peer_rows < 2^31.
+ */
+
+/* Zero bytes after each peer block for the 16-byte peer alignment option
+ * (fp8_transport.py:103-105, XGEN_PHAA_FP8_ALIGN16): (-peer_bytes) mod 16 with
+ * peer_bytes = streams * peer_rows * (width + 4) when align16, else 0. */
+int64_t xgen_fp8_wire_peer_padding(int streams, int64_t peer_rows, int64_t width, int align16);
+
+/*
+ * Encode (fp8_transport.py:26-63).  in_dtype BF16, F16 or F32.  Stream s (q,
+ * then k, v when streams == 3) is a [peers, seq, batch, heads, width] view:
+ * row (p, t, b, h) starts at element p*strides[4s] + t*strides[4s+1] +
+ * b*strides[4s+2] + h*strides[4s+3] (host array of 4*streams non-negative
+ * element strides; unit last stride).  peer_rows = seq*batch*heads.  wire:
+ * peers * (streams*peer_rows*(width+4) + peer_padding) bytes, 4-byte aligned.
+ */
+int xgen_fp8_wire_encode(int in_dtype, int streams, const void *q, const void *k, const void *v,
+                         const int64_t *strides, int64_t peers, int64_t seq, int64_t batch, int64_t heads,
+                         int64_t width, int64_t peer_padding, void *wire, hipStream_t stream);
+
+/*
+ * Decode (fp8_transport.py:66-78) into contiguous [peers*peer_rows, width]
+ * outputs q (and k, v when streams == 3) of out_dtype BF16, F16 or F32.
+ */
+int xgen_fp8_wire_decode(int out_dtype, int streams, const void *wire, int64_t peers, int64_t peer_rows,
+                         int64_t width, int64_t peer_padding, void *q, void *k, void *v, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -24,6 +24,9 @@
  *                            q = fma(e, r, q0), r = 1/s, sign of x restored,
  *                            for amax >= 2^-100)
  *                            gives the same e4m3 byte as IEEE x / s.
+ *  oracle_check_wire_division   the same check for the FP8 wire codec's scale
+ *                            s = max(amax / 448, 1e-12) (phaa/fp8_transport.py:52),
+ *                            whose kernels always take the fast division.
  *
  * NaN convention: any NaN byte is written as 0x7f (canonical positive NaN).
  * Build: oracle/build.py (gcc -O2, no fast-math: float division and fmaf are
@@ -169,6 +172,31 @@ int64_t oracle_check_fast_division(int fmt, uint32_t amax_lo, uint32_t amax_hi) 
         const float x = oracle_half_to_f32(fmt, (uint16_t)(mag | sign));
         float ref = x / s;
         float got = fast ? fast_div(x, s, r) : x / s;
+        ref = ref > 448.0f ? 448.0f : (ref < -448.0f ? -448.0f : ref);
+        got = got > 448.0f ? 448.0f : (got < -448.0f ? -448.0f : got);
+        if (oracle_e4m3_encode(ref) != oracle_e4m3_encode(got)) ++bad;
+      }
+    }
+  }
+  return bad;
+}
+
+/* Wire codec scale rule: every positive finite amax bit pattern in
+ * [amax_lo, amax_hi] and every x with |x| <= amax (both signs); count of e4m3
+ * bytes that differ between IEEE x / s and the fast division. */
+int64_t oracle_check_wire_division(int fmt, uint32_t amax_lo, uint32_t amax_hi) {
+  int64_t bad = 0;
+  for (uint32_t ab = amax_lo; ab <= amax_hi; ++ab) {
+    const float amax = oracle_half_to_f32(fmt, (uint16_t)ab);
+    if (!(amax > 0.0f) || isinf(amax) || isnan(amax)) continue;
+    float s = amax / 448.0f;
+    if (s < 1.0e-12f) s = 1.0e-12f;
+    const float r = 1.0f / s;
+    for (uint32_t mag = 0; mag <= ab; ++mag) {
+      for (uint32_t sign = 0; sign <= 0x8000u; sign += 0x8000u) {
+        const float x = oracle_half_to_f32(fmt, (uint16_t)(mag | sign));
+        float ref = x / s;
+        float got = fast_div(x, s, r);
         ref = ref > 448.0f ? 448.0f : (ref < -448.0f ? -448.0f : ref);
         got = got > 448.0f ? 448.0f : (got < -448.0f ? -448.0f : got);
         if (oracle_e4m3_encode(ref) != oracle_e4m3_encode(got)) ++bad;

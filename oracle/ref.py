@@ -27,6 +27,20 @@ Function -> reference -> how it is pinned (tests/test_oracle_*.py):
   gelu_tanh           diffusers FeedForward('gelu-approximate') = F.gelu(tanh)
         (hunyuan.py:358) — parity unpinned against diffusers itself (absent);
         checked against the closed formula in float64 within 1 bf16 ulp.
+  gate_residual       gate_residual_kernel.asc:57-67 / h3_indexed_affine.py:47
+        torch bf16 expression == numpy restatement with explicit RNE after each op.
+  swiglu_quant        swiglu_quant_reuse_kernel.asc:36-105, h3_swiglu.py:15-29
+        silu against the float64 formula; quantizer halves as quantize_rows_*.
+  fp8 wire codec      phaa/fp8_transport.py:26-144 (_encode, _decode, fp8_all_to_all_many)
+        the reference's transport tests (row of head_dim + 4 bytes, padded wire ==
+        unpadded wire + zero tail, 16-byte peer blocks, cosine > 0.99:
+        test_phaa_fp8.py:59-66, test_phaa_fp8_alignment.py:47-53); block-wise layout
+        == the reference's per-row index formula (fp8_transport.py:53-63) on small
+        cases; a simulated all-to-all delivers each peer's rows; bytes and scales ==
+        quantize_rows_fp8 wherever the 1e-12 floor is inactive, closed forms at the
+        floor; decode of all 256 codes == the e4m3 table; round-trip error bound;
+        the kernels' division exhaustively at the floor (bf16).  Non-finite rows:
+        parity unpinned (the reference leaves NaN to its min/max lowering).
   fp8 / int8 GEMM     h3_fp8.py:63-66 (_scaled_mm), matmul.py:63-64 (npu_quant_matmul)
         accumulators exact (float64 BLAS of decoded operands; every partial
         sum is an exact multiple of 2^-18 below 2^35) == int64 brute force on
@@ -66,6 +80,8 @@ def clib() -> ctypes.CDLL:
         L.oracle_quant_rows_int8.argtypes = L.oracle_quant_rows_fp8.argtypes
         L.oracle_check_fast_division.restype = ctypes.c_int64
         L.oracle_check_fast_division.argtypes = [ctypes.c_int, ctypes.c_uint32, ctypes.c_uint32]
+        L.oracle_check_wire_division.restype = ctypes.c_int64
+        L.oracle_check_wire_division.argtypes = [ctypes.c_int, ctypes.c_uint32, ctypes.c_uint32]
         _C = L
     return _C
 
@@ -249,6 +265,64 @@ def swiglu_quant(u, gate_first=False, out="int8", scale_mode=1):
             alpha = torch.tensor(127.0, dtype=torch.float32) / amax
             s = torch.tensor(1.0, dtype=torch.float32) / alpha
     return q, s, v
+
+
+# ----------------------------------------------------------------------------- FP8 wire codec
+WIRE_SCALE_FLOOR = 1.0e-12  # fp8_transport.py:52 (as float32)
+
+
+def wire_peer_padding(streams: int, peer_rows: int, width: int, align16: bool) -> int:
+    """Zero bytes after each peer block (fp8_transport.py:103-105)."""
+    return (-(peer_rows * streams * (width + 4))) % 16 if align16 else 0
+
+
+def wire_rows_fp8(v: torch.Tensor):
+    """Per-row wire quantization of float32 rows [R, W] (fp8_transport.py:51-56):
+    scale = max(amax / 448, 1e-12) (NaN propagates; written as the canonical NaN),
+    bytes = e4m3fn(clamp(v / scale, +-448)) with NaN bytes as 0x7f.  Returns (uint8 [R, W], float32 [R])."""
+    amax = v.abs().amax(dim=-1)
+    scale = (amax / FP8_MAX).clamp_min(WIRE_SCALE_FLOOR)
+    scale = torch.where(torch.isnan(scale), torch.tensor(float("nan")), scale)
+    q = (v / scale[:, None]).clamp(-FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn)
+    return canonical_nan_e4m3(q).view(torch.uint8), scale
+
+
+def fp8_wire_encode(tensors, head_dim: int, peers: int, align16: bool = False) -> torch.Tensor:
+    """The send buffer of fp8_all_to_all_many (fp8_transport.py:85-140 with _encode :26-63), built
+    block-wise: stream s's rows (logical row-major order of [..., head_dim]) split into `peers`
+    equal blocks; wire = for each peer: [stream 0 block | stream 1 block | stream 2 block] of rows
+    (head_dim e4m3 bytes + little-endian float32 scale), then the peer padding of zeros.
+    Shape (peers, peer_bytes + padding) when padded, else (streams * rows, head_dim + 4)."""
+    streams, W = len(tensors), head_dim
+    rows = tensors[0].numel() // W
+    pr = rows // peers
+    blocks = []
+    for t in tensors:
+        q, s = wire_rows_fp8(t.detach().cpu().float().reshape(rows, W))
+        rec = torch.cat([q, s.contiguous().view(torch.uint8).reshape(rows, 4)], dim=1)
+        blocks.append(rec.reshape(peers, pr, W + 4))
+    per_peer = torch.stack(blocks, dim=1).reshape(peers, streams * pr * (W + 4))
+    pad = wire_peer_padding(streams, pr, W, align16)
+    if pad:
+        return torch.cat([per_peer, torch.zeros(peers, pad, dtype=torch.uint8)], dim=1)
+    return per_peer.reshape(streams * rows, W + 4)
+
+
+def fp8_wire_decode(wire: torch.Tensor, streams: int, rows: int, head_dim: int, peers: int, peer_padding: int,
+                    out_dtype=torch.bfloat16):
+    """_decode (fp8_transport.py:66-78): for each stream a [rows, head_dim] tensor of
+    out_dtype(fl32(e4m3(byte) * scale))."""
+    W = head_dim
+    pr = rows // peers
+    flat = wire.detach().cpu().reshape(peers, -1)[:, :streams * pr * (W + 4)]
+    per = flat.reshape(peers, streams, pr, W + 4)
+    out = []
+    for s in range(streams):
+        blk = per[:, s].reshape(rows, W + 4)
+        q = blk[:, :W].contiguous().view(torch.float8_e4m3fn).float()
+        sc = blk[:, W:].contiguous().view(torch.float32).reshape(rows)
+        out.append((q * sc[:, None]).to(out_dtype))
+    return out
 
 
 def gelu_tanh_bf16(y: torch.Tensor) -> torch.Tensor:

@@ -13,7 +13,7 @@ HEADER = N.Path(__file__).resolve().parents[1] / "include" / "xgen_amd.h"
 
 def declared_functions():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^(?:int|size_t|const char \*)\s*(xgen_\w+)\(", text, re.M)))
+    return sorted(set(re.findall(r"^(?:int|int64_t|size_t|const char \*)\s*(xgen_\w+)\(", text, re.M)))
 
 
 def test_header_declares_the_path():
@@ -40,6 +40,9 @@ def test_status_strings(built_library):
     assert L.xgen_status_string(N.ERR_UNSUPPORTED) == b"unsupported shape or layout"
 
 
+_STRIDES = (N._c_i64 * 12)(384, 128, 128, 128, 384, 128, 128, 128, 384, 128, 128, 128)
+
+
 @pytest.mark.parametrize("call,status,needle", [
     (lambda L: L.xgen_quantize_rows(9, 16, 4, 64, 64, N.DTYPE_E4M3, 16, 64, 16, None), N.ERR_INVALID_ARGUMENT, b"input dtype"),
     (lambda L: L.xgen_quantize_rows(N.DTYPE_BF16, 16, 4, 64, 32, N.DTYPE_E4M3, 16, 64, 16, None), N.ERR_INVALID_ARGUMENT, b"bad shape"),
@@ -63,6 +66,22 @@ def test_status_strings(built_library):
     (lambda L: L.xgen_norm_affine_quant(16, 1, 4, 64, 64, 64, N.NORM_RMS, 16, N.DTYPE_NONE, 1e-6,
                                         16, 64, 16, 64, 20, 16, N.DTYPE_E4M3, 16, 16, None, None),
      N.ERR_INVALID_ARGUMENT, b"disagree"),
+    (lambda L: L.xgen_fp8_wire_encode(N.DTYPE_BF16, 2, 16, 16, 16, _STRIDES, 2, 3, 1, 1, 128, 0, 16, None),
+     N.ERR_INVALID_ARGUMENT, b"streams"),
+    (lambda L: L.xgen_fp8_wire_encode(N.DTYPE_BF16, 1, 16, None, None, _STRIDES, 2, 3, 1, 1, 66, 0, 16, None),
+     N.ERR_INVALID_ARGUMENT, b"multiple of 4"),
+    (lambda L: L.xgen_fp8_wire_encode(N.DTYPE_I8, 1, 16, None, None, _STRIDES, 2, 3, 1, 1, 64, 0, 16, None),
+     N.ERR_INVALID_ARGUMENT, b"input dtype"),
+    (lambda L: L.xgen_fp8_wire_encode(N.DTYPE_BF16, 1, 16, None, None, _STRIDES, 2, 3, 1, 1, 64, 6, 16, None),
+     N.ERR_INVALID_ARGUMENT, b"peer_padding"),
+    (lambda L: L.xgen_fp8_wire_encode(N.DTYPE_BF16, 1, 16, None, None, _STRIDES, 2, 3, 1, 1, 2048, 0, 16, None),
+     N.ERR_UNSUPPORTED, b"exceeds"),
+    (lambda L: L.xgen_fp8_wire_encode(N.DTYPE_BF16, 1, 17, None, None, _STRIDES, 2, 3, 1, 1, 64, 0, 16, None),
+     N.ERR_UNSUPPORTED, b"element-aligned"),
+    (lambda L: L.xgen_fp8_wire_decode(N.DTYPE_BF16, 3, 16, 2, 3, 64, 0, 16, None, 16, None),
+     N.ERR_INVALID_ARGUMENT, b"null"),
+    (lambda L: L.xgen_fp8_wire_decode(N.DTYPE_BF16, 1, 16, 2, 1 << 31, 64, 0, 16, None, None, None),
+     N.ERR_UNSUPPORTED, b"2^30"),
 ])
 def test_validation_fails_before_launch(built_library, call, status, needle):
     L = N.lib()
@@ -75,4 +94,19 @@ def test_empty_inputs_are_no_ops(built_library):
     assert L.xgen_quantize_rows(N.DTYPE_BF16, None, 0, 64, 64, N.DTYPE_E4M3, None, 64, None, None) == N.OK
     assert L.xgen_scaled_mm_fp8(None, 32, None, 32, 0, 16, 32, None, 1, None, 1, None, N.DTYPE_NONE, 0,
                                 None, N.DTYPE_BF16, 16, None, None) == N.OK
+    assert L.xgen_fp8_wire_encode(N.DTYPE_BF16, 3, None, None, None, None, 2, 0, 1, 3, 128, 0, None, None) == N.OK
+    assert L.xgen_fp8_wire_decode(N.DTYPE_F32, 1, None, 4, 0, 64, 0, None, None, None, None) == N.OK
     assert L.xgen_last_error() == b""
+
+
+def test_wire_peer_padding(built_library):
+    L = N.lib()
+    # peer_bytes = streams * peer_rows * (width + 4); padding = (-peer_bytes) mod 16
+    assert L.xgen_fp8_wire_peer_padding(1, 17 * 3, 128, 1) == (-(17 * 3 * 132)) % 16 == 4
+    assert L.xgen_fp8_wire_peer_padding(3, 20 * 2 * 3, 128, 1) == 0
+    assert L.xgen_fp8_wire_peer_padding(3, 17, 128, 0) == 0
+    for streams in (1, 3):
+        for rows in range(1, 9):
+            for width in (4, 8, 64, 68, 96, 128):
+                pad = L.xgen_fp8_wire_peer_padding(streams, rows, width, 1)
+                assert pad in (0, 4, 8, 12) and (streams * rows * (width + 4) + pad) % 16 == 0

@@ -160,3 +160,39 @@ def test_scaled_mm_gate_residual_meta():
     assert out.shape == (10, 32) and out.dtype == torch.bfloat16
     with pytest.raises(RuntimeError):   # M not a multiple of S
         xops.scaled_mm_gate_residual(a, w, sa, sw, None, res, g, torch.empty(3, dtype=torch.int64, device=m))
+
+
+# --------------------------------------------------------------------------- PHAA FP8 transport (host checks)
+@pytest.mark.parametrize("device", ["cpu", "meta"])
+def test_non_cuda_transport_is_rejected_before_collective(monkeypatch, device):
+    """test_phaa_fp8_alignment.py:9-21: non-CUDA tensors raise before any collective."""
+    from unittest.mock import patch
+
+    import torch.distributed as dist
+
+    from xgen_amd.phaa import fp8_transport as transport
+
+    monkeypatch.setenv("XGEN_PHAA_FP8_ALIGN16", "1")
+    tensor = torch.empty((2, 128), device=device)
+    with patch.object(dist, "get_world_size") as world_size, patch.object(dist, "all_to_all_single") as exchange:
+        with pytest.raises(ValueError, match="requires CUDA tensors"):
+            transport.fp8_all_to_all(torch.empty_like(tensor), tensor, 128, None)
+    world_size.assert_not_called()
+    exchange.assert_not_called()
+
+
+def test_transport_rejects_bad_stream_counts():
+    from xgen_amd.phaa import fp8_transport as transport
+
+    t = torch.empty((2, 128))
+    with pytest.raises(ValueError, match="one tensor or a QKV triple"):
+        transport.fp8_all_to_all_many((t, t), (t, t), 128, None)
+    with pytest.raises(ValueError, match="one tensor or a QKV triple"):
+        transport.fp8_all_to_all_many((t,), (t, t, t), 128, None)
+
+
+def test_wire_shape_contract():
+    from xgen_amd.phaa.fp8_transport import wire_shape
+
+    assert wire_shape(3, 2 * 17 * 3, 128, 2, 0) == (3 * 2 * 17 * 3, 132)
+    assert wire_shape(1, 2 * 17 * 3, 128, 2, 4) == (2, 17 * 3 * 132 + 4)

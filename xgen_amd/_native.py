@@ -66,6 +66,12 @@ SIGNATURES = {
     "xgen_w8a8_gate_residual": (_c_int, [
         _c_int, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64,
         _c_ptr, _c_int, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr]),
+    "xgen_fp8_wire_peer_padding": (_c_i64, [_c_int, _c_i64, _c_i64, _c_int]),
+    "xgen_fp8_wire_encode": (_c_int, [
+        _c_int, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr,
+        _c_ptr]),
+    "xgen_fp8_wire_decode": (_c_int, [
+        _c_int, _c_int, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr]),
 }
 
 

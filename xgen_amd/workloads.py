@@ -70,3 +70,15 @@ def weight(name: str, g: torch.Generator, device="cpu") -> tuple[torch.Tensor, t
     w = (torch.randn((N, K), generator=g, device=device) * 0.02).to(torch.bfloat16)
     b = (torch.randn((N,), generator=g, device=device) * 0.01).to(torch.bfloat16)
     return w, b
+
+
+# Head-parallel attention geometry of the FP8 wire codec: 24 heads x 128 (d = 3072), 8 peers.
+HEADS, HEAD_DIM, SP_PEERS = 24, 128, 8
+
+
+def qkv_head_views(fused: torch.Tensor, heads: int = HEADS, head_dim: int = HEAD_DIM, peers: int = SP_PEERS):
+    """Q, K, V of a fused [M, 3 * heads * head_dim] projection output as in-place
+    [peers, M, 1, heads / peers, head_dim] views (peer p holds heads p*H/P .. (p+1)*H/P - 1)."""
+    M = fused.shape[0]
+    return tuple(t.unflatten(-1, (peers, heads // peers, head_dim)).reshape(M, 1, peers, heads // peers, head_dim)
+                 .permute(2, 0, 1, 3, 4) for t in fused.chunk(3, dim=-1))
