@@ -1,0 +1,188 @@
+"""AdaLN schedule tables, loaded from the reference's safetensors table files into HBM.
+
+Mirrors x_base/x_base/adaln_cache/cache.py:47-296 (AdalnScheduleCache): a table
+file holds, for each sampler step i and block j, the AdaLN projection output
+`[{cond}_]step{i}_block{j}` of shape [M, 18H] (M timesteps of the step's batch,
+3 modalities x 6 modulation vectors x H) plus `step{i}_final` [M, 2H] and the
+step's `step{i}_timesteps` [M]; optional constant rows `const_timesteps`,
+`const_block{j}`, `const_final` are merged after each step's rows for the
+conditioning type's constant timesteps (cache.py:156-178, 205-258).  With
+`quantization=int8` metadata each table is `{key}_int8` times `{key}_scale`,
+rounded to bf16 (cache.py:189-201).  A block table viewed as [3M, 6H] splits
+into (shift, scale, gate, shift_mlp, scale_mlp, gate_mlp), each [3M, H]
+(cache.py:116-119; order of h3_npu_fusion.py:350); row t*3 + modality is
+addressed by `adaln_indices` (minimax_h3.py:410).
+
+Layout in HBM: every table of one schedule (all blocks, step rows then the
+merged constant rows) is one contiguous bf16 buffer [num_blocks, 3M', 6H] plus
+one [M', 2H] buffer for the final layer, resident for the life of the cache
+(the H3 tables of a 50-step schedule are about 1.4 GB of the 288 GB); lookups
+return views, so the fused front end (xgen_norm_affine_quant) and the gated
+residual read their scale / shift / gate rows straight from it with the
+[3M', H] row stride of 6H.
+"""
+from __future__ import annotations
+
+import logging
+import os
+from typing import NamedTuple
+
+import torch
+
+logger = logging.getLogger(__name__)
+
+MODALITY_NUM = 3  # video / audio / text rows per timestep (minimax_h3.py MINIMAX_H3_MODALITY_NUM)
+
+
+class BlockTables(NamedTuple):
+    """The six modulation tables of one block, each [3M', H] (a strided view)."""
+    shift: torch.Tensor
+    scale: torch.Tensor
+    gate: torch.Tensor
+    shift_mlp: torch.Tensor
+    scale_mlp: torch.Tensor
+    gate_mlp: torch.Tensor
+
+
+def adaln_indices(timestep_indices: torch.Tensor, token_tags: torch.Tensor) -> torch.Tensor:
+    """Per-token table row: timestep_index * 3 + max(token_tag, 0) (minimax_h3.py:410); padding
+    tokens (tag < 0) read the video row."""
+    return timestep_indices.long() * MODALITY_NUM + token_tags.long().clamp(min=0)
+
+
+class AdalnScheduleCache:
+    """AdaLN modulation tables keyed by timestep schedule (cache.py:47-296).
+
+        cache = AdalnScheduleCache(None, cache_file="tables.safetensors", conditioning_type="video")
+        cache.maybe_install(timesteps)       # before each denoising step
+        t = cache.block_tables(j)            # six [3M', H] views for block j
+    """
+
+    _CONST_INDEX_MAP = {"none": [], "video": [0], "audio": [1], "both": [0, 1]}
+
+    def __init__(self, model=None, cache_file: str | None = None, conditioning_type: str = "none",
+                 device: torch.device | str | None = None):
+        self.model = model
+        self._tables = {}
+        self._current_key = None
+        self._current_table = None
+        self._file_cache_loaded = False
+        self._conditioning_type = conditioning_type
+        self._source_file = os.path.realpath(cache_file) if cache_file else None
+        self._device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        if cache_file:
+            self._load_file_cache(cache_file)
+
+    # -- file cache loading ------------------------------------------------
+    def _load_file_cache(self, path: str):
+        from safetensors import safe_open
+
+        with safe_open(path, framework="pt") as f:
+            metadata = f.metadata() or {}
+            keys = set(f.keys())
+            num_eval_steps = int(metadata.get("num_eval_steps", int(metadata["num_steps"]) - 1))
+            if "num_blocks" in metadata:
+                num_blocks = int(metadata["num_blocks"])
+            elif self.model is not None:
+                num_blocks = len(self.model.transformer_blocks)
+            else:
+                raise ValueError("AdaLN table metadata has no num_blocks and no model was given")
+            quantization = metadata.get("quantization", "none")
+            if quantization not in ("none", "int8"):
+                raise ValueError(f"unsupported AdaLN table quantization {quantization!r}")
+            conditioned = metadata.get("conditioning_tables")
+            if conditioned and self._conditioning_type not in conditioned.split(","):
+                raise ValueError(f"AdaLN table does not contain conditioning={self._conditioning_type}")
+            prefix = f"{self._conditioning_type}_" if conditioned else ""
+
+            const = None
+            if "const_timesteps" in keys:
+                const = (f.get_tensor("const_timesteps"),
+                         [_rows(self._read(f, f"const_block{j}", quantization)) for j in range(num_blocks)],
+                         self._read(f, "const_final", quantization))
+            elif not conditioned:
+                logger.warning("No constant timesteps in cache file. Condition row (0.999, 1.0) cache miss will error.")
+            const_indices = [] if conditioned else self._CONST_INDEX_MAP.get(self._conditioning_type, [])
+            if const_indices and const is None:
+                raise RuntimeError(
+                    f"conditioning_type={self._conditioning_type} requires constant entries but cache file has none. "
+                    "Regenerate cache with updated precompute script.")
+
+            for i in range(num_eval_steps):
+                ts = f.get_tensor(f"{prefix}step{i}_timesteps").to(torch.float32)
+                blocks = [_rows(self._read(f, f"{prefix}step{i}_block{j}", quantization)) for j in range(num_blocks)]
+                final = self._read(f, f"{prefix}step{i}_final", quantization)
+                if const_indices:
+                    # step rows first, then the selected timesteps' 3 modality rows (cache.py:205-258)
+                    sel = torch.tensor(const_indices, dtype=torch.long)
+                    rows = (sel[:, None] * MODALITY_NUM + torch.arange(MODALITY_NUM)).reshape(-1)
+                    ts = torch.cat([ts, const[0].to(torch.float32)[sel]])
+                    blocks = [torch.cat([b, c.index_select(0, rows)]) for b, c in zip(blocks, const[1])]
+                    final = torch.cat([final, const[2].index_select(0, sel)])
+                self._tables[self._schedule_key(ts)] = self._pack(blocks, final)
+        self._file_cache_loaded = True
+        _const = const[0].tolist() if const is not None else "none"
+        logger.info(f"AdaLN cache loaded: {num_eval_steps} steps, {num_blocks} blocks, {len(self._tables)} tables, "
+                    f"conditioning={self._conditioning_type}, quant={quantization}, const={_const}, "
+                    f"variant={metadata.get('model_variant', 'unknown')}")
+
+    def _read(self, f, key: str, quantization: str) -> torch.Tensor:
+        """A table as bf16 on the host: {key}, or {key}_int8 * {key}_scale rounded to bf16 (cache.py:189-201)."""
+        if quantization == "int8":
+            return (f.get_tensor(f"{key}_int8").to(torch.float32) * f.get_tensor(f"{key}_scale")).to(torch.bfloat16)
+        return f.get_tensor(key).to(torch.bfloat16)
+
+    def _pack(self, blocks, final) -> dict:
+        """One schedule's tables as two device buffers: blocks [num_blocks, 3M', 6H], final [M', 2H]."""
+        shape = blocks[0].shape
+        if any(b.shape != shape for b in blocks):
+            raise ValueError("AdaLN block tables of one step differ in shape")
+        if final.dim() != 2 or final.shape[-1] * 3 != shape[-1]:
+            raise ValueError(f"AdaLN final table {tuple(final.shape)} does not match block rows of width {shape[-1]}")
+        packed = torch.empty((len(blocks), *shape), dtype=torch.bfloat16, device=self._device)
+        for j, b in enumerate(blocks):
+            packed[j].copy_(b)
+        final_dev = final.contiguous().to(self._device)
+        return {"packed": packed,
+                "blocks": [BlockTables(*packed[j].chunk(6, dim=-1)) for j in range(len(blocks))],
+                "final": tuple(final_dev.chunk(2, dim=-1))}
+
+    # -- key ---------------------------------------------------------------
+    @staticmethod
+    def _schedule_key(timesteps: torch.Tensor) -> bytes:
+        """Float32 bit pattern of the timesteps (cache.py:262-266)."""
+        return timesteps.detach().to(torch.float32).cpu().numpy().tobytes()
+
+    # -- install / lookup --------------------------------------------------
+    def maybe_install(self, timesteps: torch.Tensor):
+        """Install the precomputed table of this timestep schedule; KeyError if the file has none."""
+        key = self._schedule_key(timesteps)
+        if key == self._current_key:
+            return
+        self._current_table = self._tables[key]
+        self._current_key = key
+
+    @property
+    def has_current(self) -> bool:
+        return self._current_table is not None
+
+    def lookup_block(self, block_idx: int) -> BlockTables:
+        """The six [3M', H] tables of block block_idx (cache.py:290-292)."""
+        return self._current_table["blocks"][block_idx]
+
+    block_tables = lookup_block
+
+    def lookup_final(self):
+        """(shift, scale) of the final layer, each [M', H] (cache.py:294-296)."""
+        return self._current_table["final"]
+
+    def packed(self) -> torch.Tensor:
+        """The installed schedule's block tables as one [num_blocks, 3M', 6H] device buffer."""
+        return self._current_table["packed"]
+
+
+def _rows(raw: torch.Tensor) -> torch.Tensor:
+    """A block table [M, 18H] as its [3M, 6H] modality rows (cache.py:116-118)."""
+    if raw.dim() != 2 or raw.shape[-1] % (6 * MODALITY_NUM):
+        raise ValueError(f"AdaLN block table {tuple(raw.shape)} is not [M, 18H]")
+    return raw.reshape(-1, raw.shape[-1] // MODALITY_NUM)
