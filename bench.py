@@ -53,7 +53,8 @@ def parse():
 
 
 PROFILE_KERNELS = ("gemm_fp8_qkv", "gemm_int8_qkv", "gemm_fp8_ffn_up_gelu", "gemm_fp8_ffn_down", "quant_rows_fp8",
-                   "front_end_ln_mod_quant_fp8", "wire_encode_h3", "wire_decode_h3", "copy_1gib")
+                   "front_end_ln_mod_quant_fp8", "gate_residual_op", "swiglu_quant_int8_h3", "wire_encode_h3",
+                   "wire_decode_h3", "copy_1gib")
 
 
 def wire_setup(M, g, dev):
@@ -120,6 +121,15 @@ def profile_kernels(names, steps, warmup):
             fn = lambda: xops.scaled_mm(qa, qw, sa, sw, b, torch.bfloat16, act, False)  # noqa: E731
         elif name == "quant_rows_fp8":
             fn = lambda: xops.quantize_rows(nxt(), fp8)  # noqa: E731
+        elif name == "gate_residual_op":
+            res = torch.randn((1, M, K), generator=g, device=dev).to(torch.bfloat16)
+            yb = torch.randn((1, M, K), generator=g, device=dev).to(torch.bfloat16)
+            gt = (torch.randn((20, K), generator=g, device=dev) * 0.1).to(torch.bfloat16)
+            gi = torch.randint(20, (M,), generator=g, device=dev)
+            fn = lambda: xops.gate_residual(res, yb, gt, gi)  # noqa: E731
+        elif name == "swiglu_quant_int8_h3":
+            u3 = torch.randn((1, M, 2 * 14336), generator=g, device=dev).to(torch.bfloat16)
+            fn = lambda: xops.swiglu_quant(u3, False, torch.int8, 1, False)  # noqa: E731
         elif name.startswith("wire_"):
             enc, dec, _, _ = wire_setup(M, g, dev)
             enc()
@@ -274,6 +284,15 @@ def main():
         fe_gbs = fe_bytes / (ms_fe * 1e-3) / 1e9
         kernels["front_end_ln_mod_quant_fp8"] = {"ms": ms_fe, "gbs": fe_gbs, "frac_of_hbm": fe_gbs / PEAK_HBM_GBS,
                                                  "bytes": fe_bytes}
+        # the same with the table's bf16(1 + scale) prepared once (as the AdaLN loader keeps it)
+        from xgen_amd.operator.nq2 import adaln_one_plus
+        f_tab = adaln_one_plus(scale)
+        kind_p = N.NORM_LAYER | N.NORM_SCALE_ONE_PLUS
+        ms_fp = timed(lambda: xops.norm_affine_quant(nxt()[None], None, f_tab, shift, idx, 1e-6, kind_p, fp8, False),
+                      args.steps, args.warmup)
+        kernels["front_end_ln_mod_quant_fp8_prepared_scale"] = {
+            "ms": ms_fp, "gbs": fe_bytes / (ms_fp * 1e-3) / 1e9,
+            "frac_of_hbm": fe_bytes / (ms_fp * 1e-3) / 1e9 / PEAK_HBM_GBS, "bytes": fe_bytes}
 
     # ---- FFN GEMMs and INT8 QKV
     if want("ffn"):

@@ -53,6 +53,8 @@ extern "C" {
 /* normalisation kinds for xgen_norm_affine_quant */
 #define XGEN_NORM_LAYER 0 /* (x - mean) * rsqrt(var + eps), biased variance */
 #define XGEN_NORM_RMS 1   /* x * rsqrt(mean(x^2) + eps) */
+/* OR-ed into norm_kind: scale_table holds bf16(1 + scale) (xgen_adaln_one_plus) */
+#define XGEN_NORM_SCALE_ONE_PLUS 0x100
 
 /* GEMM epilogue activations */
 #define XGEN_ACT_NONE 0
@@ -121,7 +123,7 @@ int xgen_fp8_pack(int in_dtype, const void *x, int64_t numel, const float *scale
  * x: BF16 [batch, seq, width], element (b, s, c) at x[b*x_stride_batch + s*x_stride_seq + c].
  * Row r = b*seq + s uses table row g = indices[s] (int64, 0 <= g < table_rows):
  *   n    = bf16(norm(x_r) [* weight])          norm_kind LAYER or RMS, fp32 math
- *   f    = bf16(1 + scale_table[g])
+ *   f    = bf16(1 + scale_table[g])   (scale_table[g] itself with XGEN_NORM_SCALE_ONE_PLUS in norm_kind)
  *   m    = bf16(bf16(n * f) + shift_table[g])
  *   q[r] = per-row quantization of m (out_dtype E4M3 or I8, as xgen_quantize_rows)
  * norm_weight: NULL (no affine) or [width] of dtype BF16/F32.
@@ -233,6 +235,16 @@ int xgen_w8a8_gate_residual(int in_dtype, const void *a, int64_t lda, const void
 int xgen_swiglu_quant(const void *u, int64_t batch, int64_t seq, int64_t half_width, int64_t u_stride_batch,
                       int64_t u_stride_seq, int gate_first, int out_dtype, int scale_mode, void *q, float *scale,
                       void *act_out, hipStream_t stream);
+
+/*
+ * out = bf16(1 + scale_table) over [rows, width] BF16 rows (strides in elements): the
+ * `1.0 + scale` of the eager AdaLN modulation (x_base/x_base/operator/h3_indexed_affine.py:22-28,
+ * x_diffusers/x_diffusers/framework/transformer/hunyuan.py:393), computed once per table so that
+ * xgen_norm_affine_quant with XGEN_NORM_SCALE_ONE_PLUS reads it per token instead of recomputing
+ * it (the reference recomputes it in every call).  width and strides multiples of 8.
+ */
+int xgen_adaln_one_plus(const void *scale_table, int64_t rows, int64_t width, int64_t scale_row_stride,
+                        void *out, int64_t out_row_stride, hipStream_t stream);
 
 /*
  * Per-row FP8 wire codec of the head-parallel attention exchange: the encode

@@ -51,3 +51,24 @@ def test_loaded_tables_feed_front_end_and_gate(cuda, tmp_path, H, out):
     y = gate_residual(residual.to(cuda), x.to(cuda), blk.gate, idx.to(cuda))
     ref = R.gate_residual(residual, x, blk.gate.cpu(), idx)
     assert torch.equal(y.cpu().view(torch.int16), ref.view(torch.int16))
+
+
+def test_prepared_one_plus_tables_match_plain_tables(cuda, tmp_path):
+    """The loader's prepared bf16(1 + scale) tables give the plain path's bytes through the front end."""
+    H = 3072
+    path = tmp_path / "tables.safetensors"
+    t = table_file(path, H, blocks=3)
+    cache = AdalnScheduleCache(None, str(path), "none", device=cuda)
+    cache.maybe_install(t["step0_timesteps"].to(cuda))
+    x = torch.randn(1, 64, H, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16).to(cuda)
+    idx = adaln_indices(torch.randint(0, 2, (64,)), torch.randint(0, 3, (64,))).to(cuda)
+    for j in range(3):
+        blk = cache.lookup_block(j)
+        f, f_mlp = cache.one_plus_scales(j)
+        for scale, shift, prepared in ((blk.scale, blk.shift, f), (blk.scale_mlp, blk.shift_mlp, f_mlp)):
+            q0, s0 = norm_affine_quant(x, None, scale, shift, idx, eps=1e-6, norm="layer",
+                                       out_dtype=torch.float8_e4m3fn)
+            q1, s1 = norm_affine_quant(x, None, prepared, shift, idx, eps=1e-6, norm="layer",
+                                       out_dtype=torch.float8_e4m3fn, scale_is_one_plus=True)
+            assert torch.equal(q0.view(torch.uint8), q1.view(torch.uint8)) and torch.equal(s0, s1)
+            assert torch.equal(prepared.cpu().view(torch.int16), (1.0 + scale.cpu()).view(torch.int16))

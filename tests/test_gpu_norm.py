@@ -103,3 +103,37 @@ def test_full_size_front_end_c5_share(cuda):
     idx = torch.randint(20, (M,), generator=g, device=cuda)
     q, s, m = xops.norm_affine_quant(x[None], None, scale, shift, idx, 1e-6, N.NORM_LAYER, torch.float8_e4m3fn, True)
     check(x[None], None, scale, shift, idx, 1e-6, "layer", "fp8", q, s, m)
+
+
+def test_adaln_one_plus_matches_eager_bf16(cuda):
+    """bf16(1 + scale) == the eager bf16 `1.0 + scale` (torch CPU), special values included."""
+    from xgen_amd.operator.nq2 import adaln_one_plus
+    g = torch.Generator().manual_seed(4)
+    t = (torch.randn(37, 520, generator=g) * torch.logspace(-6, 3, 520)).to(torch.bfloat16)
+    t[0, :6] = torch.tensor([float("nan"), float("inf"), float("-inf"), -1.0, -0.0, 2.0 ** -133])
+    big = torch.zeros(37, 1024, dtype=torch.bfloat16)
+    big[:, :520] = t
+    got = adaln_one_plus(big.to(cuda)[:, :520]).cpu()
+    ref = 1.0 + t
+    assert ref.dtype == torch.bfloat16
+    nan = torch.isnan(ref)
+    assert torch.equal(torch.isnan(got), nan)
+    assert torch.equal(got.view(torch.int16)[~nan], ref.view(torch.int16)[~nan])
+
+
+@pytest.mark.parametrize("norm", ["layer", "rms"])
+@pytest.mark.parametrize("out", ["fp8", "int8"])
+@pytest.mark.parametrize("H", [1024, 3072, 5376])
+def test_prepared_one_plus_scale_is_bit_identical(cuda, norm, out, H):
+    """scale_is_one_plus=True with bf16(1 + scale) gives the same bytes, scales and rows as the plain call."""
+    from xgen_amd.operator.nq2 import adaln_one_plus
+    x, scale, shift, idx = inputs(2, 41, H, 7, seed=H, dev=cuda)
+    dt = torch.float8_e4m3fn if out == "fp8" else torch.int8
+    eps = 1e-6 if norm == "layer" else 1e-5
+    q0, s0, m0 = norm_affine_quant(x, None, scale, shift, idx, eps=eps, norm=norm, out_dtype=dt, return_normed=True)
+    f = adaln_one_plus(scale)
+    q1, s1, m1 = norm_affine_quant(x, None, f, shift, idx, eps=eps, norm=norm, out_dtype=dt, return_normed=True,
+                                   scale_is_one_plus=True)
+    assert torch.equal(q0.view(torch.uint8), q1.view(torch.uint8))
+    assert torch.equal(s0, s1)
+    assert torch.equal(m0.view(torch.int16), m1.view(torch.int16))

@@ -20,7 +20,7 @@ _lib = None
 
 # dtype codes, include/xgen_amd.h
 DTYPE_BF16, DTYPE_F16, DTYPE_F32, DTYPE_E4M3, DTYPE_I8, DTYPE_I32, DTYPE_NONE = 0, 1, 2, 3, 4, 5, -1
-NORM_LAYER, NORM_RMS = 0, 1
+NORM_LAYER, NORM_RMS, NORM_SCALE_ONE_PLUS = 0, 1, 0x100
 ACT_NONE, ACT_GELU_TANH = 0, 1
 OK, ERR_INVALID_ARGUMENT, ERR_UNSUPPORTED, ERR_HIP = 0, 1, 2, 3
 
@@ -66,6 +66,7 @@ SIGNATURES = {
     "xgen_w8a8_gate_residual": (_c_int, [
         _c_int, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64,
         _c_ptr, _c_int, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr]),
+    "xgen_adaln_one_plus": (_c_int, [_c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr]),
     "xgen_fp8_wire_peer_padding": (_c_i64, [_c_int, _c_i64, _c_i64, _c_int]),
     "xgen_fp8_wire_encode": (_c_int, [
         _c_int, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr,

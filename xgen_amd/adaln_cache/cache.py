@@ -180,6 +180,24 @@ class AdalnScheduleCache:
         """The installed schedule's block tables as one [num_blocks, 3M', 6H] device buffer."""
         return self._current_table["packed"]
 
+    def one_plus_scales(self, block_idx: int):
+        """(bf16(1 + scale), bf16(1 + scale_mlp)) of block block_idx, each [3M', H], for
+        norm_affine_quant(..., scale_is_one_plus=True).  Prepared on the GPU for every block of the
+        installed schedule on first use (one [num_blocks, 3M', 2H] buffer) and kept with it."""
+        t = self._current_table
+        if "one_plus" not in t:
+            from ..operator.nq2 import adaln_one_plus
+            packed = t["packed"]
+            nb, rows, six_h = packed.shape
+            h = six_h // 6
+            prepared = torch.empty((nb, rows, 2 * h), dtype=torch.bfloat16, device=packed.device)
+            for j in range(nb):
+                blk = t["blocks"][j]
+                adaln_one_plus(blk.scale, prepared[j, :, :h])
+                adaln_one_plus(blk.scale_mlp, prepared[j, :, h:])
+            t["one_plus"] = [tuple(prepared[j].chunk(2, dim=-1)) for j in range(nb)]
+        return t["one_plus"][block_idx]
+
 
 def _rows(raw: torch.Tensor) -> torch.Tensor:
     """A block table [M, 18H] as its [3M, 6H] modality rows (cache.py:116-118)."""

@@ -14,6 +14,7 @@
 // stays in registers from the single HBM read to the single quantized write;
 // mean / variance / max |m| are wave reductions (plus an LDS exchange when a
 // row spans two waves).  The two table rows come from L2 (the table is small).
+#include "fastdiv.h"
 #include "xgen_common.h"
 
 namespace xgen {
@@ -24,7 +25,7 @@ constexpr int kThreads = 256;
 
 struct NormArgs {
   const uint8_t *x;
-  int64_t seq;
+  FastDiv seq;       // row r = b * seq + s
   int64_t rows;
   int width;
   int64_t xsb_bytes, xss_bytes;
@@ -90,8 +91,12 @@ __device__ __forceinline__ void load_weight8(const void *w, int dtype, int ci, f
 // next row and table index before it works on the current row.
 // FULL: the row is exactly CH chunks per lane (width == 512 * WPR * CH), so
 // no chunk needs a bounds check.
+// NORM: XGEN_NORM_LAYER or XGEN_NORM_RMS, plus XGEN_NORM_SCALE_ONE_PLUS when
+// the scale table already holds bf16(1 + scale).
 template <int NORM, int OUT, int WPR, int CH, bool FULL>
 __global__ __launch_bounds__(kThreads) void norm_affine_quant_kernel(NormArgs a) {
+  constexpr bool kOnePlus = (NORM & XGEN_NORM_SCALE_ONE_PLUS) != 0;
+  constexpr int kNorm = NORM & ~XGEN_NORM_SCALE_ONE_PLUS;
   constexpr int kRowsPerBlock = 4 / WPR;
   __shared__ float red_f[4];
   __shared__ uint32_t red_u[4];
@@ -105,9 +110,9 @@ __global__ __launch_bounds__(kThreads) void norm_affine_quant_kernel(NormArgs a)
   // one read of a row (zeros past the last row) and its table index
   auto load_row = [&](int64_t row, u32x4 (&c)[CH], int64_t &g) {
     const bool ok = row < a.rows;
-    const int64_t r = ok ? row : 0;
-    const int64_t b = r / a.seq, s = r % a.seq;
-    const uint8_t *xr = a.x + b * a.xsb_bytes + s * a.xss_bytes;
+    const uint32_t r = ok ? (uint32_t)row : 0u;
+    const uint32_t b = fast_div(r, a.seq), s = r - b * a.seq.d;
+    const uint8_t *xr = a.x + (int64_t)b * a.xsb_bytes + (int64_t)s * a.xss_bytes;
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
       const int ci = lane_in_row + j * 64 * WPR;
@@ -130,26 +135,25 @@ __global__ __launch_bounds__(kThreads) void norm_affine_quant_kernel(NormArgs a)
 
     // statistics (fp32, two passes over the packed row; chunks past the row's
     // end are zeros and must stay out of the variance)
+    // the row as fp32, unpacked once for the statistics and the normalisation
+    float xv[CH][8];
+#pragma unroll
+    for (int j = 0; j < CH; ++j) unpack8<XGEN_DTYPE_BF16>(c[j], xv[j]);
     float rstd, nmr = 0.0f;  // n = x * rstd + nmr
-    if constexpr (NORM == XGEN_NORM_LAYER) {
+    if constexpr (kNorm == XGEN_NORM_LAYER) {
       float acc = 0.0f;
 #pragma unroll
-      for (int j = 0; j < CH; ++j) {
-        float v[8];
-        unpack8<XGEN_DTYPE_BF16>(c[j], v);
+      for (int j = 0; j < CH; ++j)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc += v[i];
-      }
+        for (int i = 0; i < 8; ++i) acc += xv[j][i];
       const float mean = row_sum<WPR>(acc, wave, lane, red_f) / (float)a.width;
       float acc2 = 0.0f;
 #pragma unroll
       for (int j = 0; j < CH; ++j) {
         if (chunk_ok(j)) {
-          float v[8];
-          unpack8<XGEN_DTYPE_BF16>(c[j], v);
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
-            const float d = v[i] - mean;
+            const float d = xv[j][i] - mean;
             acc2 = __builtin_fmaf(d, d, acc2);
           }
         }
@@ -160,12 +164,9 @@ __global__ __launch_bounds__(kThreads) void norm_affine_quant_kernel(NormArgs a)
     } else {
       float acc2 = 0.0f;
 #pragma unroll
-      for (int j = 0; j < CH; ++j) {
-        float v[8];
-        unpack8<XGEN_DTYPE_BF16>(c[j], v);
+      for (int j = 0; j < CH; ++j)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc2 = __builtin_fmaf(v[i], v[i], acc2);
-      }
+        for (int i = 0; i < 8; ++i) acc2 = __builtin_fmaf(xv[j][i], xv[j][i], acc2);
       const float ms = row_sum<WPR>(acc2, wave, lane, red_f) / (float)a.width;
       rstd = 1.0f / __builtin_sqrtf(ms + a.eps);
     }
@@ -183,9 +184,8 @@ __global__ __launch_bounds__(kThreads) void norm_affine_quant_kernel(NormArgs a)
           const u32x4 scw = *reinterpret_cast<const u32x4 *>(sr + (int64_t)ci * 16);
           const u32x4 shw = *reinterpret_cast<const u32x4 *>(tr + (int64_t)ci * 16);
           float n[8];
-          unpack8<XGEN_DTYPE_BF16>(c[j], n);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) n[i] = __builtin_fmaf(n[i], rstd, nmr);
+          for (int i = 0; i < 8; ++i) n[i] = __builtin_fmaf(xv[j][i], rstd, nmr);
           if (a.weight_dtype != XGEN_DTYPE_NONE) {
             float wv[8];
             load_weight8(a.weight, a.weight_dtype, ci, wv);
@@ -198,8 +198,11 @@ __global__ __launch_bounds__(kThreads) void norm_affine_quant_kernel(NormArgs a)
           for (int i = 0; i < 4; ++i) {
             float n0 = n[2 * i], n1 = n[2 * i + 1];
             round_bf16x2(n0, n1);
-            float f0 = 1.0f + Half2<XGEN_DTYPE_BF16>::lo(scp[i]), f1 = 1.0f + Half2<XGEN_DTYPE_BF16>::hi(scp[i]);
-            round_bf16x2(f0, f1);
+            float f0 = Half2<XGEN_DTYPE_BF16>::lo(scp[i]), f1 = Half2<XGEN_DTYPE_BF16>::hi(scp[i]);
+            if constexpr (!kOnePlus) {
+              f0 += 1.0f, f1 += 1.0f;
+              round_bf16x2(f0, f1);
+            }
             float p0 = n0 * f0, p1 = n1 * f1;
             round_bf16x2(p0, p1);
             pk[i] = pack_bf16x2(p0 + Half2<XGEN_DTYPE_BF16>::lo(shp[i]), p1 + Half2<XGEN_DTYPE_BF16>::hi(shp[i]));
@@ -296,7 +299,8 @@ extern "C" int xgen_norm_affine_quant(const void *x, int64_t batch, int64_t seq,
                                       void *q, float *token_scale, void *normed_out,
                                       hipStream_t stream) {
   const char *fn = "xgen_norm_affine_quant";
-  if (norm_kind != XGEN_NORM_LAYER && norm_kind != XGEN_NORM_RMS)
+  const int norm_base = norm_kind & ~XGEN_NORM_SCALE_ONE_PLUS;
+  if (norm_base != XGEN_NORM_LAYER && norm_base != XGEN_NORM_RMS)
     return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: unknown norm kind %d", fn, norm_kind);
   if (!is_quant_dtype(out_dtype)) return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: output dtype must be E4M3 or I8", fn);
   if (norm_weight_dtype != XGEN_DTYPE_NONE && norm_weight_dtype != XGEN_DTYPE_BF16 &&
@@ -321,11 +325,12 @@ extern "C" int xgen_norm_affine_quant(const void *x, int64_t batch, int64_t seq,
       (normed_out && !aligned16(normed_out)) || (norm_weight && !aligned16(norm_weight)))
     return fail(XGEN_ERR_UNSUPPORTED, "%s: width and row strides must be multiples of 8 elements and "
                 "buffers 16-byte aligned", fn);
-  if (rows > 0x7fffffffLL * 4) return fail(XGEN_ERR_UNSUPPORTED, "%s: too many rows", fn);
+  // row indices (plus one grid step of prefetch) stay below 2^31
+  if (rows > 0x3fffffffLL) return fail(XGEN_ERR_UNSUPPORTED, "%s: too many rows", fn);
 
   NormArgs a;
   a.x = static_cast<const uint8_t *>(x);
-  a.seq = seq;
+  a.seq = make_fastdiv((uint32_t)seq);
   a.rows = rows;
   a.width = (int)width;
   a.xsb_bytes = x_stride_batch * 2;
@@ -342,12 +347,66 @@ extern "C" int xgen_norm_affine_quant(const void *x, int64_t batch, int64_t seq,
   a.q = static_cast<uint8_t *>(q);
   a.token_scale = token_scale;
   a.normed = static_cast<uint8_t *>(normed_out);
-  if (norm_kind == XGEN_NORM_LAYER) {
-    if (out_dtype == XGEN_DTYPE_E4M3) dispatch_width<XGEN_NORM_LAYER, XGEN_DTYPE_E4M3>(a, stream);
-    else dispatch_width<XGEN_NORM_LAYER, XGEN_DTYPE_I8>(a, stream);
-  } else {
-    if (out_dtype == XGEN_DTYPE_E4M3) dispatch_width<XGEN_NORM_RMS, XGEN_DTYPE_E4M3>(a, stream);
-    else dispatch_width<XGEN_NORM_RMS, XGEN_DTYPE_I8>(a, stream);
+  constexpr int kP = XGEN_NORM_SCALE_ONE_PLUS;
+  const bool e4m3 = out_dtype == XGEN_DTYPE_E4M3;
+  switch (norm_kind) {
+    case XGEN_NORM_LAYER:
+      if (e4m3) dispatch_width<XGEN_NORM_LAYER, XGEN_DTYPE_E4M3>(a, stream);
+      else dispatch_width<XGEN_NORM_LAYER, XGEN_DTYPE_I8>(a, stream);
+      break;
+    case XGEN_NORM_RMS:
+      if (e4m3) dispatch_width<XGEN_NORM_RMS, XGEN_DTYPE_E4M3>(a, stream);
+      else dispatch_width<XGEN_NORM_RMS, XGEN_DTYPE_I8>(a, stream);
+      break;
+    case XGEN_NORM_LAYER | kP:
+      if (e4m3) dispatch_width<XGEN_NORM_LAYER | kP, XGEN_DTYPE_E4M3>(a, stream);
+      else dispatch_width<XGEN_NORM_LAYER | kP, XGEN_DTYPE_I8>(a, stream);
+      break;
+    default:
+      if (e4m3) dispatch_width<XGEN_NORM_RMS | kP, XGEN_DTYPE_E4M3>(a, stream);
+      else dispatch_width<XGEN_NORM_RMS | kP, XGEN_DTYPE_I8>(a, stream);
+      break;
   }
+  return launch_status(fn);
+}
+
+// out[r, c] = bf16(1 + scale[r, c]): the `1.0 + scale` of the eager modulation
+// (x_base/x_base/operator/h3_indexed_affine.py:22-28, hunyuan.py:393), computed once per
+// table so the fused front end reads it directly (XGEN_NORM_SCALE_ONE_PLUS).
+__global__ __launch_bounds__(256) void adaln_one_plus_kernel(const uint8_t *scale, int64_t s_stride_bytes,
+                                                             uint8_t *out, int64_t o_stride_bytes, int64_t rows,
+                                                             int chunks) {
+  const int64_t total = rows * chunks;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / chunks;
+    const int c = (int)(i - r * chunks);
+    const u32x4 v = *reinterpret_cast<const u32x4 *>(scale + r * s_stride_bytes + (int64_t)c * 16);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      o[k] = pack_bf16x2(1.0f + Half2<XGEN_DTYPE_BF16>::lo(w[k]), 1.0f + Half2<XGEN_DTYPE_BF16>::hi(w[k]));
+    *reinterpret_cast<u32x4 *>(out + r * o_stride_bytes + (int64_t)c * 16) = u32x4{o[0], o[1], o[2], o[3]};
+  }
+}
+
+extern "C" int xgen_adaln_one_plus(const void *scale_table, int64_t rows, int64_t width, int64_t scale_row_stride,
+                                   void *out, int64_t out_row_stride, hipStream_t stream) {
+  const char *fn = "xgen_adaln_one_plus";
+  if (rows < 0 || width <= 0 || scale_row_stride < width || out_row_stride < width)
+    return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: bad shape rows=%lld width=%lld (row strides must be >= width)", fn,
+                (long long)rows, (long long)width);
+  if (rows == 0) return ok();
+  if (!scale_table || !out) return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+  if (width % 8 || scale_row_stride % 8 || out_row_stride % 8 || !aligned16(scale_table) || !aligned16(out))
+    return fail(XGEN_ERR_UNSUPPORTED, "%s: width and row strides must be multiples of 8 elements and buffers "
+                "16-byte aligned", fn);
+  if (width / 8 > 0x7fffffffLL) return fail(XGEN_ERR_UNSUPPORTED, "%s: row too wide", fn);
+  const int chunks = (int)(width / 8);
+  const int64_t total = rows * chunks;
+  const int64_t blocks = (total + 255) / 256;
+  adaln_one_plus_kernel<<<dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, stream>>>(
+      static_cast<const uint8_t *>(scale_table), scale_row_stride * 2, static_cast<uint8_t *>(out),
+      out_row_stride * 2, rows, chunks);
   return launch_status(fn);
 }

@@ -86,7 +86,8 @@ def _norm_check(x, weight, scale, shift, indices, eps, norm_kind, out_dtype):
     _require(indices.dim() == 1 and indices.shape[0] == x.shape[1] and indices.dtype == torch.int64
              and indices.is_contiguous(), "norm_affine_quant: contiguous INT64 indices [S] required")
     _require(0 < eps < 1, "norm_affine_quant: eps must be in (0, 1)")
-    _require(norm_kind in (N.NORM_LAYER, N.NORM_RMS), "norm_affine_quant: norm_kind must be 0 (layer) or 1 (rms)")
+    _require(norm_kind & ~N.NORM_SCALE_ONE_PLUS in (N.NORM_LAYER, N.NORM_RMS),
+             "norm_affine_quant: norm_kind must be 0 (layer) or 1 (rms), optionally | 0x100 (scale is 1 + scale)")
     _require(out_dtype in (torch.float8_e4m3fn, torch.int8), "norm_affine_quant: out_dtype must be float8_e4m3fn or int8")
 
 
