@@ -356,6 +356,28 @@ def main():
                              "frac_of_hbm": sw_bytes / (ms_sw * 1e-3) / 1e9 / PEAK_HBM_GBS, "bytes": sw_bytes}
         del u3
 
+    # ---- H3's FFN on the same kernels (d = 5,376, F = 14,336): FP8 up -> SwiGLU + FP8 requant -> FP8 down
+    if want("h3_ffn"):
+        d3, F3 = 5376, 14336
+        x3 = torch.randn((M, d3), generator=g, device=dev).to(torch.bfloat16)
+        wu3 = (torch.randn((2 * F3, d3), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        wd3 = (torch.randn((d3, F3), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        qx3, sx3 = xops.quantize_rows(x3, fp8)
+        qu3, su3 = xops.quantize_rows(wu3, fp8)
+        qd3, sd3 = xops.quantize_rows(wd3, fp8)
+        u3, _ = xops.scaled_mm(qx3, qu3, sx3, su3, None, torch.bfloat16, N.ACT_NONE, False)
+        qh3, sh3, _ = xops.swiglu_quant(u3[None], False, fp8, 1, False)
+        f_up3, f_dn3 = 2.0 * M * 2 * F3 * d3, 2.0 * M * d3 * F3
+        ms_u3 = timed(lambda: xops.scaled_mm(qx3, qu3, sx3, su3, None, torch.bfloat16, N.ACT_NONE, False),
+                      max(5, args.steps // 5), args.warmup)
+        ms_d3 = timed(lambda: xops.scaled_mm(qh3, qd3, sh3, sd3, None, torch.bfloat16, N.ACT_NONE, False),
+                      max(5, args.steps // 5), args.warmup)
+        kernels["h3_ffn_up_fp8"] = {"ms": ms_u3, "tflops": f_up3 / (ms_u3 * 1e-3) / 1e12,
+                                    "frac_of_peak": f_up3 / (ms_u3 * 1e-3) / 1e12 / PEAK_FP8_TFLOPS}
+        kernels["h3_ffn_down_fp8"] = {"ms": ms_d3, "tflops": f_dn3 / (ms_d3 * 1e-3) / 1e12,
+                                      "frac_of_peak": f_dn3 / (ms_d3 * 1e-3) / 1e12 / PEAK_FP8_TFLOPS}
+        del x3, wu3, wd3, qu3, qd3, u3, qh3
+
     # ---- FP8 wire codec of the head-parallel attention exchange (Q/K/V at M=15,624, 24 x 128, 8 peers)
     if want("wire"):
         enc, dec, enc_bytes, dec_bytes = wire_setup(M, g, dev)

@@ -81,3 +81,26 @@ def test_h3_ffn_int8(cuda):
     qr, sr, _ = R.swiglu_quant(u, False, "int8", 1)
     yr = R.w8a8_linear_int8(qr, sr, down.weight.cpu(), down.antiquant_scale.cpu(), None)
     assert R.rel_l2(y, yr) <= 1e-2 and R.cosine(y, yr) >= 0.9999
+
+
+def test_h3_ffn_fp8(cuda):
+    """H3 geometry at reduced M on the FP8 path: up (per-channel W, per-token x) -> SwiGLU + FP8
+    requant -> down; each stage against the oracle given the stage's own input."""
+    from xgen_amd.operator.h3_fp8 import H3FP8Linear
+    g = torch.Generator().manual_seed(7)
+    M, d, F = 80, 5376, 14336
+    x = torch.randn((1, M, d), generator=g).to(torch.bfloat16).to(cuda)
+    wu = (torch.randn((2 * F, d), generator=g) * 0.02).to(torch.bfloat16)
+    wd = (torch.randn((d, F), generator=g) * 0.02).to(torch.bfloat16)
+    opts = dict(weight_scaling="channel", activation_scaling="token")
+    up, down = H3FP8Linear(wu.to(cuda), None, **opts), H3FP8Linear(wd.to(cuda), None, **opts)
+    u = up(x)
+    qa, sa = R.quantize_rows_fp8(x.cpu().reshape(M, d))
+    ur = R.w8a8_linear_fp8(qa, sa, up.weight.cpu(), up.weight_scale.cpu(), None)
+    assert R.rel_l2(u.reshape(M, 2 * F), ur) <= 1e-3
+    q, s, _ = xops.swiglu_quant(u, False, torch.float8_e4m3fn, 1, False)
+    qr, sr, _ = R.swiglu_quant(u, False, "fp8", 1)
+    assert torch.equal(q.cpu().view(torch.uint8), qr.view(torch.uint8).reshape(q.shape)) and torch.equal(s.cpu(), sr)
+    y = down.forward_quantized(q, s)
+    yr = R.w8a8_linear_fp8(qr, sr, down.weight.cpu(), down.weight_scale.cpu(), None)
+    assert R.rel_l2(y.reshape(M, d), yr) <= 1e-3 and R.cosine(y.reshape(M, d), yr) >= 0.9999
