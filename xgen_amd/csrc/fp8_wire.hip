@@ -435,20 +435,22 @@ Shape pick_shape(int width, int E, int c_max) {
 // 16-byte chunk per lane (16 lanes per row), the decoder with two.
 constexpr int kEncodeChunks = 1, kDecodeChunks = 2;
 
-// Persistent grid: one resident wave of blocks, or fewer when the rows run out.
-template <typename Kernel, typename Args>
-void launch_rows(Kernel kernel, const Args &a, int rows_per_block, hipStream_t stream) {
+// Persistent grid: one resident wave of blocks, or fewer when the rows run out
+// (the occupancy of each kernel is queried once).
+template <typename KS, typename Args>
+void launch_rows(const Args &a, int rows_per_block, hipStream_t stream) {
+  static const int per_cu = resident_blocks_per_cu(KS::kernel, kThreads);
   const int64_t need = ((int64_t)a.g.total + rows_per_block - 1) / rows_per_block;
-  const int64_t cap = (int64_t)device_cu_count() * resident_blocks_per_cu(kernel, kThreads);
-  kernel<<<dim3((unsigned)(need < cap ? need : cap)), dim3(kThreads), 0, stream>>>(a);
+  const int64_t cap = (int64_t)device_cu_count() * per_cu;
+  KS::kernel<<<dim3((unsigned)(need < cap ? need : cap)), dim3(kThreads), 0, stream>>>(a);
 }
 
 template <template <int, int, bool, int> class K, int T, int E, bool ALIGNED, typename Args>
 void launch_c(const Args &a, const Shape &sh, hipStream_t stream) {
   const int rows_per_block = kThreads >> sh.log2_lanes;
-  if (sh.C == 1) launch_rows(K<T, E, ALIGNED, 1>::kernel, a, rows_per_block, stream);
-  else if (sh.C == 2) launch_rows(K<T, E, ALIGNED, 2>::kernel, a, rows_per_block, stream);
-  else launch_rows(K<T, E, ALIGNED, 4>::kernel, a, rows_per_block, stream);
+  if (sh.C == 1) launch_rows<K<T, E, ALIGNED, 1>>(a, rows_per_block, stream);
+  else if (sh.C == 2) launch_rows<K<T, E, ALIGNED, 2>>(a, rows_per_block, stream);
+  else launch_rows<K<T, E, ALIGNED, 4>>(a, rows_per_block, stream);
 }
 template <template <int, int, bool, int> class K, int T, bool ALIGNED, typename Args>
 void launch_ec(const Args &a, const Shape &sh, hipStream_t stream) {
