@@ -237,6 +237,21 @@ int xgen_swiglu_quant(const void *u, int64_t batch, int64_t seq, int64_t half_wi
                       void *act_out, hipStream_t stream);
 
 /*
+ * table[i] = bf16(silu(bf16 with bits i)) for all 65,536 bit patterns (128 KB, 16-byte aligned),
+ * with xgen_swiglu_quant's silu (IEEE division, the device expf): the same values by construction.
+ * No reference counterpart (the reference evaluates silu per element); prepared once per device.
+ */
+int xgen_silu_bf16_table(void *table, hipStream_t stream);
+
+/*
+ * xgen_swiglu_quant with a = silu_table[gate bits] (from xgen_silu_bf16_table): the same outputs;
+ * the table is read into LDS and the exponential and division leave the per-element work.
+ */
+int xgen_swiglu_quant_lut(const void *u, int64_t batch, int64_t seq, int64_t half_width, int64_t u_stride_batch,
+                          int64_t u_stride_seq, int gate_first, int out_dtype, int scale_mode, void *q, float *scale,
+                          void *act_out, const void *silu_table, hipStream_t stream);
+
+/*
  * out = bf16(1 + scale_table) over [rows, width] BF16 rows (strides in elements): the
  * `1.0 + scale` of the eager AdaLN modulation (x_base/x_base/operator/h3_indexed_affine.py:22-28,
  * x_diffusers/x_diffusers/framework/transformer/hunyuan.py:393), computed once per table so that

@@ -70,6 +70,12 @@ _STRIDES = (N._c_i64 * 12)(384, 128, 128, 128, 384, 128, 128, 128, 384, 128, 128
                                         16, 64, 16, 64, 20, 16, N.DTYPE_E4M3, 16, 16, None, None),
      N.ERR_INVALID_ARGUMENT, b"norm kind"),
     (lambda L: L.xgen_adaln_one_plus(16, 4, 64, 32, 16, 64, None), N.ERR_INVALID_ARGUMENT, b"bad shape"),
+    (lambda L: L.xgen_silu_bf16_table(None, None), N.ERR_INVALID_ARGUMENT, b"null"),
+    (lambda L: L.xgen_silu_bf16_table(8, None), N.ERR_UNSUPPORTED, b"aligned"),
+    (lambda L: L.xgen_swiglu_quant_lut(16, 1, 4, 64, 128, 128, 0, N.DTYPE_E4M3, 1, 16, 16, None, None, None),
+     N.ERR_INVALID_ARGUMENT, b"null silu table"),
+    (lambda L: L.xgen_swiglu_quant_lut(16, 1, 4, 64, 128, 128, 0, N.DTYPE_E4M3, 1, 16, 16, None, 8, None),
+     N.ERR_UNSUPPORTED, b"silu table must be 16-byte aligned"),
     (lambda L: L.xgen_adaln_one_plus(None, 4, 64, 64, 16, 64, None), N.ERR_INVALID_ARGUMENT, b"null"),
     (lambda L: L.xgen_adaln_one_plus(16, 4, 60, 64, 16, 64, None), N.ERR_UNSUPPORTED, b"multiples of 8"),
     (lambda L: L.xgen_fp8_wire_encode(N.DTYPE_BF16, 2, 16, 16, 16, _STRIDES, 2, 3, 1, 1, 128, 0, 16, None),

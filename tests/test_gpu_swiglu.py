@@ -104,3 +104,47 @@ def test_h3_ffn_fp8(cuda):
     y = down.forward_quantized(q, s)
     yr = R.w8a8_linear_fp8(qr, sr, down.weight.cpu(), down.weight_scale.cpu(), None)
     assert R.rel_l2(y.reshape(M, d), yr) <= 1e-3 and R.cosine(y.reshape(M, d), yr) >= 0.9999
+
+
+def _direct(u, gate_first, out_dtype, scale_mode):
+    """xgen_swiglu_quant (per-element silu) through the C ABI, for comparison with the table path."""
+    from xgen_amd import _native as N
+    B, S, F2 = u.shape
+    F = F2 // 2
+    q = torch.empty((B * S, F), dtype=out_dtype, device=u.device)
+    s = torch.empty((B * S,), dtype=torch.float32, device=u.device)
+    act = torch.empty((B * S, F), dtype=torch.bfloat16, device=u.device)
+    st = N.lib().xgen_swiglu_quant(u.data_ptr(), B, S, F, u.stride(0), u.stride(1), int(gate_first),
+                                   N.dtype_code(out_dtype), scale_mode, q.data_ptr(), s.data_ptr(), act.data_ptr(),
+                                   N.stream_of(u))
+    N.check(st, "xgen_swiglu_quant")
+    return q, s, act
+
+
+def test_silu_table_equals_oracle_on_every_bf16(cuda):
+    """All 65,536 entries of the table == bf16(g / (1 + exp(-g))) of the oracle (torch CPU), NaN by position."""
+    from xgen_amd.ops import silu_table
+    t = silu_table(cuda).cpu().view(torch.bfloat16)
+    g = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16).float()
+    ref = (g / (1.0 + torch.exp(-g))).to(torch.bfloat16)
+    nan = torch.isnan(ref)
+    assert torch.equal(torch.isnan(t), nan)
+    assert torch.equal(t.view(torch.int16)[~nan], ref.view(torch.int16)[~nan])
+
+
+@pytest.mark.parametrize("out", [torch.float8_e4m3fn, torch.int8])
+@pytest.mark.parametrize("F", [256, 1000, 3072, 5376, 14336, 16384])
+def test_table_path_equals_direct_path(cuda, out, F):
+    g = torch.Generator().manual_seed(F)
+    u = (torch.randn((2, 33, 2 * F), generator=g) * 4).to(torch.bfloat16)
+    u[0, 0, F + 3] = float("nan")
+    u[0, 1, F + 5] = float("inf")
+    u[0, 2, F + 7] = float("-inf")
+    u[1, 3, F:] = -0.0
+    u = u.to(cuda)
+    for gate_first in (False, True):
+        q0, s0, a0 = _direct(u, gate_first, out, 1)
+        q1, s1, a1 = xops.swiglu_quant(u, gate_first, out, 1, True)
+        assert torch.equal(q0.view(torch.uint8), q1.view(torch.uint8))
+        assert torch.equal(s0.view(torch.int32), s1.view(torch.int32))
+        assert torch.equal(a0.view(torch.int16), a1.view(torch.int16))

@@ -63,6 +63,10 @@ SIGNATURES = {
         _c_ptr, _c_ptr]),
     "xgen_swiglu_quant": (_c_int, [
         _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr]),
+    "xgen_silu_bf16_table": (_c_int, [_c_ptr, _c_ptr]),
+    "xgen_swiglu_quant_lut": (_c_int, [
+        _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
+        _c_ptr]),
     "xgen_w8a8_gate_residual": (_c_int, [
         _c_int, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64,
         _c_ptr, _c_int, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr]),

@@ -287,17 +287,36 @@ def _gate_gpu(residual, branch, gate_table, indices):
     return out
 
 
+_SILU_TABLES: dict[int, torch.Tensor] = {}
+
+
+def silu_table(device: torch.device) -> torch.Tensor:
+    """The device's bf16(silu(g)) table over all 65,536 bf16 patterns (xgen_silu_bf16_table), built on
+    first use and kept for the process.  Built on the current stream and waited for once, so any
+    stream may read it afterwards."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    t = _SILU_TABLES.get(idx)
+    if t is None:
+        t = torch.empty(65536, dtype=torch.int16, device=torch.device("cuda", idx))
+        stream = torch.cuda.current_stream(t.device)
+        N.check(N.lib().xgen_silu_bf16_table(t.data_ptr(), stream.cuda_stream), "xgen_silu_bf16_table")
+        stream.synchronize()
+        _SILU_TABLES[idx] = t
+    return t
+
+
 def _swiglu_gpu(u, gate_first, out_dtype, scale_mode, return_act):
     _on_gpu(u)
     q, s, act = _swiglu_meta(u, gate_first, out_dtype, scale_mode, return_act)
     if q.numel() == 0:
         return q, s, act
     u = u if u.stride(2) == 1 else u.contiguous()
-    st = N.lib().xgen_swiglu_quant(
+    table = silu_table(u.device)
+    st = N.lib().xgen_swiglu_quant_lut(
         u.data_ptr(), u.shape[0], u.shape[1], u.shape[2] // 2, u.stride(0), u.stride(1), int(bool(gate_first)),
         N.dtype_code(out_dtype), scale_mode, q.data_ptr(), s.data_ptr(), act.data_ptr() if return_act else None,
-        N.stream_of(u))
-    N.check(st, "xgen_swiglu_quant")
+        table.data_ptr(), N.stream_of(u))
+    N.check(st, "xgen_swiglu_quant_lut")
     return q, s, act
 
 
