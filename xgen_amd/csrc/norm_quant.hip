@@ -10,10 +10,11 @@
 // with every intermediate rounded to bf16 as the eager bf16 ops round it
 // (x_base/x_base/operator/h3_indexed_affine.py:22-28).
 //
-// Layout: one to four waves per row (at most 4 chunks of 8 per lane).  The row
-// stays in registers from the single HBM read to the single quantized write;
-// mean / variance / max |m| are wave reductions (plus an LDS exchange when a
-// row spans two waves).  The two table rows come from L2 (the table is small).
+// Layout: one wave per row up to width 3072, two or four beyond (at most 6
+// chunks of 8 per lane).  The row stays in registers from the single HBM read
+// to the single quantized write; the row sums and max |m| are wave reductions
+// (plus an LDS exchange when a row spans several waves).  The two table rows
+// come from L2 (the table is small).
 #include "fastdiv.h"
 #include "xgen_common.h"
 
@@ -29,8 +30,7 @@ struct NormArgs {
   int64_t rows;
   int width;
   int64_t xsb_bytes, xss_bytes;
-  const void *weight;
-  int weight_dtype;  // XGEN_DTYPE_NONE / BF16 / F32
+  const void *weight;  // per-column weight of dtype WT (kernel template), or null
   float eps;
   const uint8_t *scale_tab;
   int64_t scale_stride_bytes;
@@ -42,6 +42,21 @@ struct NormArgs {
   float *token_scale;
   uint8_t *normed;  // optional bf16 [rows, width]
 };
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// a.lo * b.lo + a.hi * b.hi + c on two packed bf16 pairs (v_dot2c_f32_bf16);
+// used only for the row statistics, whose rounding is not bit-specified.
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c,
+                                         false);
+}
+constexpr uint32_t kBf16OnePair = 0x3f803f80u;
+
+// The one-pass variance E[x^2] - mean^2 loses at most one bit to cancellation
+// while mean^2 <= E[x^2] / 2; other rows (including constant rows, and NaN or
+// infinite statistics) take the two-pass variance sum((x - mean)^2) / width.
+__device__ __forceinline__ bool needs_two_pass(float mean, float ex2) { return !(mean * mean <= 0.5f * ex2); }
 
 template <int WPR>
 __device__ __forceinline__ float row_sum(float v, int wave, int lane, float *red) {
@@ -56,6 +71,42 @@ __device__ __forceinline__ float row_sum(float v, int wave, int lane, float *red
     for (int i = 1; i < WPR; ++i) v += red[w0 + i];
   }
   return v;
+}
+
+// Sum and sum of squares of a row, reduced together.  two_pass_here: this row
+// needs the two-pass variance; two_pass_any: some row of the workgroup does
+// (the same value in every wave, so the second reduction's barriers stay in
+// step; each row still uses only its own statistics).
+struct RowMoments {
+  float s1, s2;
+  bool two_pass_here, two_pass_any;
+};
+
+template <int WPR>
+__device__ __forceinline__ RowMoments row_moments(float s1, float s2, int wave, int lane, float *red,
+                                                  float inv_w) {
+  s1 = wave_sum_f32(s1);
+  s2 = wave_sum_f32(s2);
+  RowMoments m;
+  if constexpr (WPR == 1) {
+    m.s1 = s1, m.s2 = s2;
+    m.two_pass_here = m.two_pass_any = needs_two_pass(s1 * inv_w, s2 * inv_w);
+  } else {
+    __syncthreads();  // red[] reuse
+    if (lane == 0) red[wave] = s1, red[4 + wave] = s2;
+    __syncthreads();
+    m.two_pass_any = false;
+#pragma unroll
+    for (int r = 0; r < 4 / WPR; ++r) {
+      float t1 = red[r * WPR], t2 = red[4 + r * WPR];
+#pragma unroll
+      for (int i = 1; i < WPR; ++i) t1 += red[r * WPR + i], t2 += red[4 + r * WPR + i];
+      const bool need = needs_two_pass(t1 * inv_w, t2 * inv_w);
+      m.two_pass_any |= need;
+      if (r == wave / WPR) m.s1 = t1, m.s2 = t2, m.two_pass_here = need;
+    }
+  }
+  return m;
 }
 
 template <int WPR>
@@ -73,215 +124,273 @@ __device__ __forceinline__ uint32_t row_max_u32(uint32_t v, int wave, int lane, 
   return v;
 }
 
-__device__ __forceinline__ void load_weight8(const void *w, int dtype, int ci, float (&wv)[8]) {
-  if (dtype == XGEN_DTYPE_BF16) {
-    const u32x4 c = *reinterpret_cast<const u32x4 *>(static_cast<const uint8_t *>(w) + (int64_t)ci * 16);
-    unpack8<XGEN_DTYPE_BF16>(c, wv);
-  } else {
-    const f32x4 *p = reinterpret_cast<const f32x4 *>(static_cast<const uint8_t *>(w) + (int64_t)ci * 32);
-    const f32x4 a = p[0], b = p[1];
-    wv[0] = a.x; wv[1] = a.y; wv[2] = a.z; wv[3] = a.w;
-    wv[4] = b.x; wv[5] = b.y; wv[6] = b.z; wv[7] = b.w;
+// The 8 weights of chunk ci (WT = BF16 or F32) as fp32.
+template <int WT>
+struct Weight8 {
+  static constexpr int kWords = WT == XGEN_DTYPE_F32 ? 8 : 4;
+  uint32_t w[kWords];
+  __device__ __forceinline__ void load(const void *p, int ci) {
+    if constexpr (WT == XGEN_DTYPE_F32) {
+      const u32x4 *q = reinterpret_cast<const u32x4 *>(static_cast<const uint8_t *>(p) + (int64_t)ci * 32);
+      const u32x4 a = q[0], b = q[1];
+      w[0] = a.x, w[1] = a.y, w[2] = a.z, w[3] = a.w, w[4] = b.x, w[5] = b.y, w[6] = b.z, w[7] = b.w;
+    } else if constexpr (WT == XGEN_DTYPE_BF16) {
+      const u32x4 a = *reinterpret_cast<const u32x4 *>(static_cast<const uint8_t *>(p) + (int64_t)ci * 16);
+      w[0] = a.x, w[1] = a.y, w[2] = a.z, w[3] = a.w;
+    }
   }
-}
+  __device__ __forceinline__ float get(int i) const {
+    if constexpr (WT == XGEN_DTYPE_F32) return __uint_as_float(w[i]);
+    else return (i & 1) ? Half2<XGEN_DTYPE_BF16>::hi(w[i >> 1]) : Half2<XGEN_DTYPE_BF16>::lo(w[i >> 1]);
+  }
+};
 
 // Streaming: a grid of as many workgroups as are resident walks the rows
 // (4 / WPR rows per workgroup per step; the walk is uniform over the
-// workgroup, so the cross-wave reductions stay in step); each wave loads its
-// next row and table index before it works on the current row.
+// workgroup, so the cross-wave reductions stay in step).  Software pipeline
+// per wave: at the top of a step it issues the next row's table index and x
+// read; once the current row's modulation has consumed its table rows it
+// issues the next row's table (and weight) reads into the same registers; so
+// every read has about one step of work to hide behind.  Every memory access
+// of the loop is unconditional, so the compiler's wait counts name exactly
+// the loads a step needs: rows past the end redo the last row (writing the
+// same bytes as its owner), chunks past a row's end read chunk 0 and are
+// zeroed, a row whose index is outside the table reads table row 0 and
+// selects its poisoned output.
 // FULL: the row is exactly CH chunks per lane (width == 512 * WPR * CH), so
-// no chunk needs a bounds check.
+// no chunk is past the end.
 // NORM: XGEN_NORM_LAYER or XGEN_NORM_RMS, plus XGEN_NORM_SCALE_ONE_PLUS when
-// the scale table already holds bf16(1 + scale).
-template <int NORM, int OUT, int WPR, int CH, bool FULL>
-__global__ __launch_bounds__(kThreads) void norm_affine_quant_kernel(NormArgs a) {
+// the scale table already holds bf16(1 + scale).  WT: weight dtype (NONE,
+// BF16, F32).  NORMED: also store the pre-quantization rows.
+template <int NORM, int OUT, int WT, int WPR, int CH, bool FULL, bool NORMED>
+__device__ __forceinline__ void norm_rows(const NormArgs &a, float *red_f, uint32_t *red_u) {
   constexpr bool kOnePlus = (NORM & XGEN_NORM_SCALE_ONE_PLUS) != 0;
   constexpr int kNorm = NORM & ~XGEN_NORM_SCALE_ONE_PLUS;
   constexpr int kRowsPerBlock = 4 / WPR;
-  __shared__ float red_f[4];
-  __shared__ uint32_t red_u[4];
-  const int wave = threadIdx.x >> 6;
+  // the wave index as a wave-uniform value: row indices and addresses are
+  // then computed by the scalar unit, loads and stores take a scalar base
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int lane_in_row = (wave % WPR) * 64 + lane;
-  const int nchunks = a.width >> 3;
   const int64_t step = (int64_t)gridDim.x * kRowsPerBlock;
-  auto chunk_ok = [&](int j) { return FULL || lane_in_row + j * 64 * WPR < nchunks; };
-
-  // one read of a row (zeros past the last row) and its table index
-  auto load_row = [&](int64_t row, u32x4 (&c)[CH], int64_t &g) {
-    const bool ok = row < a.rows;
-    const uint32_t r = ok ? (uint32_t)row : 0u;
-    const uint32_t b = fast_div(r, a.seq), s = r - b * a.seq.d;
-    const uint8_t *xr = a.x + (int64_t)b * a.xsb_bytes + (int64_t)s * a.xss_bytes;
+  const float inv_w = 1.0f / (float)a.width;
+  auto chunk_ok = [&](int j) { return FULL || lane_in_row + j * 64 * WPR < (a.width >> 3); };
+  // byte offset of chunk j of this lane in a bf16 row (chunk 0 when past the end)
+  auto chunk_off = [&](int j) -> uint32_t { return chunk_ok(j) ? (uint32_t)(lane_in_row + j * 64 * WPR) * 16u : 0u; };
+  auto clamp_row = [&](int64_t row) -> uint32_t { return (uint32_t)(row < a.rows ? row : a.rows - 1); };
+  // row r = b * seq + s: x row address and the token's index position s
+  auto x_row = [&](uint32_t r, uint32_t &s) {
+    const uint32_t b = fast_div(r, a.seq);
+    s = r - b * a.seq.d;
+    return a.x + (int64_t)b * a.xsb_bytes + (int64_t)s * a.xss_bytes;
+  };
+  // table indices through the constant address space: a scalar load (the
+  // index is wave-uniform), waited for only where the table rows are read
+  const __attribute__((address_space(4))) int64_t *indices =
+      (const __attribute__((address_space(4))) int64_t *)a.indices;
+  auto load_x = [&](const uint8_t *xr, u32x4 (&c)[CH]) {
+#pragma unroll
+    for (int j = 0; j < CH; ++j) c[j] = *reinterpret_cast<const u32x4 *>(xr + chunk_off(j));
+  };
+  // table rows of index g (row 0 stands in for an index outside the table)
+  u32x4 scw[CH], shw[CH];
+  Weight8<WT> wt[CH];
+  auto load_tables = [&](int64_t g) {
+    const int64_t gt = (g >= 0 && g < a.table_rows) ? g : 0;
+    const uint8_t *sr = a.scale_tab + gt * a.scale_stride_bytes;
+    const uint8_t *tr = a.shift_tab + gt * a.shift_stride_bytes;
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
-      const int ci = lane_in_row + j * 64 * WPR;
-      c[j] = (ok && chunk_ok(j)) ? *reinterpret_cast<const u32x4 *>(xr + (int64_t)ci * 16) : u32x4{0, 0, 0, 0};
+      scw[j] = *reinterpret_cast<const u32x4 *>(sr + chunk_off(j));
+      shw[j] = *reinterpret_cast<const u32x4 *>(tr + chunk_off(j));
+      if constexpr (WT != XGEN_DTYPE_NONE) wt[j].load(a.weight, (int)(chunk_off(j) >> 4));
     }
-    g = ok ? a.indices[s] : 0;
   };
 
   u32x4 c[CH];
-  int64_t g;
   int64_t base = (int64_t)blockIdx.x * kRowsPerBlock;
-  load_row(base + wave / WPR, c, g);
+  uint32_t s0;
+  const uint8_t *x0 = x_row(clamp_row(base + wave / WPR), s0);
+  int64_t g = indices[s0];
+  load_x(x0, c);
+  __builtin_amdgcn_sched_barrier(0);  // the same issue order as in the loop: x before the table rows
+  load_tables(g);
   for (; base < a.rows; base += step) {
-    const int64_t row = base + wave / WPR;
-    const bool row_ok = row < a.rows;
-    u32x4 cn[CH];
-    int64_t gn;
-    load_row(row + step, cn, gn);
-    const bool g_ok = g >= 0 && g < a.table_rows;
+    const uint32_t row = clamp_row(base + wave / WPR);
+    const bool g_ok = g >= 0 && g < a.table_rows;  // uniform over the wave (one row per wave)
 
-    // statistics (fp32, two passes over the packed row; chunks past the row's
-    // end are zeros and must stay out of the variance)
-    // the row as fp32, unpacked once for the statistics and the normalisation
-    float xv[CH][8];
+    // the next row's index, then its x
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t sn;
+    const uint8_t *xn = x_row(clamp_row(base + step + wave / WPR), sn);
+    const int64_t gn = indices[sn];
+    u32x4 cn[CH];
+    load_x(xn, cn);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (!FULL) {
 #pragma unroll
-    for (int j = 0; j < CH; ++j) unpack8<XGEN_DTYPE_BF16>(c[j], xv[j]);
+      for (int j = 0; j < CH; ++j)
+        if (!chunk_ok(j)) c[j] = u32x4{0, 0, 0, 0};
+    }
+
+    // statistics in fp32 (chunks past the row's end are zeros)
     float rstd, nmr = 0.0f;  // n = x * rstd + nmr
     if constexpr (kNorm == XGEN_NORM_LAYER) {
-      float acc = 0.0f;
-#pragma unroll
-      for (int j = 0; j < CH; ++j)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc += xv[j][i];
-      const float mean = row_sum<WPR>(acc, wave, lane, red_f) / (float)a.width;
-      float acc2 = 0.0f;
+      float s1[2] = {0.0f, 0.0f}, s2[2] = {0.0f, 0.0f};
 #pragma unroll
       for (int j = 0; j < CH; ++j) {
-        if (chunk_ok(j)) {
+        const uint32_t w[4] = {c[j].x, c[j].y, c[j].z, c[j].w};
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const float d = xv[j][i] - mean;
-            acc2 = __builtin_fmaf(d, d, acc2);
-          }
+        for (int k = 0; k < 4; ++k) {
+          s1[k & 1] = dot2_bf16(kBf16OnePair, w[k], s1[k & 1]);
+          s2[k & 1] = dot2_bf16(w[k], w[k], s2[k & 1]);
         }
       }
-      const float var = row_sum<WPR>(acc2, wave, lane, red_f) / (float)a.width;
-      rstd = 1.0f / __builtin_sqrtf(var + a.eps);
+      const RowMoments mo = row_moments<WPR>(s1[0] + s1[1], s2[0] + s2[1], wave, lane, red_f, inv_w);
+      const float mean = mo.s1 * inv_w;
+      float var = __builtin_fmaxf(mo.s2 * inv_w - mean * mean, 0.0f);
+      if (mo.two_pass_any) {  // uniform over the workgroup
+        float acc2 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+          if (chunk_ok(j)) {
+            float xv[8];
+            unpack8<XGEN_DTYPE_BF16>(c[j], xv);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              const float d = xv[i] - mean;
+              acc2 = __builtin_fmaf(d, d, acc2);
+            }
+          }
+        }
+        const float var2 = row_sum<WPR>(acc2, wave, lane, red_f) * inv_w;
+        if (mo.two_pass_here) var = var2;
+      }
+      rstd = __builtin_amdgcn_rsqf(var + a.eps);
       nmr = -mean * rstd;
     } else {
-      float acc2 = 0.0f;
+      float s2[2] = {0.0f, 0.0f};
 #pragma unroll
-      for (int j = 0; j < CH; ++j)
+      for (int j = 0; j < CH; ++j) {
+        const uint32_t w[4] = {c[j].x, c[j].y, c[j].z, c[j].w};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc2 = __builtin_fmaf(xv[j][i], xv[j][i], acc2);
-      const float ms = row_sum<WPR>(acc2, wave, lane, red_f) / (float)a.width;
-      rstd = 1.0f / __builtin_sqrtf(ms + a.eps);
+        for (int k = 0; k < 4; ++k) s2[k & 1] = dot2_bf16(w[k], w[k], s2[k & 1]);
+      }
+      const float ms = row_sum<WPR>(s2[0] + s2[1], wave, lane, red_f) * inv_w;
+      rstd = __builtin_amdgcn_rsqf(ms + a.eps);
     }
 
     // normalise, modulate with the table row, keep m as packed bf16 (in c);
     // bf16 roundings two at a time (one conversion per pair)
     u16x2 am = {0, 0};
-    if (row_ok && g_ok) {  // uniform over the wave (one row per wave)
-      const uint8_t *sr = a.scale_tab + g * a.scale_stride_bytes;
-      const uint8_t *tr = a.shift_tab + g * a.shift_stride_bytes;
 #pragma unroll
-      for (int j = 0; j < CH; ++j) {
-        const int ci = lane_in_row + j * 64 * WPR;
-        if (chunk_ok(j)) {
-          const u32x4 scw = *reinterpret_cast<const u32x4 *>(sr + (int64_t)ci * 16);
-          const u32x4 shw = *reinterpret_cast<const u32x4 *>(tr + (int64_t)ci * 16);
-          float n[8];
+    for (int j = 0; j < CH; ++j) {
+      float xv[8], n[8];
+      unpack8<XGEN_DTYPE_BF16>(c[j], xv);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) n[i] = __builtin_fmaf(xv[j][i], rstd, nmr);
-          if (a.weight_dtype != XGEN_DTYPE_NONE) {
-            float wv[8];
-            load_weight8(a.weight, a.weight_dtype, ci, wv);
+      for (int i = 0; i < 8; ++i) n[i] = __builtin_fmaf(xv[i], rstd, nmr);
+      if constexpr (WT != XGEN_DTYPE_NONE) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) n[i] *= wv[i];
-          }
-          const uint32_t scp[4] = {scw.x, scw.y, scw.z, scw.w}, shp[4] = {shw.x, shw.y, shw.z, shw.w};
-          uint32_t pk[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float n0 = n[2 * i], n1 = n[2 * i + 1];
-            round_bf16x2(n0, n1);
-            float f0 = Half2<XGEN_DTYPE_BF16>::lo(scp[i]), f1 = Half2<XGEN_DTYPE_BF16>::hi(scp[i]);
-            if constexpr (!kOnePlus) {
-              f0 += 1.0f, f1 += 1.0f;
-              round_bf16x2(f0, f1);
-            }
-            float p0 = n0 * f0, p1 = n1 * f1;
-            round_bf16x2(p0, p1);
-            pk[i] = pack_bf16x2(p0 + Half2<XGEN_DTYPE_BF16>::lo(shp[i]), p1 + Half2<XGEN_DTYPE_BF16>::hi(shp[i]));
-          }
-          c[j] = u32x4{pk[0], pk[1], pk[2], pk[3]};
-          am = absmax_chunk<XGEN_DTYPE_BF16>(c[j], am);
-        } else {
-          c[j] = u32x4{0, 0, 0, 0};
-        }
+        for (int i = 0; i < 8; ++i) n[i] *= wt[j].get(i);
       }
+      const uint32_t scp[4] = {scw[j].x, scw[j].y, scw[j].z, scw[j].w};
+      const uint32_t shp[4] = {shw[j].x, shw[j].y, shw[j].z, shw[j].w};
+      uint32_t pk[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float n0 = n[2 * i], n1 = n[2 * i + 1];
+        round_bf16x2(n0, n1);
+        float f0 = Half2<XGEN_DTYPE_BF16>::lo(scp[i]), f1 = Half2<XGEN_DTYPE_BF16>::hi(scp[i]);
+        if constexpr (!kOnePlus) {
+          f0 += 1.0f, f1 += 1.0f;
+          round_bf16x2(f0, f1);
+        }
+        float p0 = n0 * f0, p1 = n1 * f1;
+        round_bf16x2(p0, p1);
+        pk[i] = pack_bf16x2(p0 + Half2<XGEN_DTYPE_BF16>::lo(shp[i]), p1 + Half2<XGEN_DTYPE_BF16>::hi(shp[i]));
+      }
+      c[j] = chunk_ok(j) ? u32x4{pk[0], pk[1], pk[2], pk[3]} : u32x4{0, 0, 0, 0};
+      am = absmax_chunk<XGEN_DTYPE_BF16>(c[j], am);
     }
+    // the table rows are consumed: the next row's go into the same registers
+    __builtin_amdgcn_sched_barrier(0);
+    load_tables(gn);
+    __builtin_amdgcn_sched_barrier(0);
     const uint32_t amax_bits = row_max_u32<WPR>(hmax_u16x2(am), wave, lane, red_u);
 
-    // quantize from registers
-    if (row_ok) {
-      uint8_t *qr = a.q + row * (int64_t)a.width;
-      const float amax = Half2<XGEN_DTYPE_BF16>::from_absbits(amax_bits);
-      const RowQuant p = (OUT == XGEN_DTYPE_E4M3) ? fp8_row_params(amax) : i8_row_params(amax);
-      if (g_ok) {
-        uint8_t *nr = a.normed ? a.normed + row * (int64_t)a.width * 2 : nullptr;
+    // quantize from registers; a row whose index is outside the table is
+    // poisoned (NaN scale; NaN bytes for E4M3, zeros for I8; zero normed row)
+    const float amax = Half2<XGEN_DTYPE_BF16>::from_absbits(amax_bits);
+    const RowQuant p = (OUT == XGEN_DTYPE_E4M3) ? fp8_row_params(amax) : i8_row_params(amax);
+    const u32x2 bad = (OUT == XGEN_DTYPE_E4M3) ? u32x2{0x7f7f7f7fu, 0x7f7f7f7fu} : u32x2{0u, 0u};
+    uint8_t *qr = a.q + (int64_t)row * a.width;
 #pragma unroll
-        for (int j = 0; j < CH; ++j) {
-          const int ci = lane_in_row + j * 64 * WPR;
-          if (chunk_ok(j)) {
-            float v[8];
-            unpack8<XGEN_DTYPE_BF16>(c[j], v);
-            *reinterpret_cast<u32x2 *>(qr + (int64_t)ci * 8) = quant8<OUT>(c[j], v, p);
-            if (nr) *reinterpret_cast<u32x4 *>(nr + (int64_t)ci * 16) = c[j];
-          }
-        }
-        if (lane_in_row == 0) a.token_scale[row] = p.s;
-      } else {  // index outside the table: a poisoned row (NaN scale; NaN bytes or zeros)
-        const u32x2 bad = (OUT == XGEN_DTYPE_E4M3) ? u32x2{0x7f7f7f7fu, 0x7f7f7f7fu} : u32x2{0u, 0u};
-        uint8_t *nr = a.normed ? a.normed + row * (int64_t)a.width * 2 : nullptr;
-#pragma unroll
-        for (int j = 0; j < CH; ++j) {
-          const int ci = lane_in_row + j * 64 * WPR;
-          if (chunk_ok(j)) {
-            *reinterpret_cast<u32x2 *>(qr + (int64_t)ci * 8) = bad;
-            if (nr) *reinterpret_cast<u32x4 *>(nr + (int64_t)ci * 16) = u32x4{0, 0, 0, 0};
-          }
-        }
-        if (lane_in_row == 0) a.token_scale[row] = __builtin_nanf("");
+    for (int j = 0; j < CH; ++j) {
+      const uint32_t off = chunk_off(j);
+      float v[8];
+      unpack8<XGEN_DTYPE_BF16>(c[j], v);
+      const u32x2 qb = g_ok ? quant8<OUT>(c[j], v, p) : bad;
+      const u32x4 nb = g_ok ? c[j] : u32x4{0, 0, 0, 0};
+      if (chunk_ok(j)) {  // only the stores are masked (past a row's end, when not FULL)
+        *reinterpret_cast<u32x2 *>(qr + (off >> 1)) = qb;
+        if constexpr (NORMED) *reinterpret_cast<u32x4 *>(a.normed + (int64_t)row * a.width * 2 + off) = nb;
       }
     }
+    a.token_scale[row] = g_ok ? p.s : __builtin_nanf("");  // every lane of the row: the same value
 #pragma unroll
     for (int j = 0; j < CH; ++j) c[j] = cn[j];
     g = gn;
   }
 }
 
-template <int NORM, int OUT, int WPR, int CH, bool FULL>
+template <int NORM, int OUT, int WT, int WPR, int CH, bool FULL>
+__global__ __launch_bounds__(kThreads) void norm_affine_quant_kernel(NormArgs a) {
+  __shared__ float red_f[8];
+  __shared__ uint32_t red_u[4];
+  if (a.normed) norm_rows<NORM, OUT, WT, WPR, CH, FULL, true>(a, red_f, red_u);
+  else norm_rows<NORM, OUT, WT, WPR, CH, FULL, false>(a, red_f, red_u);
+}
+
+template <int NORM, int OUT, int WT, int WPR, int CH, bool FULL>
 void launch_kernel(const NormArgs &a, hipStream_t stream) {
   constexpr int kRowsPerBlock = 4 / WPR;
-  static const int per_cu = resident_blocks_per_cu(norm_affine_quant_kernel<NORM, OUT, WPR, CH, FULL>, kThreads);
+  static const int per_cu =
+      resident_blocks_per_cu(norm_affine_quant_kernel<NORM, OUT, WT, WPR, CH, FULL>, kThreads);
   const int64_t need = (a.rows + kRowsPerBlock - 1) / kRowsPerBlock;
   const int64_t cap = (int64_t)device_cu_count() * per_cu;
-  norm_affine_quant_kernel<NORM, OUT, WPR, CH, FULL>
+  norm_affine_quant_kernel<NORM, OUT, WT, WPR, CH, FULL>
       <<<dim3((unsigned)(need < cap ? need : cap)), dim3(kThreads), 0, stream>>>(a);
 }
 
-template <int NORM, int OUT, int WPR, int CH>
+// Rows without a weight (the AdaLN front end) get a variant without bounds
+// checks when the width fills the lanes exactly.
+template <int NORM, int OUT, int WT, int WPR, int CH>
 void launch(const NormArgs &a, hipStream_t stream) {
-  if (a.width == 512 * WPR * CH) launch_kernel<NORM, OUT, WPR, CH, true>(a, stream);
-  else launch_kernel<NORM, OUT, WPR, CH, false>(a, stream);
+  if constexpr (WT == XGEN_DTYPE_NONE) {
+    if (a.width == 512 * WPR * CH) return launch_kernel<NORM, OUT, WT, WPR, CH, true>(a, stream);
+  }
+  launch_kernel<NORM, OUT, WT, WPR, CH, false>(a, stream);
 }
 
-// Waves per row and chunks per lane by width: at most 4 chunks (32 values) per
-// lane keeps a wave's registers at occupancy >= 3; the row's reductions are
-// DPP shuffles plus one LDS exchange between the row's waves.
-template <int NORM, int OUT>
+// Waves per row and chunks per lane by width: up to 3072 one wave per row (no
+// barriers; at most 6 chunks = 48 values per lane), wider rows two or four
+// waves with one LDS exchange per reduction.
+template <int NORM, int OUT, int WT>
 void dispatch_width(const NormArgs &a, hipStream_t stream) {
   const int w = a.width;
-  if (w <= 1024) launch<NORM, OUT, 1, 2>(a, stream);
-  else if (w <= 2048) launch<NORM, OUT, 2, 2>(a, stream);
-  else if (w <= 3072) launch<NORM, OUT, 2, 3>(a, stream);
-  else if (w <= 4096) launch<NORM, OUT, 2, 4>(a, stream);
-  else if (w <= 6144) launch<NORM, OUT, 4, 3>(a, stream);
-  else launch<NORM, OUT, 4, 4>(a, stream);
+  if (w <= 1024) launch<NORM, OUT, WT, 1, 2>(a, stream);
+  else if (w <= 2048) launch<NORM, OUT, WT, 1, 4>(a, stream);
+  else if (w <= 3072) launch<NORM, OUT, WT, 1, 6>(a, stream);
+  else if (w <= 4096) launch<NORM, OUT, WT, 2, 4>(a, stream);
+  else if (w <= 6144) launch<NORM, OUT, WT, 2, 6>(a, stream);
+  else launch<NORM, OUT, WT, 4, 4>(a, stream);
+}
+
+template <int NORM, int OUT>
+void dispatch_weight(const NormArgs &a, int weight_dtype, hipStream_t stream) {
+  if (weight_dtype == XGEN_DTYPE_BF16) dispatch_width<NORM, OUT, XGEN_DTYPE_BF16>(a, stream);
+  else if (weight_dtype == XGEN_DTYPE_F32) dispatch_width<NORM, OUT, XGEN_DTYPE_F32>(a, stream);
+  else dispatch_width<NORM, OUT, XGEN_DTYPE_NONE>(a, stream);
 }
 
 }  // namespace
@@ -336,7 +445,6 @@ extern "C" int xgen_norm_affine_quant(const void *x, int64_t batch, int64_t seq,
   a.xsb_bytes = x_stride_batch * 2;
   a.xss_bytes = x_stride_seq * 2;
   a.weight = norm_weight;
-  a.weight_dtype = norm_weight_dtype;
   a.eps = eps;
   a.scale_tab = static_cast<const uint8_t *>(scale_table);
   a.scale_stride_bytes = scale_row_stride * 2;
@@ -351,20 +459,20 @@ extern "C" int xgen_norm_affine_quant(const void *x, int64_t batch, int64_t seq,
   const bool e4m3 = out_dtype == XGEN_DTYPE_E4M3;
   switch (norm_kind) {
     case XGEN_NORM_LAYER:
-      if (e4m3) dispatch_width<XGEN_NORM_LAYER, XGEN_DTYPE_E4M3>(a, stream);
-      else dispatch_width<XGEN_NORM_LAYER, XGEN_DTYPE_I8>(a, stream);
+      if (e4m3) dispatch_weight<XGEN_NORM_LAYER, XGEN_DTYPE_E4M3>(a, norm_weight_dtype, stream);
+      else dispatch_weight<XGEN_NORM_LAYER, XGEN_DTYPE_I8>(a, norm_weight_dtype, stream);
       break;
     case XGEN_NORM_RMS:
-      if (e4m3) dispatch_width<XGEN_NORM_RMS, XGEN_DTYPE_E4M3>(a, stream);
-      else dispatch_width<XGEN_NORM_RMS, XGEN_DTYPE_I8>(a, stream);
+      if (e4m3) dispatch_weight<XGEN_NORM_RMS, XGEN_DTYPE_E4M3>(a, norm_weight_dtype, stream);
+      else dispatch_weight<XGEN_NORM_RMS, XGEN_DTYPE_I8>(a, norm_weight_dtype, stream);
       break;
     case XGEN_NORM_LAYER | kP:
-      if (e4m3) dispatch_width<XGEN_NORM_LAYER | kP, XGEN_DTYPE_E4M3>(a, stream);
-      else dispatch_width<XGEN_NORM_LAYER | kP, XGEN_DTYPE_I8>(a, stream);
+      if (e4m3) dispatch_weight<XGEN_NORM_LAYER | kP, XGEN_DTYPE_E4M3>(a, norm_weight_dtype, stream);
+      else dispatch_weight<XGEN_NORM_LAYER | kP, XGEN_DTYPE_I8>(a, norm_weight_dtype, stream);
       break;
     default:
-      if (e4m3) dispatch_width<XGEN_NORM_RMS | kP, XGEN_DTYPE_E4M3>(a, stream);
-      else dispatch_width<XGEN_NORM_RMS | kP, XGEN_DTYPE_I8>(a, stream);
+      if (e4m3) dispatch_weight<XGEN_NORM_RMS | kP, XGEN_DTYPE_E4M3>(a, norm_weight_dtype, stream);
+      else dispatch_weight<XGEN_NORM_RMS | kP, XGEN_DTYPE_I8>(a, norm_weight_dtype, stream);
       break;
   }
   return launch_status(fn);
