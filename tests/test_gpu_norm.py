@@ -3,8 +3,10 @@
 Contract (the reductions of the norm are order-dependent in float32):
   * pre-quant bf16 rows m >= 99.9% bit-identical to the oracle (float64
     statistics, eager bf16 modulation); elsewhere the difference is what one
-    bf16 ulp of the normalised value n can become after the modulation:
-    |dm| <= ulp(bf16(n*f)) + ulp(m) (bf16(n*f) + shift may cancel, so ulps of
+    bf16 ulp of the normalised value n can become after the modulation: it
+    moves the exact n*f by |f| ulp(n) <= 2^-7 |n*f|, rounding bf16(n*f) can add
+    one more ulp, and rounding m one ulp of m, so
+    |dm| <= 2^-6 |n*f| + 2^-7 |m| (bf16(n*f) + shift may cancel, so ulps of
     m alone do not bound it);
   * quantized bytes and scales bit-exact given the kernel's own pre-quant rows.
 """
@@ -41,7 +43,7 @@ def check(x, weight, scale, shift, idx, eps, norm, out, q, s, m):
     nf = n * (1.0 + scale.cpu()[g])  # eager bf16: bf16(n * bf16(1 + scale))
     ulps = R.bf16_ulp_diff(m.cpu(), mr)
     assert (ulps == 0).float().mean() >= 0.999
-    bound = 2.0 ** -7 * (nf.double().abs() + mr.double().abs()) + 1e-30
+    bound = 2.0 ** -6 * nf.double().abs() + 2.0 ** -7 * mr.double().abs() + 1e-30
     assert ((m.cpu().double() - mr.double()).abs() <= bound).all()
     q2, s2 = (R.quantize_rows_fp8 if out == "fp8" else R.quantize_rows_int8)(m.cpu())
     if out == "fp8":
@@ -92,6 +94,34 @@ def test_out_of_range_index_poisons_only_its_row(cuda):
     q, s, _ = xops.norm_affine_quant(x, None, scale, shift, idx, 1e-6, N.NORM_LAYER, torch.float8_e4m3fn, True)
     assert torch.isnan(s[5]) and (q[5].view(torch.uint8) == 0x7F).all()
     assert torch.isfinite(s[torch.arange(8, device=cuda) != 5]).all()
+
+
+@pytest.mark.parametrize("H", [1000, 3072, 5376, 8192])
+def test_offset_and_constant_rows(cuda, H):
+    """Rows with a large common offset (the one-pass variance E[x^2] - mean^2 would cancel) take
+    the two-pass variance, next to ordinary rows in the same workgroup (one, two and four waves
+    per row); constant rows normalise to exactly zero, as the eager (x - mean) * rstd does, so
+    their modulated row is the shift row; every row's result is independent of its neighbours."""
+    g = torch.Generator().manual_seed(H)
+    S = 24
+    x = torch.randn(1, S, H, generator=g)
+    x[0, 1::3] += 6.0  # mean^2 ~ 36 of E[x^2] ~ 37: two-pass
+    const_rows, consts = list(range(2, S, 6)), [1.5, -3.0, 100.0, 0.0]
+    for r, c in zip(const_rows, consts):
+        x[0, r] = c
+    x = x.to(torch.bfloat16).to(cuda)
+    shift = (torch.randn((5, H), generator=g) * 0.1).to(torch.bfloat16).to(cuda)
+    scale = (torch.randn((5, H), generator=g) * 0.1).to(torch.bfloat16).to(cuda)
+    idx = torch.randint(5, (S,), generator=g).to(cuda)
+    q, s, m = xops.norm_affine_quant(x, None, scale, shift, idx, 1e-6, N.NORM_LAYER, torch.float8_e4m3fn, True)
+    check(x, None, scale, shift, idx, 1e-6, "layer", "fp8", q, s, m)
+    for r in const_rows:
+        assert torch.equal(m[r].view(torch.int16), shift[idx[r]].view(torch.int16))
+    for r in (0, 1, 2, 7):
+        q1, s1, m1 = xops.norm_affine_quant(x[:, r:r + 1], None, scale, shift, idx[r:r + 1], 1e-6, N.NORM_LAYER,
+                                            torch.float8_e4m3fn, True)
+        assert torch.equal(m1[0].view(torch.int16), m[r].view(torch.int16))
+        assert torch.equal(q1[0].view(torch.uint8), q[r].view(torch.uint8)) and torch.equal(s1[0], s[r])
 
 
 def test_full_size_front_end_c5_share(cuda):

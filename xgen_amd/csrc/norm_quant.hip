@@ -234,7 +234,7 @@ __device__ __forceinline__ void norm_rows(const NormArgs &a, float *red_f, uint3
     }
 
     // statistics in fp32 (chunks past the row's end are zeros)
-    float rstd, nmr = 0.0f;  // n = x * rstd + nmr
+    float rstd, mean = 0.0f;  // n = (x - mean) * rstd, as the eager LayerNorm computes it
     if constexpr (kNorm == XGEN_NORM_LAYER) {
       float s1[2] = {0.0f, 0.0f}, s2[2] = {0.0f, 0.0f};
 #pragma unroll
@@ -247,7 +247,10 @@ __device__ __forceinline__ void norm_rows(const NormArgs &a, float *red_f, uint3
         }
       }
       const RowMoments mo = row_moments<WPR>(s1[0] + s1[1], s2[0] + s2[1], wave, lane, red_f, inv_w);
-      const float mean = mo.s1 * inv_w;
+      // sum / width: the product with 1 / width plus one FMA correction, exact
+      // whenever the quotient is representable (a constant row's mean is its value)
+      const float mean0 = mo.s1 * inv_w;
+      mean = __builtin_fmaf(__builtin_fmaf(-mean0, (float)a.width, mo.s1), inv_w, mean0);
       float var = __builtin_fmaxf(mo.s2 * inv_w - mean * mean, 0.0f);
       if (mo.two_pass_any) {  // uniform over the workgroup
         float acc2 = 0.0f;
@@ -267,7 +270,6 @@ __device__ __forceinline__ void norm_rows(const NormArgs &a, float *red_f, uint3
         if (mo.two_pass_here) var = var2;
       }
       rstd = __builtin_amdgcn_rsqf(var + a.eps);
-      nmr = -mean * rstd;
     } else {
       float s2[2] = {0.0f, 0.0f};
 #pragma unroll
@@ -288,7 +290,7 @@ __device__ __forceinline__ void norm_rows(const NormArgs &a, float *red_f, uint3
       float xv[8], n[8];
       unpack8<XGEN_DTYPE_BF16>(c[j], xv);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) n[i] = __builtin_fmaf(xv[i], rstd, nmr);
+      for (int i = 0; i < 8; ++i) n[i] = (kNorm == XGEN_NORM_LAYER ? xv[i] - mean : xv[i]) * rstd;
       if constexpr (WT != XGEN_DTYPE_NONE) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) n[i] *= wt[j].get(i);
