@@ -2,10 +2,11 @@
 
 Contract (the reductions of the norm are order-dependent in float32):
   * pre-quant bf16 rows m >= 99.9% bit-identical to the oracle (float64
-    statistics, eager bf16 modulation); elsewhere the difference is what one
-    bf16 ulp of the normalised value n can become after the modulation: it
-    moves the exact n*f by |f| ulp(n) <= 2^-7 |n*f|, rounding bf16(n*f) can add
-    one more ulp, and rounding m one ulp of m, so
+    statistics, eager bf16 modulation) and >= 99.99% within one bf16 ulp;
+    elsewhere the difference is what one bf16 ulp of the normalised value n
+    can become after the modulation: it moves the exact n*f by
+    |f| ulp(n) <= 2^-7 |n*f|, rounding bf16(n*f) can add one more ulp, and
+    rounding m one ulp of m, so
     |dm| <= 2^-6 |n*f| + 2^-7 |m| (bf16(n*f) + shift may cancel, so ulps of
     m alone do not bound it);
   * quantized bytes and scales bit-exact given the kernel's own pre-quant rows.
@@ -43,6 +44,7 @@ def check(x, weight, scale, shift, idx, eps, norm, out, q, s, m):
     nf = n * (1.0 + scale.cpu()[g])  # eager bf16: bf16(n * bf16(1 + scale))
     ulps = R.bf16_ulp_diff(m.cpu(), mr)
     assert (ulps == 0).float().mean() >= 0.999
+    assert (ulps <= 1).float().mean() >= 0.9999
     bound = 2.0 ** -6 * nf.double().abs() + 2.0 ** -7 * mr.double().abs() + 1e-30
     assert ((m.cpu().double() - mr.double()).abs() <= bound).all()
     q2, s2 = (R.quantize_rows_fp8 if out == "fp8" else R.quantize_rows_int8)(m.cpu())
