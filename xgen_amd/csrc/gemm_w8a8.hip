@@ -38,8 +38,6 @@ constexpr int kStages = 4;                    // LDS ring depth
 constexpr int kTileBytes = 256 * BK;          // one operand tile of one stage: 16 KB
 constexpr int kStageBytes = 2 * kTileBytes;   // activations + weights: 32 KB
 constexpr int kGroupM = 8;
-constexpr int kBufferFlags = 0x00020000;  // raw buffer, 32-bit dword format (gfx9)
-constexpr uint32_t kOutOfRange = 0x80000000u;
 // instruction classes of __builtin_amdgcn_sched_group_barrier
 constexpr int kMfma = 0x008, kVmemRead = 0x020, kDsRead = 0x100;
 

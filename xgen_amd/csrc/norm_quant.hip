@@ -43,12 +43,10 @@ struct NormArgs {
   uint8_t *normed;  // optional bf16 [rows, width]
 };
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-
 // a.lo * b.lo + a.hi * b.hi + c on two packed bf16 pairs (v_dot2c_f32_bf16);
 // used only for the row statistics, whose rounding is not bit-specified.
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c,
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c,
                                          false);
 }
 constexpr uint32_t kBf16OnePair = 0x3f803f80u;

@@ -26,39 +26,46 @@ constexpr int kThreads = 256;  // 4 waves per workgroup
 // Streaming: a grid of a few workgroups per CU walks the rows (4 / WPR rows
 // per workgroup per step); each wave loads its next row before it reduces and
 // stores the current one, so loads stay in flight through the reduction.
+// gfx9 counts loads and stores with one in-order counter, so the loop's memory
+// accesses are all unconditional and the same on every path: rows go through
+// per-row buffer resources (chunks past a row's end load zeros, their stores
+// are dropped), rows past the end redo the last row (writing the same bytes as
+// its owner), and the first row is peeled so that the loop is entered as it is
+// repeated; the compiler's wait counts then name exactly the loads a step
+// needs.  The wave index is made wave-uniform, so row addresses are
+// scalar-unit work.
 template <int DT, int OUT, int WPR, int CH>
 __global__ __launch_bounds__(kThreads) void quant_rows_vec_kernel(
     const uint8_t *__restrict__ x, int64_t rows, int cols, int64_t ldx_bytes,
     uint8_t *__restrict__ q, int64_t ldq, float *__restrict__ scale) {
   constexpr int kRowsPerBlock = 4 / WPR;
   __shared__ uint32_t red[2][4];  // cross-wave max, double-buffered by step parity
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int row_in_block = wave / WPR;
-  const int wave_in_row = wave % WPR;
+  const int lane_in_row = (wave % WPR) * 64 + lane;
   const int nchunks = cols >> 3;
-  const int lane_in_row = wave_in_row * 64 + lane;
   const int64_t step = (int64_t)gridDim.x * kRowsPerBlock;
-
+  // byte offset of chunk j of this lane in an input row (kOutOfRange past the end)
+  auto in_off = [&](int j) -> uint32_t {
+    const int ci = lane_in_row + j * 64 * WPR;
+    return ci < nchunks ? (uint32_t)ci * 16u : kOutOfRange;
+  };
+  auto clamp_row = [&](int64_t row) { return row < rows ? row : rows - 1; };
   auto load_row = [&](int64_t row, u32x4 (&c)[CH]) {
-    const bool ok = row < rows;
-    const uint8_t *xr = x + (ok ? row : 0) * ldx_bytes;
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(x + clamp_row(row) * ldx_bytes), (short)0, cols * 2, kBufferFlags);
 #pragma unroll
-    for (int j = 0; j < CH; ++j) {
-      const int ci = lane_in_row + j * 64 * WPR;
-      c[j] = (ok && ci < nchunks) ? *reinterpret_cast<const u32x4 *>(xr + (int64_t)ci * 16) : u32x4{0, 0, 0, 0};
-    }
+    for (int j = 0; j < CH; ++j) c[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, in_off(j), 0, 0);
   };
 
-  u32x4 c[CH];
-  int parity = 0;
-  int64_t base = (int64_t)blockIdx.x * kRowsPerBlock;  // uniform over the workgroup
-  load_row(base + row_in_block, c);
-  for (; base < rows; base += step, parity ^= 1) {
-    const int64_t row = base + row_in_block;
-    u32x4 cn[CH];
-    load_row(row + step, cn);
-
+  u32x4 c[CH], cn[CH];
+  // one row: issue the next row's read, reduce, quantize from registers, store
+  auto row_step = [&](int64_t base, int parity) {
+    const int64_t row = clamp_row(base + row_in_block);
+    __builtin_amdgcn_sched_barrier(0);
+    load_row(base + step + row_in_block, cn);
+    __builtin_amdgcn_sched_barrier(0);
     u16x2 m = {0, 0};
 #pragma unroll
     for (int j = 0; j < CH; ++j) m = absmax_chunk<DT>(c[j], m);
@@ -70,24 +77,28 @@ __global__ __launch_bounds__(kThreads) void quant_rows_vec_kernel(
 #pragma unroll
       for (int i = 0; i < WPR; ++i) amax_bits = amax_bits > red[parity][w0 + i] ? amax_bits : red[parity][w0 + i];
     }
-    if (row < rows) {
-      const float amax = Half2<DT>::from_absbits(amax_bits);
-      const RowQuant p = (OUT == XGEN_DTYPE_E4M3) ? fp8_row_params(amax) : i8_row_params(amax);
-      uint8_t *qr = q + row * ldq;
+    const float amax = Half2<DT>::from_absbits(amax_bits);
+    const RowQuant p = (OUT == XGEN_DTYPE_E4M3) ? fp8_row_params(amax) : i8_row_params(amax);
+    const __amdgpu_buffer_rsrc_t rq =
+        __builtin_amdgcn_make_buffer_rsrc(q + row * ldq, (short)0, cols, kBufferFlags);
 #pragma unroll
-      for (int j = 0; j < CH; ++j) {
-        const int ci = lane_in_row + j * 64 * WPR;
-        if (ci < nchunks) {
-          float v[8];
-          unpack8<DT>(c[j], v);
-          *reinterpret_cast<u32x2 *>(qr + (int64_t)ci * 8) = quant8<OUT>(c[j], v, p);
-        }
-      }
-      if (lane_in_row == 0) scale[row] = p.s;
+    for (int j = 0; j < CH; ++j) {
+      float v[8];
+      unpack8<DT>(c[j], v);
+      // a chunk past the end: its offset stays past the row's bytes, the store is dropped
+      __builtin_amdgcn_raw_buffer_store_b64(quant8<OUT>(c[j], v, p), rq, in_off(j) >> 1, 0, 0);
     }
+    scale[row] = p.s;  // every lane of the row: the same value
 #pragma unroll
     for (int j = 0; j < CH; ++j) c[j] = cn[j];
-  }
+  };
+
+  int64_t base = (int64_t)blockIdx.x * kRowsPerBlock;  // uniform over the workgroup
+  load_row(base + row_in_block, c);
+  if (base >= rows) return;
+  row_step(base, 0);
+  base += step;
+  for (int parity = 1; base < rows; base += step, parity ^= 1) row_step(base, parity);
 }
 
 // Any width / alignment: one workgroup per row, two passes over global memory.

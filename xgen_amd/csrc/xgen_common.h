@@ -47,6 +47,12 @@ typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// Raw buffer resources (gfx9, 32-bit dword format): a load at an offset past
+// the resource's byte count returns zeros and such a store is dropped, so lanes
+// with nothing to move take the offset kOutOfRange instead of a branch.
+constexpr int kBufferFlags = 0x00020000;
+constexpr uint32_t kOutOfRange = 0x80000000u;
+
 constexpr float kE4M3Max = 448.0f;
 // torch.finfo(torch.float32).tiny, the clamp floor of the FP8 scale (h3_fp8.py:11).
 constexpr float kFltMin = 1.17549435082228750797e-38f;
