@@ -122,18 +122,21 @@ __device__ __forceinline__ uint32_t row_max_u32(uint32_t v, int wave, int lane, 
   return v;
 }
 
-// The 8 weights of chunk ci (WT = BF16 or F32) as fp32.
+// The 8 weights of one chunk (WT = BF16 or F32) as fp32, read through the
+// weight row's buffer resource (zeros past the row's end).
 template <int WT>
 struct Weight8 {
   static constexpr int kWords = WT == XGEN_DTYPE_F32 ? 8 : 4;
   uint32_t w[kWords];
-  __device__ __forceinline__ void load(const void *p, int ci) {
+  // off: byte offset of the chunk's bf16 elements (kOutOfRange past the end)
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     if constexpr (WT == XGEN_DTYPE_F32) {
-      const u32x4 *q = reinterpret_cast<const u32x4 *>(static_cast<const uint8_t *>(p) + (int64_t)ci * 32);
-      const u32x4 a = q[0], b = q[1];
+      const uint32_t o = off == kOutOfRange ? kOutOfRange : off * 2u;
+      const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, o, 0, 0);
+      const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(r, o == kOutOfRange ? o : o + 16u, 0, 0);
       w[0] = a.x, w[1] = a.y, w[2] = a.z, w[3] = a.w, w[4] = b.x, w[5] = b.y, w[6] = b.z, w[7] = b.w;
     } else if constexpr (WT == XGEN_DTYPE_BF16) {
-      const u32x4 a = *reinterpret_cast<const u32x4 *>(static_cast<const uint8_t *>(p) + (int64_t)ci * 16);
+      const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
       w[0] = a.x, w[1] = a.y, w[2] = a.z, w[3] = a.w;
     }
   }
@@ -149,32 +152,40 @@ struct Weight8 {
 // per wave: at the top of a step it issues the next row's table index and x
 // read; once the current row's modulation has consumed its table rows it
 // issues the next row's table (and weight) reads into the same registers; so
-// every read has about one step of work to hide behind.  Every memory access
-// of the loop is unconditional, so the compiler's wait counts name exactly
-// the loads a step needs: rows past the end redo the last row (writing the
-// same bytes as its owner), chunks past a row's end read chunk 0 and are
-// zeroed, a row whose index is outside the table reads table row 0 and
-// selects its poisoned output.
-// FULL: the row is exactly CH chunks per lane (width == 512 * WPR * CH), so
-// no chunk is past the end.
+// every read has about one step of work to hide behind.
+// gfx9 counts loads and stores with one in-order counter, so the loop's memory
+// accesses are unconditional and the same on every path: rows go through
+// buffer resources (chunks past a row's end load zeros, their stores are
+// dropped), rows past the end redo the last row (writing the same bytes as its
+// owner), a row whose index is outside the table reads table row 0 and selects
+// its poisoned output, and the first row is peeled so that the loop is entered
+// as it is repeated; the compiler's wait counts then name exactly the loads a
+// step needs.
 // NORM: XGEN_NORM_LAYER or XGEN_NORM_RMS, plus XGEN_NORM_SCALE_ONE_PLUS when
 // the scale table already holds bf16(1 + scale).  WT: weight dtype (NONE,
 // BF16, F32).  NORMED: also store the pre-quantization rows.
-template <int NORM, int OUT, int WT, int WPR, int CH, bool FULL, bool NORMED>
+template <int NORM, int OUT, int WT, int WPR, int CH, bool NORMED>
 __device__ __forceinline__ void norm_rows(const NormArgs &a, float *red_f, uint32_t *red_u) {
   constexpr bool kOnePlus = (NORM & XGEN_NORM_SCALE_ONE_PLUS) != 0;
   constexpr int kNorm = NORM & ~XGEN_NORM_SCALE_ONE_PLUS;
   constexpr int kRowsPerBlock = 4 / WPR;
   // the wave index as a wave-uniform value: row indices and addresses are
-  // then computed by the scalar unit, loads and stores take a scalar base
+  // then computed by the scalar unit
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int lane_in_row = (wave % WPR) * 64 + lane;
   const int64_t step = (int64_t)gridDim.x * kRowsPerBlock;
   const float inv_w = 1.0f / (float)a.width;
-  auto chunk_ok = [&](int j) { return FULL || lane_in_row + j * 64 * WPR < (a.width >> 3); };
-  // byte offset of chunk j of this lane in a bf16 row (chunk 0 when past the end)
-  auto chunk_off = [&](int j) -> uint32_t { return chunk_ok(j) ? (uint32_t)(lane_in_row + j * 64 * WPR) * 16u : 0u; };
+  const int row_bytes = a.width * 2;
+  const bool full = a.width == 512 * WPR * CH;  // no chunk past the row's end
+  auto chunk_ok = [&](int j) { return lane_in_row + j * 64 * WPR < (a.width >> 3); };
+  // byte offset of chunk j of this lane in a bf16 row (kOutOfRange past the end)
+  auto in_off = [&](int j) -> uint32_t {
+    return chunk_ok(j) ? (uint32_t)(lane_in_row + j * 64 * WPR) * 16u : kOutOfRange;
+  };
+  auto rsrc = [](const void *base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, bytes, kBufferFlags);
+  };
   auto clamp_row = [&](int64_t row) -> uint32_t { return (uint32_t)(row < a.rows ? row : a.rows - 1); };
   // row r = b * seq + s: x row address and the token's index position s
   auto x_row = [&](uint32_t r, uint32_t &s) {
@@ -187,33 +198,31 @@ __device__ __forceinline__ void norm_rows(const NormArgs &a, float *red_f, uint3
   const __attribute__((address_space(4))) int64_t *indices =
       (const __attribute__((address_space(4))) int64_t *)a.indices;
   auto load_x = [&](const uint8_t *xr, u32x4 (&c)[CH]) {
+    const __amdgpu_buffer_rsrc_t r = rsrc(xr, row_bytes);
 #pragma unroll
-    for (int j = 0; j < CH; ++j) c[j] = *reinterpret_cast<const u32x4 *>(xr + chunk_off(j));
+    for (int j = 0; j < CH; ++j) c[j] = __builtin_amdgcn_raw_buffer_load_b128(r, in_off(j), 0, 0);
   };
+  const __amdgpu_buffer_rsrc_t rw =
+      rsrc(a.weight, WT == XGEN_DTYPE_NONE ? 0 : a.width * (WT == XGEN_DTYPE_F32 ? 4 : 2));
   // table rows of index g (row 0 stands in for an index outside the table)
   u32x4 scw[CH], shw[CH];
   Weight8<WT> wt[CH];
   auto load_tables = [&](int64_t g) {
     const int64_t gt = (g >= 0 && g < a.table_rows) ? g : 0;
-    const uint8_t *sr = a.scale_tab + gt * a.scale_stride_bytes;
-    const uint8_t *tr = a.shift_tab + gt * a.shift_stride_bytes;
+    const __amdgpu_buffer_rsrc_t rs = rsrc(a.scale_tab + gt * a.scale_stride_bytes, row_bytes);
+    const __amdgpu_buffer_rsrc_t rt = rsrc(a.shift_tab + gt * a.shift_stride_bytes, row_bytes);
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
-      scw[j] = *reinterpret_cast<const u32x4 *>(sr + chunk_off(j));
-      shw[j] = *reinterpret_cast<const u32x4 *>(tr + chunk_off(j));
-      if constexpr (WT != XGEN_DTYPE_NONE) wt[j].load(a.weight, (int)(chunk_off(j) >> 4));
+      scw[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, in_off(j), 0, 0);
+      shw[j] = __builtin_amdgcn_raw_buffer_load_b128(rt, in_off(j), 0, 0);
+      if constexpr (WT != XGEN_DTYPE_NONE) wt[j].load(rw, in_off(j));
     }
   };
 
-  u32x4 c[CH];
-  int64_t base = (int64_t)blockIdx.x * kRowsPerBlock;
-  uint32_t s0;
-  const uint8_t *x0 = x_row(clamp_row(base + wave / WPR), s0);
-  int64_t g = indices[s0];
-  load_x(x0, c);
-  __builtin_amdgcn_sched_barrier(0);  // the same issue order as in the loop: x before the table rows
-  load_tables(g);
-  for (; base < a.rows; base += step) {
+  u32x4 c[CH], cn[CH];
+  int64_t g;
+  // one row (base: the workgroup's first row of this step)
+  auto row_step = [&](int64_t base) {
     const uint32_t row = clamp_row(base + wave / WPR);
     const bool g_ok = g >= 0 && g < a.table_rows;  // uniform over the wave (one row per wave)
 
@@ -222,14 +231,8 @@ __device__ __forceinline__ void norm_rows(const NormArgs &a, float *red_f, uint3
     uint32_t sn;
     const uint8_t *xn = x_row(clamp_row(base + step + wave / WPR), sn);
     const int64_t gn = indices[sn];
-    u32x4 cn[CH];
     load_x(xn, cn);
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (!FULL) {
-#pragma unroll
-      for (int j = 0; j < CH; ++j)
-        if (!chunk_ok(j)) c[j] = u32x4{0, 0, 0, 0};
-    }
 
     // statistics in fp32 (chunks past the row's end are zeros)
     float rstd, mean = 0.0f;  // n = (x - mean) * rstd, as the eager LayerNorm computes it
@@ -282,7 +285,6 @@ __device__ __forceinline__ void norm_rows(const NormArgs &a, float *red_f, uint3
 
     // normalise, modulate with the table row, keep m as packed bf16 (in c);
     // bf16 roundings two at a time (one conversion per pair)
-    u16x2 am = {0, 0};
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
       float xv[8], n[8];
@@ -309,9 +311,16 @@ __device__ __forceinline__ void norm_rows(const NormArgs &a, float *red_f, uint3
         round_bf16x2(p0, p1);
         pk[i] = pack_bf16x2(p0 + Half2<XGEN_DTYPE_BF16>::lo(shp[i]), p1 + Half2<XGEN_DTYPE_BF16>::hi(shp[i]));
       }
-      c[j] = chunk_ok(j) ? u32x4{pk[0], pk[1], pk[2], pk[3]} : u32x4{0, 0, 0, 0};
-      am = absmax_chunk<XGEN_DTYPE_BF16>(c[j], am);
+      c[j] = u32x4{pk[0], pk[1], pk[2], pk[3]};
     }
+    if (!full) {  // uniform: chunks past the row's end are zeros again (they stay out of the row max)
+#pragma unroll
+      for (int j = 0; j < CH; ++j)
+        if (!chunk_ok(j)) c[j] = u32x4{0, 0, 0, 0};
+    }
+    u16x2 am = {0, 0};
+#pragma unroll
+    for (int j = 0; j < CH; ++j) am = absmax_chunk<XGEN_DTYPE_BF16>(c[j], am);
     // the table rows are consumed: the next row's go into the same registers
     __builtin_amdgcn_sched_barrier(0);
     load_tables(gn);
@@ -323,53 +332,52 @@ __device__ __forceinline__ void norm_rows(const NormArgs &a, float *red_f, uint3
     const float amax = Half2<XGEN_DTYPE_BF16>::from_absbits(amax_bits);
     const RowQuant p = (OUT == XGEN_DTYPE_E4M3) ? fp8_row_params(amax) : i8_row_params(amax);
     const u32x2 bad = (OUT == XGEN_DTYPE_E4M3) ? u32x2{0x7f7f7f7fu, 0x7f7f7f7fu} : u32x2{0u, 0u};
-    uint8_t *qr = a.q + (int64_t)row * a.width;
+    const __amdgpu_buffer_rsrc_t rq = rsrc(a.q + (int64_t)row * a.width, a.width);
+    const __amdgpu_buffer_rsrc_t rn = rsrc(NORMED ? a.normed + (int64_t)row * row_bytes : a.q, NORMED ? row_bytes : 0);
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
-      const uint32_t off = chunk_off(j);
       float v[8];
       unpack8<XGEN_DTYPE_BF16>(c[j], v);
       const u32x2 qb = g_ok ? quant8<OUT>(c[j], v, p) : bad;
-      const u32x4 nb = g_ok ? c[j] : u32x4{0, 0, 0, 0};
-      if (chunk_ok(j)) {  // only the stores are masked (past a row's end, when not FULL)
-        *reinterpret_cast<u32x2 *>(qr + (off >> 1)) = qb;
-        if constexpr (NORMED) *reinterpret_cast<u32x4 *>(a.normed + (int64_t)row * a.width * 2 + off) = nb;
-      }
+      // a chunk past the end: its offset stays past the row's bytes, the stores are dropped
+      __builtin_amdgcn_raw_buffer_store_b64(qb, rq, in_off(j) >> 1, 0, 0);
+      if constexpr (NORMED)
+        __builtin_amdgcn_raw_buffer_store_b128(g_ok ? c[j] : u32x4{0, 0, 0, 0}, rn, in_off(j), 0, 0);
     }
     a.token_scale[row] = g_ok ? p.s : __builtin_nanf("");  // every lane of the row: the same value
 #pragma unroll
     for (int j = 0; j < CH; ++j) c[j] = cn[j];
     g = gn;
-  }
+  };
+
+  int64_t base = (int64_t)blockIdx.x * kRowsPerBlock;
+  uint32_t s0;
+  const uint8_t *x0 = x_row(clamp_row(base + wave / WPR), s0);
+  g = indices[s0];
+  load_x(x0, c);
+  __builtin_amdgcn_sched_barrier(0);
+  load_tables(g);
+  if (base >= a.rows) return;
+  row_step(base);  // peeled: the loop is then entered with the pending accesses of a step
+  for (base += step; base < a.rows; base += step) row_step(base);
 }
 
-template <int NORM, int OUT, int WT, int WPR, int CH, bool FULL>
+template <int NORM, int OUT, int WT, int WPR, int CH>
 __global__ __launch_bounds__(kThreads) void norm_affine_quant_kernel(NormArgs a) {
   __shared__ float red_f[8];
   __shared__ uint32_t red_u[4];
-  if (a.normed) norm_rows<NORM, OUT, WT, WPR, CH, FULL, true>(a, red_f, red_u);
-  else norm_rows<NORM, OUT, WT, WPR, CH, FULL, false>(a, red_f, red_u);
+  if (a.normed) norm_rows<NORM, OUT, WT, WPR, CH, true>(a, red_f, red_u);
+  else norm_rows<NORM, OUT, WT, WPR, CH, false>(a, red_f, red_u);
 }
 
-template <int NORM, int OUT, int WT, int WPR, int CH, bool FULL>
-void launch_kernel(const NormArgs &a, hipStream_t stream) {
-  constexpr int kRowsPerBlock = 4 / WPR;
-  static const int per_cu =
-      resident_blocks_per_cu(norm_affine_quant_kernel<NORM, OUT, WT, WPR, CH, FULL>, kThreads);
-  const int64_t need = (a.rows + kRowsPerBlock - 1) / kRowsPerBlock;
-  const int64_t cap = (int64_t)device_cu_count() * per_cu;
-  norm_affine_quant_kernel<NORM, OUT, WT, WPR, CH, FULL>
-      <<<dim3((unsigned)(need < cap ? need : cap)), dim3(kThreads), 0, stream>>>(a);
-}
-
-// Rows without a weight (the AdaLN front end) get a variant without bounds
-// checks when the width fills the lanes exactly.
 template <int NORM, int OUT, int WT, int WPR, int CH>
 void launch(const NormArgs &a, hipStream_t stream) {
-  if constexpr (WT == XGEN_DTYPE_NONE) {
-    if (a.width == 512 * WPR * CH) return launch_kernel<NORM, OUT, WT, WPR, CH, true>(a, stream);
-  }
-  launch_kernel<NORM, OUT, WT, WPR, CH, false>(a, stream);
+  constexpr int kRowsPerBlock = 4 / WPR;
+  static const int per_cu = resident_blocks_per_cu(norm_affine_quant_kernel<NORM, OUT, WT, WPR, CH>, kThreads);
+  const int64_t need = (a.rows + kRowsPerBlock - 1) / kRowsPerBlock;
+  const int64_t cap = (int64_t)device_cu_count() * per_cu;
+  norm_affine_quant_kernel<NORM, OUT, WT, WPR, CH>
+      <<<dim3((unsigned)(need < cap ? need : cap)), dim3(kThreads), 0, stream>>>(a);
 }
 
 // Waves per row and chunks per lane by width: up to 3072 one wave per row (no
