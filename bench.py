@@ -293,6 +293,24 @@ def main():
         kernels["front_end_ln_mod_quant_fp8_prepared_scale"] = {
             "ms": ms_fp, "gbs": fe_bytes / (ms_fp * 1e-3) / 1e9,
             "frac_of_hbm": fe_bytes / (ms_fp * 1e-3) / 1e9 / PEAK_HBM_GBS, "bytes": fe_bytes}
+        # the reference operator's own configuration (nq2: RMSNorm x weight, INT8 out) at H3 width
+        d3, g3 = 5376, W.generator(3, dev)  # its own stream: the other sections' inputs stay as they were
+        x3 = [torch.randn((1, M, d3), generator=g3, device=dev).to(torch.bfloat16) for _ in range(4)]
+        w3 = (1 + 0.1 * torch.randn(d3, generator=g3, device=dev)).to(torch.bfloat16)
+        sh3, sc3 = W.adaln_tables(20, d3, g3, dev)
+        st3 = {"i": 0}
+
+        def nxt3():
+            st3["i"] += 1
+            return x3[st3["i"] & 3]
+
+        ms_h3 = timed(lambda: xops.norm_affine_quant(nxt3(), w3, sc3, sh3, idx, 1e-5, N.NORM_RMS, torch.int8, False),
+                      args.steps, args.warmup)
+        h3_bytes = M * d3 * 2 + M * d3 + 4 * M + 8 * M
+        kernels["front_end_rms_weight_int8_h3"] = {
+            "ms": ms_h3, "gbs": h3_bytes / (ms_h3 * 1e-3) / 1e9,
+            "frac_of_hbm": h3_bytes / (ms_h3 * 1e-3) / 1e9 / PEAK_HBM_GBS, "bytes": h3_bytes}
+        del x3
 
     # ---- FFN GEMMs and INT8 QKV
     if want("ffn"):
