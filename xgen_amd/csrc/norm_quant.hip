@@ -151,8 +151,8 @@ struct Weight8 {
 // workgroup, so the cross-wave reductions stay in step).  Software pipeline
 // per wave: at the top of a step it issues the next row's table index and x
 // read; once the current row's modulation has consumed its table rows it
-// issues the next row's table (and weight) reads into the same registers; so
-// every read has about one step of work to hide behind.
+// issues the next row's table reads into the same registers; so every read
+// has about one step of work to hide behind (the weight is read once).
 // gfx9 counts loads and stores with one in-order counter, so the loop's memory
 // accesses are unconditional and the same on every path: rows go through
 // buffer resources (chunks past a row's end load zeros, their stores are
@@ -204,9 +204,14 @@ __device__ __forceinline__ void norm_rows(const NormArgs &a, float *red_f, uint3
   };
   const __amdgpu_buffer_rsrc_t rw =
       rsrc(a.weight, WT == XGEN_DTYPE_NONE ? 0 : a.width * (WT == XGEN_DTYPE_F32 ? 4 : 2));
+  // the weight is the same for every row: read once, kept in registers
+  Weight8<WT> wt[CH];
+  if constexpr (WT != XGEN_DTYPE_NONE) {
+#pragma unroll
+    for (int j = 0; j < CH; ++j) wt[j].load(rw, in_off(j));
+  }
   // table rows of index g (row 0 stands in for an index outside the table)
   u32x4 scw[CH], shw[CH];
-  Weight8<WT> wt[CH];
   auto load_tables = [&](int64_t g) {
     const int64_t gt = (g >= 0 && g < a.table_rows) ? g : 0;
     const __amdgpu_buffer_rsrc_t rs = rsrc(a.scale_tab + gt * a.scale_stride_bytes, row_bytes);
@@ -215,7 +220,6 @@ __device__ __forceinline__ void norm_rows(const NormArgs &a, float *red_f, uint3
     for (int j = 0; j < CH; ++j) {
       scw[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, in_off(j), 0, 0);
       shw[j] = __builtin_amdgcn_raw_buffer_load_b128(rt, in_off(j), 0, 0);
-      if constexpr (WT != XGEN_DTYPE_NONE) wt[j].load(rw, in_off(j));
     }
   };
 
