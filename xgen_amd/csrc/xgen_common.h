@@ -183,8 +183,18 @@ __device__ __forceinline__ uint32_t q_i8(float x, float alpha) {
   float y = __builtin_rintf(x * alpha);
   return (uint32_t)(int32_t)y & 0xffu;
 }
+// Four lane values as bytes, for finite products |x * alpha| <= 127.5 (the
+// row quantizer's, alpha = fl(127 / amax)): y = fl(x * alpha) plus 1.5 * 2^23
+// is rounded once, to the nearest integer with ties to even, and the sum's low
+// mantissa byte is rint(y) in two's complement (the sum lies in [2^23, 2^24));
+// v_perm_b32 gathers the four low bytes.  The product and the sum stay two
+// roundings (no FMA contraction), as rint(fl(x * alpha)) requires.
 __device__ __forceinline__ uint32_t pack_i8x4(float a, float b, float c, float d, float alpha) {
-  return q_i8(a, alpha) | (q_i8(b, alpha) << 8) | (q_i8(c, alpha) << 16) | (q_i8(d, alpha) << 24);
+#pragma clang fp contract(off)
+  constexpr float kRintMagic = 12582912.0f;  // 1.5 * 2^23
+  const uint32_t za = __float_as_uint(a * alpha + kRintMagic), zb = __float_as_uint(b * alpha + kRintMagic);
+  const uint32_t zc = __float_as_uint(c * alpha + kRintMagic), zd = __float_as_uint(d * alpha + kRintMagic);
+  return __builtin_amdgcn_perm(zb, za, 0x0c0c0400u) | __builtin_amdgcn_perm(zd, zc, 0x04000c0cu);
 }
 
 // --- wave64 reductions ---------------------------------------------------------
