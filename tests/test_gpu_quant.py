@@ -68,6 +68,22 @@ def test_row_quantizers_match_oracle(cuda, dtype, K, out):
     assert_same_quant(q, s, q_ref, s_ref)
 
 
+def test_every_bf16_amax_quotient(cuda):
+    """For every positive finite bf16 amax, the row's largest quotient amax / RN(amax / 448) may exceed
+    448 by an ulp or two; the quantizer does not clamp it and relies on the conversion rounding it to
+    448: bytes and scales equal the oracle's (which clamps) on rows [amax, -amax, 0.3 amax, ...]."""
+    bits = np.arange(1, 0x7F80, dtype=np.int32) << 16
+    a = torch.from_numpy(bits).view(torch.float32).to(torch.bfloat16)
+    x = torch.zeros(len(a), 16, dtype=torch.bfloat16)
+    x[:, 0], x[:, 1] = a, -a
+    x[:, 2:] = (a.float()[:, None] * torch.linspace(-0.99, 0.99, 14)).to(torch.bfloat16)
+    q, s = xops.quantize_rows(x.to(cuda), torch.float8_e4m3fn)
+    q_ref, s_ref = R.quantize_rows_c(x, "fp8")
+    assert_same_quant(q, s, q_ref, s_ref)
+    fast = a.float() >= 2.0 ** -100
+    assert (u8(q)[fast, 0] == 0x7E).all() and (u8(q)[fast, 1] == 0xFE).all()
+
+
 def test_row_quantizer_on_strided_rows(cuda):
     x = rows_with_edges(40, 1024, torch.bfloat16).to(cuda)
     view = x[:, 128:128 + 768]  # leading dimension 1024
