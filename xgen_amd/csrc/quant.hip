@@ -33,8 +33,9 @@ constexpr int kThreads = 256;  // 4 waves per workgroup
 // its owner), and the first row is peeled so that the loop is entered as it is
 // repeated; the compiler's wait counts then name exactly the loads a step
 // needs.  The wave index is made wave-uniform, so row addresses are
-// scalar-unit work.
-template <int DT, int OUT, int WPR, int CH>
+// scalar-unit work.  NT: the input is read non-temporally (calls larger than
+// the last-level cache).
+template <int DT, int OUT, int WPR, int CH, bool NT>
 __global__ __launch_bounds__(kThreads) void quant_rows_vec_kernel(
     const uint8_t *__restrict__ x, int64_t rows, int cols, int64_t ldx_bytes,
     uint8_t *__restrict__ q, int64_t ldq, float *__restrict__ scale) {
@@ -56,7 +57,7 @@ __global__ __launch_bounds__(kThreads) void quant_rows_vec_kernel(
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t *>(x + clamp_row(row) * ldx_bytes), (short)0, cols * 2, kBufferFlags);
 #pragma unroll
-    for (int j = 0; j < CH; ++j) c[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, in_off(j), 0, 0);
+    for (int j = 0; j < CH; ++j) c[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, in_off(j), 0, NT ? kCachePolicyNT : 0);
   };
 
   u32x4 c[CH], cn[CH];
@@ -138,18 +139,26 @@ __global__ __launch_bounds__(kThreads) void quant_rows_generic_kernel(
   if (threadIdx.x == 0) scale[row] = p.s;
 }
 
-template <int DT, int OUT, int WPR, int CH>
-void launch_vec(const void *x, int64_t rows, int64_t cols, int64_t ldx, void *q, int64_t ldq,
-                float *scale, hipStream_t stream) {
+template <int DT, int OUT, int WPR, int CH, bool NT>
+void launch_vec_policy(const void *x, int64_t rows, int64_t cols, int64_t ldx, void *q, int64_t ldq,
+                       float *scale, hipStream_t stream) {
   constexpr int kRowsPerBlock = 4 / WPR;
   // as many workgroups as are resident at once (a streaming grid must not queue)
-  static const int per_cu = resident_blocks_per_cu(quant_rows_vec_kernel<DT, OUT, WPR, CH>, kThreads);
+  static const int per_cu = resident_blocks_per_cu(quant_rows_vec_kernel<DT, OUT, WPR, CH, NT>, kThreads);
   const int64_t need = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
   const int64_t cap = (int64_t)device_cu_count() * per_cu;
   const int64_t blocks = need < cap ? need : cap;
-  quant_rows_vec_kernel<DT, OUT, WPR, CH><<<dim3((unsigned)blocks), dim3(kThreads), 0, stream>>>(
-      static_cast<const uint8_t *>(x), rows, (int)cols, ldx * 2, static_cast<uint8_t *>(q), ldq,
-      scale);
+  quant_rows_vec_kernel<DT, OUT, WPR, CH, NT><<<dim3((unsigned)blocks), dim3(kThreads), 0, stream>>>(
+      static_cast<const uint8_t *>(x), rows, (int)cols, ldx * 2, static_cast<uint8_t *>(q), ldq, scale);
+}
+
+template <int DT, int OUT, int WPR, int CH>
+void launch_vec(const void *x, int64_t rows, int64_t cols, int64_t ldx, void *q, int64_t ldq,
+                float *scale, hipStream_t stream) {
+  if (rows * cols * 3 > kLastLevelCacheBytes)  // 2 bytes read + 1 written per element
+    launch_vec_policy<DT, OUT, WPR, CH, true>(x, rows, cols, ldx, q, ldq, scale, stream);
+  else
+    launch_vec_policy<DT, OUT, WPR, CH, false>(x, rows, cols, ldx, q, ldq, scale, stream);
 }
 
 template <int DT, int OUT>

@@ -149,7 +149,8 @@ __global__ __launch_bounds__(256) void silu_table_kernel(uint16_t *table) {
   table[i] = (uint16_t)(__float_as_uint(a0) >> 16);
 }
 
-template <int OUT, int WPR, int CH>
+// NT: u is read non-temporally (calls larger than the last-level cache).
+template <int OUT, int WPR, int CH, bool NT>
 __global__ __launch_bounds__(kLutThreads) void swiglu_quant_lut_kernel(SwigluArgs a, const uint16_t *table) {
   constexpr int kWaves = kLutThreads / 64;
   constexpr int kRowsPerBlock = kWaves / WPR;
@@ -166,6 +167,11 @@ __global__ __launch_bounds__(kLutThreads) void swiglu_quant_lut_kernel(SwigluArg
   const int64_t step = (int64_t)gridDim.x * kRowsPerBlock;
   const int hoff = a.gate_first ? a.half * 2 : 0, goff = a.gate_first ? 0 : a.half * 2;  // bytes
 
+  auto load16 = [](const uint8_t *ptr) {
+    const u32x4 *v = reinterpret_cast<const u32x4 *>(ptr);
+    if constexpr (NT) return __builtin_nontemporal_load(v);
+    else return *v;
+  };
   auto load_row = [&](int64_t row, u32x4 (&h)[CH], u32x4 (&g)[CH]) {
     const bool ok = row < a.rows;
     const int64_t r = ok ? row : 0;
@@ -174,8 +180,8 @@ __global__ __launch_bounds__(kLutThreads) void swiglu_quant_lut_kernel(SwigluArg
     for (int j = 0; j < CH; ++j) {
       const int ci = lane_in_row + j * 64 * WPR;
       const bool in = ok && ci < nchunks;
-      h[j] = in ? *reinterpret_cast<const u32x4 *>(ur + hoff + (int64_t)ci * 16) : u32x4{0, 0, 0, 0};
-      g[j] = in ? *reinterpret_cast<const u32x4 *>(ur + goff + (int64_t)ci * 16) : u32x4{0, 0, 0, 0};
+      h[j] = in ? load16(ur + hoff + (int64_t)ci * 16) : u32x4{0, 0, 0, 0};
+      g[j] = in ? load16(ur + goff + (int64_t)ci * 16) : u32x4{0, 0, 0, 0};
     }
   };
 
@@ -243,8 +249,11 @@ void launch_lut(const SwigluArgs &a, const uint16_t *table, hipStream_t stream) 
   constexpr int kRowsPerBlock = kLutThreads / 64 / WPR;
   const int64_t need = (a.rows + kRowsPerBlock - 1) / kRowsPerBlock;
   const int64_t cap = device_cu_count();  // the 128 KB table: one workgroup per CU
-  swiglu_quant_lut_kernel<OUT, WPR, CH>
-      <<<dim3((unsigned)(need < cap ? need : cap)), dim3(kLutThreads), 0, stream>>>(a, table);
+  const dim3 grid((unsigned)(need < cap ? need : cap)), block(kLutThreads);
+  if (a.rows * (int64_t)a.half * 5 > kLastLevelCacheBytes)  // 4 bytes read + 1 written per output
+    swiglu_quant_lut_kernel<OUT, WPR, CH, true><<<grid, block, 0, stream>>>(a, table);
+  else
+    swiglu_quant_lut_kernel<OUT, WPR, CH, false><<<grid, block, 0, stream>>>(a, table);
 }
 
 // At most 4 chunks of 8 per lane (16 waves of a workgroup share the registers of a CU).
