@@ -64,9 +64,12 @@ __device__ __forceinline__ uint32_t group_max_u32(uint32_t v, int lanes) {
 // Accesses through byte addresses, marked as global memory (global_load /
 // global_store rather than flat).
 #define XGEN_GLOBAL __attribute__((address_space(1)))
-template <typename T>
+// NT: non-temporal load, for inputs streamed once through a call whose
+// footprint exceeds the last-level cache.
+template <typename T, bool NT = false>
 __device__ __forceinline__ T ld_global(const void *p) {
-  return *(const XGEN_GLOBAL T *)p;
+  if constexpr (NT) return __builtin_nontemporal_load((const XGEN_GLOBAL T *)p);
+  else return *(const XGEN_GLOBAL T *)p;
 }
 template <typename T>
 __device__ __forceinline__ void st_global(void *p, const T &v) {
@@ -121,15 +124,15 @@ struct Chunk {
   uint32_t w[kWords];
 };
 
-template <int DT, int E, bool ALIGNED>
+template <int DT, int E, bool ALIGNED, bool NT>
 __device__ __forceinline__ void load_chunk(const uint8_t *p, Chunk<DT, E> &c) {
   constexpr int kWords = Chunk<DT, E>::kWords;
   if constexpr (ALIGNED) {
     if constexpr (kWords == 2) {
-      const u32x2 v = ld_global<u32x2>(p);
+      const u32x2 v = ld_global<u32x2, NT>(p);
       c.w[0] = v.x, c.w[1] = v.y;
     } else {
-      const u32x4 v = ld_global<u32x4>(p);
+      const u32x4 v = ld_global<u32x4, NT>(p);
       c.w[0] = v.x, c.w[1] = v.y, c.w[2] = v.z, c.w[3] = v.w;
     }
   } else if constexpr (DT == XGEN_DTYPE_F32) {
@@ -212,7 +215,7 @@ __device__ __forceinline__ uint32_t quant4(const uint32_t *w, const WireScale &q
          (wire_byte_exact(v[3], q.s) << 24);
 }
 
-template <int DT, int E, bool ALIGNED, int C>
+template <int DT, int E, bool ALIGNED, int C, bool NT>
 __global__ __launch_bounds__(kThreads) void wire_encode_kernel(EncodeArgs a) {
   constexpr int kEb = Elem<DT>::kBytes;
   constexpr int kWords = Chunk<DT, E>::kWords;
@@ -249,7 +252,7 @@ __global__ __launch_bounds__(kThreads) void wire_encode_kernel(EncodeArgs a) {
     for (int j = 0; j < C; ++j) {
       const int e0 = (lig + j * lanes) * E;
       if (ok && e0 < a.width) {
-        load_chunk<DT, E, ALIGNED>(row + (int64_t)e0 * kEb, r.c[j]);
+        load_chunk<DT, E, ALIGNED, NT>(row + (int64_t)e0 * kEb, r.c[j]);
       } else {
 #pragma unroll
         for (int i = 0; i < kWords; ++i) r.c[j].w[i] = 0;
@@ -459,7 +462,14 @@ void launch_ec(const Args &a, const Shape &sh, hipStream_t stream) {
 }
 template <int DT, int E, bool ALIGNED, int C>
 struct EncodeK {
-  static constexpr auto kernel = wire_encode_kernel<DT, E, ALIGNED, C>;
+  static constexpr auto kernel = wire_encode_kernel<DT, E, ALIGNED, C, false>;
+};
+// Non-temporal input loads: 8% faster (H3 Q/K/V, 288 MB in + 149 MB out) once
+// a call's footprint exceeds the last-level cache; the decoder, whose input is
+// the smaller side, gains nothing from them.
+template <int DT, int E, bool ALIGNED, int C>
+struct EncodeNtK {
+  static constexpr auto kernel = wire_encode_kernel<DT, E, ALIGNED, C, true>;
 };
 template <int OT, int E, bool ALIGNED, int C>
 struct DecodeK {
@@ -551,17 +561,22 @@ extern "C" int xgen_fp8_wire_encode(int in_dtype, int streams, const void *q, co
   // chunks of 8 values (16-byte loads of 16-bit input) or 4 (16-byte f32 / 8-byte loads)
   const Shape sh = pick_shape((int)width, vec16 ? 8 : 4, kEncodeChunks);
   a.log2_lanes = sh.log2_lanes;
+  // bytes read and written by the call
+  const bool nt = (int64_t)a.g.total * (width * (eb + 1) + 4) > kLastLevelCacheBytes;
   switch (in_dtype) {
     case XGEN_DTYPE_BF16:
-      if (vec) launch_ec<EncodeK, XGEN_DTYPE_BF16, true>(a, sh, stream);
+      if (vec && nt) launch_ec<EncodeNtK, XGEN_DTYPE_BF16, true>(a, sh, stream);
+      else if (vec) launch_ec<EncodeK, XGEN_DTYPE_BF16, true>(a, sh, stream);
       else launch_ec<EncodeK, XGEN_DTYPE_BF16, false>(a, sh, stream);
       break;
     case XGEN_DTYPE_F16:
-      if (vec) launch_ec<EncodeK, XGEN_DTYPE_F16, true>(a, sh, stream);
+      if (vec && nt) launch_ec<EncodeNtK, XGEN_DTYPE_F16, true>(a, sh, stream);
+      else if (vec) launch_ec<EncodeK, XGEN_DTYPE_F16, true>(a, sh, stream);
       else launch_ec<EncodeK, XGEN_DTYPE_F16, false>(a, sh, stream);
       break;
     default:
-      if (vec) launch_ec<EncodeK, XGEN_DTYPE_F32, true>(a, sh, stream);
+      if (vec && nt) launch_ec<EncodeNtK, XGEN_DTYPE_F32, true>(a, sh, stream);
+      else if (vec) launch_ec<EncodeK, XGEN_DTYPE_F32, true>(a, sh, stream);
       else launch_ec<EncodeK, XGEN_DTYPE_F32, false>(a, sh, stream);
       break;
   }
