@@ -35,7 +35,7 @@ PEAK_INT8_TOPS = 5000.0    # MI355X dense INT8 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 # HBM (fabric) bytes per launch of the QKV GEMM, from rocprofv3 FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000
 # (copy-kernel calibration); profiles/hbm_traffic_c2_qkv_gemm_and_path_kernels.md holds the counts.
-QKV_GEMM_TRAFFIC_BYTES = (397598 * 2.0 + 281232 * 1.0) * 1024
+QKV_GEMM_TRAFFIC_BYTES = (419575 * 2.0 + 281232 * 1.0) * 1024
 METRIC = "FP8 W8A8 linear TFLOP/s (% MFMA peak) + quant GB/s, M=15.6k d=3072, 1 GPU"
 
 
@@ -53,8 +53,8 @@ def parse():
 
 
 PROFILE_KERNELS = ("gemm_fp8_qkv", "gemm_int8_qkv", "gemm_fp8_ffn_up_gelu", "gemm_fp8_ffn_down", "quant_rows_fp8",
-                   "front_end_ln_mod_quant_fp8", "gate_residual_op", "swiglu_quant_int8_h3", "wire_encode_h3",
-                   "wire_decode_h3", "copy_1gib")
+                   "requant_fp8_12288", "front_end_ln_mod_quant_fp8", "gate_residual_op", "swiglu_quant_int8_h3",
+                   "wire_encode_h3", "wire_decode_h3", "copy_1gib")
 
 
 def wire_setup(M, g, dev):
@@ -121,6 +121,9 @@ def profile_kernels(names, steps, warmup):
             fn = lambda: xops.scaled_mm(qa, qw, sa, sw, b, torch.bfloat16, act, False)  # noqa: E731
         elif name == "quant_rows_fp8":
             fn = lambda: xops.quantize_rows(nxt(), fp8)  # noqa: E731
+        elif name == "requant_fp8_12288":  # the FFN-down input: [M, 4d] bf16, 576 MB per call
+            hq = torch.randn((M, 4 * K), generator=g, device=dev).to(torch.bfloat16)
+            fn = lambda: xops.quantize_rows(hq, fp8)  # noqa: E731
         elif name == "gate_residual_op":
             res = torch.randn((1, M, K), generator=g, device=dev).to(torch.bfloat16)
             yb = torch.randn((1, M, K), generator=g, device=dev).to(torch.bfloat16)
