@@ -124,6 +124,20 @@ def test_pack_with_caller_scale(cuda):
     assert torch.equal(u8(q), R.canonical_nan_e4m3(ref).view(torch.uint8))
 
 
+def test_full_size_requant_k12288(cuda):
+    """The FFN-down requant at C3 size (M=15,624, K=12,288): the call moves 576 MB, more than the
+    256 MB last-level cache, so the quantizer takes its non-temporal-load form.  Bytes and scales
+    of every row against the oracle, FP8 and INT8."""
+    g = torch.Generator(device=cuda).manual_seed(12)
+    h = torch.randn((workloads.M_5S, 4 * workloads.D_MODEL), generator=g, device=cuda).to(torch.bfloat16)
+    h[7] *= 50
+    hc = h.cpu()
+    for out, dt in (("fp8", torch.float8_e4m3fn), ("int8", torch.int8)):
+        q, s = xops.quantize_rows(h, dt)
+        q_ref, s_ref = R.quantize_rows_c(hc, out)
+        assert_same_quant(q, s, q_ref, s_ref)
+
+
 def test_full_size_token_quant_c2(cuda):
     """C2 activations (M=15,624, K=3,072, outlier channels) quantized per token."""
     g = workloads.generator(0, cuda)

@@ -8,6 +8,7 @@ import torch
 
 import oracle.ref as R
 import xgen_amd  # noqa: F401
+from xgen_amd import workloads
 from xgen_amd.operator.matmul import WeightQuantLinearModule
 from xgen_amd.operator.swiglu_quant import swiglu_quant, swiglu_quantize_reuse
 
@@ -148,3 +149,23 @@ def test_table_path_equals_direct_path(cuda, out, F):
         assert torch.equal(q0.view(torch.uint8), q1.view(torch.uint8))
         assert torch.equal(s0.view(torch.int32), s1.view(torch.int32))
         assert torch.equal(a0.view(torch.int16), a1.view(torch.int16))
+
+
+@pytest.mark.parametrize("out", [torch.float8_e4m3fn, torch.int8])
+def test_h3_size_table_path(cuda, out):
+    """H3's FFN activation at full size (M=15,624, F=14,336): the call moves 1.12 GB, so the table
+    kernel takes its non-temporal-load form.  Every row equal to the per-element kernel's (ordinary
+    loads), and 64 seeded rows (first and last included) against the oracle."""
+    M, F = workloads.M_5S, 14336
+    g = torch.Generator(device=cuda).manual_seed(14)
+    u = (torch.randn((1, M, 2 * F), generator=g, device=cuda) * 2).to(torch.bfloat16)
+    q0, s0, a0 = _direct(u, False, out, 1)
+    q1, s1, a1 = xops.swiglu_quant(u, False, out, 1, True)
+    assert torch.equal(q0.view(torch.uint8), q1.view(torch.uint8))
+    assert torch.equal(s0.view(torch.int32), s1.view(torch.int32))
+    assert torch.equal(a0.view(torch.int16), a1.view(torch.int16))
+    del q0, s0, a0
+    rows = torch.randperm(M, generator=torch.Generator().manual_seed(3))[:64]
+    rows[0], rows[1] = 0, M - 1
+    rc = rows.to(cuda)
+    check(u[:, rc], False, out, 1, q1[rc], s1[rc], a1[rc])
