@@ -57,8 +57,9 @@ constexpr int kCachePolicyNT = 2;
 // MI355X's last-level (memory-side) cache.  A streaming call whose reads and
 // writes exceed it reads its input non-temporally: measured on the per-token
 // quantizer, ordinary loads are ~5% faster while the footprint fits (96-192 MB
-// inputs), non-temporal loads 14-16% faster beyond it (288-384 MB inputs) —
-// the input then no longer evicts the call's own output from that cache.
+// inputs; equal at 192 MB), non-temporal loads 14-16% faster beyond it
+// (288-384 MB inputs).  A likely reason: the streamed input then stops
+// evicting the call's own output lines from that cache.
 constexpr int64_t kLastLevelCacheBytes = 256ll << 20;
 
 constexpr float kE4M3Max = 448.0f;
