@@ -56,7 +56,7 @@ constexpr uint32_t kOutOfRange = 0x80000000u;
 constexpr int kCachePolicyNT = 2;
 // MI355X's last-level (memory-side) cache.  A streaming call whose reads and
 // writes exceed it reads its input non-temporally: measured on the per-token
-// quantizer, ordinary loads are ~5% faster while the footprint fits (96-192 MB
+// quantizer, ordinary loads are ~5% faster while the footprint fits (96-168 MB
 // inputs; equal at 192 MB), non-temporal loads 14-16% faster beyond it
 // (288-384 MB inputs).  A likely reason: the streamed input then stops
 // evicting the call's own output lines from that cache.
