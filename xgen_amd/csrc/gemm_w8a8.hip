@@ -37,7 +37,6 @@ constexpr int BK = 64;                        // K bytes per pipeline stage
 constexpr int kStages = 4;                    // LDS ring depth
 constexpr int kTileBytes = 256 * BK;          // one operand tile of one stage: 16 KB
 constexpr int kStageBytes = 2 * kTileBytes;   // activations + weights: 32 KB
-constexpr int kGroupM = 8;
 // instruction classes of __builtin_amdgcn_sched_group_barrier
 constexpr int kMfma = 0x008, kVmemRead = 0x020, kDsRead = 0x100;
 
@@ -59,6 +58,7 @@ struct GemmArgs {
   int64_t ldo;  // elements
   void *acc_out;
   int tiles_m, tiles_n, per_xcd;
+  int group_m;  // tile-rows per group of the tile order
   uint32_t a_bytes, w_bytes;
   // gated residual epilogue (GATED kernels only)
   const uint8_t *residual;
@@ -175,12 +175,12 @@ __device__ __forceinline__ float bias_at(const uint8_t *bias, int dtype, int n) 
   return dtype == XGEN_DTYPE_BF16 ? Half2<XGEN_DTYPE_BF16>::lo(h) : Half2<XGEN_DTYPE_F16>::lo(h);
 }
 
-// Output tile -> (m0, n0): tiles are walked in groups of kGroupM tile-rows.
-__device__ __forceinline__ void tile_origin(int pid, int tiles_m, int tiles_n, int &m0, int &n0) {
-  const int group_size = kGroupM * tiles_n;
+// Output tile -> (m0, n0): tiles are walked in groups of group_m tile-rows.
+__device__ __forceinline__ void tile_origin(int pid, int tiles_m, int tiles_n, int group_m, int &m0, int &n0) {
+  const int group_size = group_m * tiles_n;
   const int group = pid / group_size;
-  const int first_m = group * kGroupM;
-  const int gm = min(tiles_m - first_m, kGroupM);
+  const int first_m = group * group_m;
+  const int gm = min(tiles_m - first_m, group_m);
   const int in_group = pid - group * group_size;
   m0 = (first_m + in_group % gm) * BM;
   n0 = (in_group / gm) * BN;
@@ -269,7 +269,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) 
   uint32_t offa[kWaveLoads], offw[kWaveLoads];
   int dma_m0 = 0, dma_n0 = 0;
   auto set_dma_tile = [&](int i) {  // row offsets of my i-th tile
-    tile_origin(t_first + i * wgs_per_xcd, p.tiles_m, p.tiles_n, dma_m0, dma_n0);
+    tile_origin(t_first + i * wgs_per_xcd, p.tiles_m, p.tiles_n, p.group_m, dma_m0, dma_n0);
 #pragma unroll
     for (int l = 0; l < kWaveLoads; ++l) {
       const int r = wave * kRowsPerWave + l * 16 + (lane >> 2);
@@ -404,7 +404,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) 
     // acc[i][j] element e: feature n = n0 + wn*(BN/WN) + i*32 + (e/4)*8 + (lane/32)*4 + e%4,
     //                      token   m = m0 + wm*(BM/WM) + j*32 + lane%32.
     int m0, n0;
-    tile_origin(t_first + tile_i * wgs_per_xcd, p.tiles_m, p.tiles_n, m0, n0);
+    tile_origin(t_first + tile_i * wgs_per_xcd, p.tiles_m, p.tiles_n, p.group_m, m0, n0);
     uint8_t *prm = smem + kStages * kStageBytes + (tile_i % kParamSets) * kParamSetBytes;
     float *psa = reinterpret_cast<float *>(prm);
     float *psw = reinterpret_cast<float *>(prm + kParamBytes);
@@ -619,6 +619,11 @@ int gemm_entry(const char *fn, const void *a, int64_t lda, const void *w, int64_
   g.tiles_m = (int)((M + BM - 1) / BM);
   g.tiles_n = (int)((N + BN - 1) / BN);
   g.per_xcd = (g.tiles_m * g.tiles_n + 7) / 8;
+  // The 32 tiles one XCD runs at once span group_m tile-rows.  Measured at
+  // M=15,624, K=3,072: 4 rows beat 8 for wide outputs (QKV N=9,216 0.9%, FFN
+  // up N=12,288 2.8% faster), 8 beat 4 for the 12 tile-columns of FFN down
+  // (1.7%); 2 and 16 were slower than both.
+  g.group_m = g.tiles_n >= 24 ? 4 : 8;
   g.a_bytes = (uint32_t)a_bytes;
   g.w_bytes = (uint32_t)w_bytes;
   g.residual = static_cast<const uint8_t *>(gp.residual);
