@@ -622,7 +622,8 @@ int gemm_entry(const char *fn, const void *a, int64_t lda, const void *w, int64_
   // The 32 tiles one XCD runs at once span group_m tile-rows.  Measured at
   // M=15,624, K=3,072: 4 rows beat 8 for wide outputs (QKV N=9,216 0.9%, FFN
   // up N=12,288 2.8% faster), 8 beat 4 for the 12 tile-columns of FFN down
-  // (1.7%); 2 and 16 were slower than both.
+  // (1.7%); 2, 3, 6 and 16 were slower for the wide outputs, 6 and 12 no
+  // better than 8 for FFN down.
   g.group_m = g.tiles_n >= 24 ? 4 : 8;
   g.a_bytes = (uint32_t)a_bytes;
   g.w_bytes = (uint32_t)w_bytes;
