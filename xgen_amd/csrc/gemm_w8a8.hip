@@ -620,11 +620,11 @@ int gemm_entry(const char *fn, const void *a, int64_t lda, const void *w, int64_
   g.tiles_n = (int)((N + BN - 1) / BN);
   g.per_xcd = (g.tiles_m * g.tiles_n + 7) / 8;
   // The 32 tiles one XCD runs at once span group_m tile-rows.  Measured at
-  // M=15,624, K=3,072: 4 rows beat 8 for wide outputs (QKV N=9,216 0.9%, FFN
-  // up N=12,288 2.8% faster), 8 beat 4 for the 12 tile-columns of FFN down
-  // (1.7%); 2, 3, 6 and 16 were slower for the wide outputs, 6 and 12 no
-  // better than 8 for FFN down.
-  g.group_m = g.tiles_n >= 24 ? 4 : 8;
+  // M=15,624: 4 rows beat 8 for outputs of 24-63 tile-columns (QKV N=9,216
+  // 0.9%, FFN up N=12,288 2.8% faster); 8 beat 4 for FFN down's 12 (1.7%), and
+  // for H3's FFN up (N=28,672: 112 tile-columns, 2.5%); 2, 3, 6, 12 and 16
+  // were no better.
+  g.group_m = g.tiles_n >= 24 && g.tiles_n < 64 ? 4 : 8;
   g.a_bytes = (uint32_t)a_bytes;
   g.w_bytes = (uint32_t)w_bytes;
   g.residual = static_cast<const uint8_t *>(gp.residual);
