@@ -1,4 +1,5 @@
-"""Builds the oracle's C restatement (oracle/quant_ref.c) with gcc into
+"""Builds the oracle's C code (oracle/quant_ref.c, the quantizer restatement,
+and oracle/mfma_model.c, the model of gfx950's FP8 matrix sum) with gcc into
 oracle/_lib/liboracle_quant.so — test infrastructure only.
 
 No reference source is compiled: the reference's path is Python/Triton plus
@@ -12,7 +13,7 @@ import subprocess
 from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
-SRC = HERE / "quant_ref.c"
+SOURCES = (HERE / "quant_ref.c", HERE / "mfma_model.c")
 OUT = HERE / "_lib" / "liboracle_quant.so"
 
 
@@ -22,7 +23,7 @@ def build(verbose: bool = False) -> Path:
     tmp = OUT.with_suffix(".so.tmp")
     # -O2 without fast-math: IEEE float division, correctly rounded fmaf, no FTZ.
     cmd = [cc, "-O2", "-std=c11", "-fPIC", "-shared", "-fno-fast-math", "-ffp-contract=off",
-           str(SRC), "-o", str(tmp), "-lm"]
+           *map(str, SOURCES), "-o", str(tmp), "-lm"]
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"oracle build failed:\n{proc.stdout}")

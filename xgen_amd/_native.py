@@ -55,6 +55,9 @@ SIGNATURES = {
     "xgen_scaled_mm_fp8": (_c_int, [
         _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64,
         _c_ptr, _c_int, _c_int, _c_ptr, _c_int, _c_i64, _c_ptr, _c_ptr]),
+    "xgen_scaled_mm_fp8_exact": (_c_int, [
+        _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64,
+        _c_ptr, _c_int, _c_int, _c_ptr, _c_int, _c_i64, _c_ptr, _c_ptr]),
     "xgen_quant_matmul_int8": (_c_int, [
         _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64,
         _c_ptr, _c_int, _c_int, _c_ptr, _c_int, _c_i64, _c_ptr, _c_ptr]),

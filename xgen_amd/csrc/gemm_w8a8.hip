@@ -1,10 +1,21 @@
 // W8A8 GEMM with fused per-token x per-channel dequant, bias and optional
 // GELU-tanh epilogue, on gfx950 matrix cores.
 //
-//   FP8 : v_mfma_f32_32x32x64_f8f6f4 (e4m3fn x e4m3fn -> fp32)
-//         replaces torch._scaled_mm at x_base/x_base/operator/h3_fp8.py:63-66
-//   INT8: v_mfma_i32_32x32x32_i8      (int8 x int8 -> exact int32)
-//         replaces torch_npu.npu_quant_matmul at x_base/x_base/operator/matmul.py:63-64
+//   FP8      : v_mfma_f32_32x32x64_f8f6f4 (e4m3fn x e4m3fn -> fp32)
+//              replaces torch._scaled_mm at x_base/x_base/operator/h3_fp8.py:63-66
+//   FP8 exact: the same e4m3fn operands, converted to bf16 (exactly) after the
+//              LDS reads and multiplied by v_mfma_f32_32x32x16_bf16: exact
+//              products summed in fp32, the accumulation _scaled_mm's
+//              use_fast_accum=False asks for (h3_fp8.py:63-66), at twice the
+//              matrix-core time of the FP8 instructions
+//   INT8     : v_mfma_i32_32x32x32_i8      (int8 x int8 -> exact int32)
+//              replaces torch_npu.npu_quant_matmul at x_base/x_base/operator/matmul.py:63-64
+//
+// The FP8 instructions (all shapes, measured on gfx950) do not sum like IEEE
+// fp32: within each group of 8 consecutive K the products are truncated toward
+// zero to a multiple of 2^(E - 13), E the largest exponent sum e(a) + e(w) of
+// the group, so the result can differ from the exactly rounded sum by up to
+// ~2^-13 of the group's largest product.  The FP8-exact kind avoids that sum.
 //
 // out[m, n] = act(cvt(acc[m, n] * (sa[m] * sw[n]) + bias[n])),  acc = sum_k a[m,k] w[n,k]
 //
@@ -79,11 +90,14 @@ __device__ __forceinline__ int swz(int row, int chunk) {
   return row * BK + ((chunk ^ ((row >> 2) & 3)) << 4);
 }
 
-template <bool FP8>
+// Operand kinds of the kernel template.
+enum Kind { kInt8 = 0, kFp8 = 1, kFp8Exact = 2 };
+
+template <int KIND>
 struct Mfma;
 
 template <>
-struct Mfma<true> {
+struct Mfma<kFp8> {
   typedef f32x16 acc_t;
   typedef i32x8 frag_t;
   static constexpr int kSteps = BK / 64;  // 32x32x64: one step per stage
@@ -99,10 +113,47 @@ struct Mfma<true> {
     return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w, x, c, 0, 0, 0, 0, 0, 0);
   }
   static __device__ __forceinline__ float to_f32(float v) { return v; }
+  static constexpr int kMfmaPerMma = 1;
+};
+
+// e4m3fn bytes of one fragment (32 per lane, the FP8 kind's LDS reads) as four
+// 32x32x16 bf16 MFMAs: step s takes bytes 8s..8s+7 of each lane's 32, from both
+// operands alike, so every product pairs the same K index of the two.  The
+// conversion is exact (bf16 holds every e4m3fn value, subnormals included).
+template <>
+struct Mfma<kFp8Exact> {
+  typedef f32x16 acc_t;
+  typedef i32x8 frag_t;
+  static constexpr int kSteps = 1;
+  static constexpr int kReads = 2;
+  static __device__ __forceinline__ frag_t load(const uint8_t *tile, int row, int ks, int lane) {
+    return Mfma<kFp8>::load(tile, row, ks, lane);
+  }
+  static __device__ __forceinline__ bf16x8 widen(int lo, int hi) {
+    const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false);
+    const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true);
+    const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false);
+    const bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true);
+    return bf16x8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+  }
+  // Each call converts its own copies: shared across the calls of a stage the
+  // converted weight fragments would stay live (32 more registers) and spill.
+  static __device__ __forceinline__ acc_t mma(const frag_t &w, const frag_t &x, const acc_t &c) {
+    acc_t r = c;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      int w0 = w[2 * s], w1 = w[2 * s + 1];
+      asm volatile("" : "+v"(w0), "+v"(w1));
+      r = __builtin_amdgcn_mfma_f32_32x32x16_bf16(widen(w0, w1), widen(x[2 * s], x[2 * s + 1]), r, 0, 0, 0);
+    }
+    return r;
+  }
+  static __device__ __forceinline__ float to_f32(float v) { return v; }
+  static constexpr int kMfmaPerMma = 4;
 };
 
 template <>
-struct Mfma<false> {
+struct Mfma<kInt8> {
   typedef i32x16 acc_t;
   typedef i32x4 frag_t;
   static constexpr int kSteps = BK / 32;  // 32x32x32: two steps per stage
@@ -116,6 +167,7 @@ struct Mfma<false> {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(w, x, c, 0, 0, 0);
   }
   static __device__ __forceinline__ float to_f32(int v) { return (float)v; }
+  static constexpr int kMfmaPerMma = 1;
 };
 
 // One 16-byte-per-lane buffer load on the LDS-DMA path: lane l's 16 bytes land
@@ -211,9 +263,9 @@ constexpr int kParamSets = kStages + 1;
 constexpr int kLdsBytes = kStages * kStageBytes + kParamSets * kParamSetBytes;
 
 // GATED: the bf16 output y feeds out = bf16(residual + bf16(y * gate[indices[m % seq]])).
-template <bool FP8, int ACT, int OUT_DT, bool ACC_OUT, int WM, int WN, bool GATED = false>
+template <int KIND, int ACT, int OUT_DT, bool ACC_OUT, int WM, int WN, bool GATED = false>
 __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) {
-  typedef Mfma<FP8> T;
+  typedef Mfma<KIND> T;
   constexpr int kWaves = WM * WN;
   constexpr int FM = BM / WM / 32;               // activation (token) fragments per wave
   constexpr int FN = BN / WN / 32;               // weight (feature) fragments per wave
@@ -393,7 +445,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) 
     __builtin_amdgcn_sched_group_barrier(kDsRead, T::kReads * T::kSteps * FN, 0);
 #pragma unroll
     for (int k = 0; k < kSlots; ++k) {
-      __builtin_amdgcn_sched_group_barrier(kMfma, FN, 0);
+      __builtin_amdgcn_sched_group_barrier(kMfma, FN * T::kMfmaPerMma, 0);
       __builtin_amdgcn_sched_group_barrier(kDsRead, T::kReads, 0);
       if (k % kEvery == 0) __builtin_amdgcn_sched_group_barrier(kVmemRead, kPerSlot, 0);
     }
@@ -455,7 +507,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) 
           if constexpr (ACC_OUT) {
             const int m = m0 + ml, n = n0 + nl;
             if (m < p.M && n < p.N) {
-              if constexpr (FP8) {
+              if constexpr (KIND != kInt8) {
                 const f32x4 v = {acc[i][j][gq * 4 + 0], acc[i][j][gq * 4 + 1], acc[i][j][gq * 4 + 2],
                                  acc[i][j][gq * 4 + 3]};
                 *reinterpret_cast<f32x4 *>(static_cast<float *>(p.acc_out) + (int64_t)m * p.N + n) = v;
@@ -535,16 +587,16 @@ dim3 gemm_grid(const GemmArgs &a) {
   return dim3((unsigned)wgs);
 }
 
-template <bool FP8, int ACT, int OUT_DT>
+template <int KIND, int ACT, int OUT_DT>
 void launch_gemm(const GemmArgs &a, bool acc_out, hipStream_t stream) {
   const dim3 grid = gemm_grid(a), block(64 * kWavesM * kWavesN);
-  if (acc_out) gemm_w8a8_kernel<FP8, ACT, OUT_DT, true, kWavesM, kWavesN><<<grid, block, 0, stream>>>(a);
-  else gemm_w8a8_kernel<FP8, ACT, OUT_DT, false, kWavesM, kWavesN><<<grid, block, 0, stream>>>(a);
+  if (acc_out) gemm_w8a8_kernel<KIND, ACT, OUT_DT, true, kWavesM, kWavesN><<<grid, block, 0, stream>>>(a);
+  else gemm_w8a8_kernel<KIND, ACT, OUT_DT, false, kWavesM, kWavesN><<<grid, block, 0, stream>>>(a);
 }
 
-template <bool FP8>
+template <int KIND>
 void launch_gemm_gated(const GemmArgs &a, hipStream_t stream) {
-  gemm_w8a8_kernel<FP8, XGEN_ACT_NONE, XGEN_DTYPE_BF16, false, kWavesM, kWavesN, true>
+  gemm_w8a8_kernel<KIND, XGEN_ACT_NONE, XGEN_DTYPE_BF16, false, kWavesM, kWavesN, true>
       <<<gemm_grid(a), dim3(64 * kWavesM * kWavesN), 0, stream>>>(a);
 }
 
@@ -557,7 +609,7 @@ struct GateParams {  // the gated residual epilogue's inputs (null residual: pla
   int64_t seq = 0;
 };
 
-template <bool FP8>
+template <int KIND>
 int gemm_entry(const char *fn, const void *a, int64_t lda, const void *w, int64_t ldw, int64_t M,
                int64_t N, int64_t K, const float *sa, int64_t sa_stride, const float *sw,
                int64_t sw_stride, const void *bias, int bias_dtype, int activation, void *out,
@@ -636,13 +688,13 @@ int gemm_entry(const char *fn, const void *a, int64_t lda, const void *w, int64_
   g.seq = (uint32_t)gp.seq;
   const bool with_acc = acc_out != nullptr;
   if (gated) {
-    launch_gemm_gated<FP8>(g, stream);
+    launch_gemm_gated<KIND>(g, stream);
   } else if (activation == XGEN_ACT_NONE) {
-    if (out_dtype == XGEN_DTYPE_BF16) launch_gemm<FP8, XGEN_ACT_NONE, XGEN_DTYPE_BF16>(g, with_acc, stream);
-    else launch_gemm<FP8, XGEN_ACT_NONE, XGEN_DTYPE_F16>(g, with_acc, stream);
+    if (out_dtype == XGEN_DTYPE_BF16) launch_gemm<KIND, XGEN_ACT_NONE, XGEN_DTYPE_BF16>(g, with_acc, stream);
+    else launch_gemm<KIND, XGEN_ACT_NONE, XGEN_DTYPE_F16>(g, with_acc, stream);
   } else {
-    if (out_dtype == XGEN_DTYPE_BF16) launch_gemm<FP8, XGEN_ACT_GELU_TANH, XGEN_DTYPE_BF16>(g, with_acc, stream);
-    else launch_gemm<FP8, XGEN_ACT_GELU_TANH, XGEN_DTYPE_F16>(g, with_acc, stream);
+    if (out_dtype == XGEN_DTYPE_BF16) launch_gemm<KIND, XGEN_ACT_GELU_TANH, XGEN_DTYPE_BF16>(g, with_acc, stream);
+    else launch_gemm<KIND, XGEN_ACT_GELU_TANH, XGEN_DTYPE_F16>(g, with_acc, stream);
   }
   return launch_status(fn);
 }
@@ -658,9 +710,19 @@ extern "C" int xgen_scaled_mm_fp8(const void *a, int64_t lda, const void *w, int
                                   const float *w_scale, int64_t w_scale_stride, const void *bias,
                                   int bias_dtype, int activation, void *out, int out_dtype,
                                   int64_t ldo, float *acc_out, hipStream_t stream) {
-  return gemm_entry<true>("xgen_scaled_mm_fp8", a, lda, w, ldw, M, N, K, a_scale, a_scale_stride,
+  return gemm_entry<kFp8>("xgen_scaled_mm_fp8", a, lda, w, ldw, M, N, K, a_scale, a_scale_stride,
                           w_scale, w_scale_stride, bias, bias_dtype, activation, out, out_dtype, ldo,
                           acc_out, stream);
+}
+
+extern "C" int xgen_scaled_mm_fp8_exact(const void *a, int64_t lda, const void *w, int64_t ldw, int64_t M,
+                                        int64_t N, int64_t K, const float *a_scale, int64_t a_scale_stride,
+                                        const float *w_scale, int64_t w_scale_stride, const void *bias,
+                                        int bias_dtype, int activation, void *out, int out_dtype,
+                                        int64_t ldo, float *acc_out, hipStream_t stream) {
+  return gemm_entry<kFp8Exact>("xgen_scaled_mm_fp8_exact", a, lda, w, ldw, M, N, K, a_scale, a_scale_stride,
+                               w_scale, w_scale_stride, bias, bias_dtype, activation, out, out_dtype, ldo,
+                               acc_out, stream);
 }
 
 extern "C" int xgen_quant_matmul_int8(const void *a, int64_t lda, const void *w, int64_t ldw,
@@ -669,7 +731,7 @@ extern "C" int xgen_quant_matmul_int8(const void *a, int64_t lda, const void *w,
                                       int64_t w_scale_stride, const void *bias, int bias_dtype,
                                       int activation, void *out, int out_dtype, int64_t ldo,
                                       int32_t *acc_out, hipStream_t stream) {
-  return gemm_entry<false>("xgen_quant_matmul_int8", a, lda, w, ldw, M, N, K, pertoken_scale,
+  return gemm_entry<kInt8>("xgen_quant_matmul_int8", a, lda, w, ldw, M, N, K, pertoken_scale,
                            pertoken_scale_stride, w_scale, w_scale_stride, bias, bias_dtype,
                            activation, out, out_dtype, ldo, acc_out, stream);
 }
@@ -694,8 +756,8 @@ extern "C" int xgen_w8a8_gate_residual(int in_dtype, const void *a, int64_t lda,
   gp.indices = indices;
   gp.seq = seq;
   if (in_dtype == XGEN_DTYPE_E4M3)
-    return gemm_entry<true>(fn, a, lda, w, ldw, M, N, K, a_scale, a_scale_stride, w_scale, w_scale_stride, bias,
+    return gemm_entry<kFp8>(fn, a, lda, w, ldw, M, N, K, a_scale, a_scale_stride, w_scale, w_scale_stride, bias,
                             bias_dtype, XGEN_ACT_NONE, out, XGEN_DTYPE_BF16, ldo, nullptr, stream, gp);
-  return gemm_entry<false>(fn, a, lda, w, ldw, M, N, K, a_scale, a_scale_stride, w_scale, w_scale_stride, bias,
+  return gemm_entry<kInt8>(fn, a, lda, w, ldw, M, N, K, a_scale, a_scale_stride, w_scale, w_scale_stride, bias,
                            bias_dtype, XGEN_ACT_NONE, out, XGEN_DTYPE_BF16, ldo, nullptr, stream, gp);
 }

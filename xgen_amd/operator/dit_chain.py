@@ -15,6 +15,13 @@ every later projection quantizes its own input per token:
     h    = ff_up(o)  with the GELU-tanh epilogue         # [M, 4d]
     y    = ff_down(h)                                    # [M, d]
 
+``accumulation`` ("mfma" or "exact") is passed to the four linears.  Each
+per-token requantization can turn a last-bit difference of its bf16 input
+into a different e4m3 rounding, so differences in the GEMMs' sums grow along
+the chain: with the FP8 MFMA's truncating sum (the numerics of every FP8 GEMM
+on this GPU, torch._scaled_mm's included) the FFN output of C5 sits at
+rel-L2 ~2e-2 from the exactly summed chain, with "exact" at ~4e-4.
+
 Attention is outside this path; without a callable the V third of the QKV
 output stands in for it (the out-projection then sees a real [M, d] bf16
 activation of the right statistics).  Residual adds and gates are left to the
@@ -33,9 +40,10 @@ class DiTLinearChain(nn.Module):
     """QKV, out-projection, FFN up (GELU-tanh) and FFN down as W8A8 FP8
     linears with per-channel weight and per-token activation scales."""
 
-    def __init__(self, w_qkv, b_qkv, w_out, b_out, w_up, b_up, w_down, b_down, *, eps: float = 1e-6):
+    def __init__(self, w_qkv, b_qkv, w_out, b_out, w_up, b_up, w_down, b_down, *, eps: float = 1e-6,
+                 accumulation: str = "mfma"):
         super().__init__()
-        opts = dict(weight_scaling="channel", activation_scaling="token")
+        opts = dict(weight_scaling="channel", activation_scaling="token", accumulation=accumulation)
         self.qkv = H3FP8Linear(w_qkv, b_qkv, **opts)
         self.out = H3FP8Linear(w_out, b_out, **opts)
         self.ff_up = H3FP8Linear(w_up, b_up, activation="gelu_tanh", **opts)

@@ -12,6 +12,14 @@ per call.  ``weight_scaling="channel"`` keeps one scale per output feature
 one scale per token: the W8A8 layout of the DiT linear path.  The GEMM and its
 dequant / bias / optional GELU-tanh epilogue are one HIP kernel; rows need no
 padding to 16 (the reference pads, h3_fp8.py:58-59).
+
+``accumulation`` picks how the K sums are formed.  "mfma" (default) uses
+gfx950's FP8 MFMA, whose sum truncates each product of a group of 8
+consecutive K to a multiple of 2^(E - 13), E the group's largest exponent sum
+(torch._scaled_mm computes the same on this GPU).  "exact" multiplies the same
+e4m3fn bytes exactly on the bf16 MFMA and sums in fp32: the accumulation the
+reference requests with use_fast_accum=False (h3_fp8.py:63-66), at twice the
+matrix-core time.
 """
 from __future__ import annotations
 
@@ -24,6 +32,7 @@ from .h3_fp8_quant import quantize_activation, quantize_activation_rows
 
 _FP8_MAX = 448.0
 _ACTIVATIONS = {None: N.ACT_NONE, "none": N.ACT_NONE, "gelu_tanh": N.ACT_GELU_TANH}
+_ACCUMULATIONS = ("mfma", "exact")
 
 
 def _device_weight(value: torch.Tensor) -> torch.Tensor:
@@ -53,7 +62,7 @@ class H3FP8Linear(nn.Module):
     """Keep FP8 weights; quantize activations to E4M3 and run the FP8 MFMA GEMM."""
 
     def __init__(self, weight, bias=None, *, weight_scaling: str = "tensor",
-                 activation_scaling: str = "tensor", activation: str | None = None):
+                 activation_scaling: str = "tensor", activation: str | None = None, accumulation: str = "mfma"):
         super().__init__()
         if weight.ndim != 2 or weight.shape[0] % 16 or weight.shape[1] % 16:
             raise ValueError("H3 FP8 requires projection dimensions divisible by 16")
@@ -61,6 +70,8 @@ class H3FP8Linear(nn.Module):
             raise ValueError("weight_scaling must be 'tensor'|'channel', activation_scaling 'tensor'|'token'")
         if activation not in _ACTIVATIONS:
             raise ValueError(f"unsupported activation {activation!r}")
+        if accumulation not in _ACCUMULATIONS:
+            raise ValueError(f"accumulation must be one of {_ACCUMULATIONS}")
         self.out_features, self.in_features = weight.shape
         packed, scale = (quantize_per_tensor(weight) if weight_scaling == "tensor"
                          else quantize_per_channel(weight))
@@ -69,18 +80,20 @@ class H3FP8Linear(nn.Module):
         self.register_buffer('bias', bias.detach().clone().to(packed.device) if bias is not None else None)
         self.activation_scaling = activation_scaling
         self.activation = activation
+        self.accumulation = accumulation
         self.calls = 0
 
     @classmethod
     def from_packed(cls, weight, scale, bias=None, *, activation_scaling: str = "tensor",
-                    activation: str | None = None):
+                    activation: str | None = None, accumulation: str = "mfma"):
         """Reuse already quantized bytes and their original scale(s) without requantization."""
         if weight.dtype != torch.float8_e4m3fn or weight.ndim != 2 or any(n % 16 for n in weight.shape):
             raise ValueError('Packed H3 FP8 projection requires an aligned E4M3 matrix')
         if scale.dtype != torch.float32 or scale.numel() not in (1, weight.shape[0]):
             raise ValueError('Packed H3 FP8 projection requires one FP32 weight scale (or one per row)')
-        if activation_scaling not in ("tensor", "token") or activation not in _ACTIVATIONS:
-            raise ValueError("bad activation_scaling / activation")
+        if activation_scaling not in ("tensor", "token") or activation not in _ACTIVATIONS \
+                or accumulation not in _ACCUMULATIONS:
+            raise ValueError("bad activation_scaling / activation / accumulation")
         result = cls.__new__(cls)
         nn.Module.__init__(result)
         result.out_features, result.in_features = weight.shape
@@ -89,6 +102,7 @@ class H3FP8Linear(nn.Module):
         result.register_buffer('bias', bias.detach().clone() if bias is not None else None)
         result.activation_scaling = activation_scaling
         result.activation = activation
+        result.accumulation = accumulation
         result.calls = 0
         return result
 
@@ -108,7 +122,7 @@ class H3FP8Linear(nn.Module):
         x_diffusers/x_diffusers/framework/transformer/h3_npu_fusion.py:103-119)."""
         act = _ACTIVATIONS[activation if activation is not None else self.activation]
         out, _ = xops.scaled_mm(packed, self.weight, scale, self.weight_scale.reshape(-1), self.bias,
-                                out_dtype, act, False)
+                                out_dtype, act, False, self.accumulation == "exact")
         self.calls += 1
         return out
 
@@ -117,8 +131,10 @@ class H3FP8Linear(nn.Module):
         epilogue (the out-projection / FFN-down of a DiT block followed by
         x_base/x_base/operator/h3_indexed_affine.py:58-61).  x: bf16/fp16 [B, S, K]; residual bf16
         [B, S, N]; gate_table bf16 [T, N]; indices int64 [S].  Per-token activation scaling only."""
-        if self.activation_scaling != "token" or _ACTIVATIONS[self.activation] != N.ACT_NONE:
-            raise ValueError("forward_gate_residual needs activation_scaling='token' and no activation")
+        if self.activation_scaling != "token" or _ACTIVATIONS[self.activation] != N.ACT_NONE \
+                or self.accumulation != "mfma":
+            raise ValueError("forward_gate_residual needs activation_scaling='token', no activation and "
+                             "accumulation='mfma'")
         if x.dim() != 3 or residual.shape != (*x.shape[:-1], self.out_features):
             raise ValueError("forward_gate_residual: x [B,S,K] and residual [B,S,N] required")
         packed, scale = self.quantize_input(x.reshape(-1, x.shape[-1]))
@@ -137,11 +153,11 @@ class H3FP8Linear(nn.Module):
             return x.new_empty((*x.shape[:-1], self.out_features))
         packed, scale = self.quantize_input(matrix)
         output, _ = xops.scaled_mm(packed, self.weight, scale, self.weight_scale.reshape(-1), bias, x.dtype,
-                                   _ACTIVATIONS[self.activation], False)
+                                   _ACTIVATIONS[self.activation], False, self.accumulation == "exact")
         self.calls += 1
         return output.reshape(*x.shape[:-1], self.out_features)
 
     def extra_repr(self):
         return (f"in_features={self.in_features}, out_features={self.out_features}, "
                 f"weight_scale={tuple(self.weight_scale.shape)}, activation_scaling={self.activation_scaling}, "
-                f"activation={self.activation}")
+                f"activation={self.activation}, accumulation={self.accumulation}")

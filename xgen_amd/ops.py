@@ -27,7 +27,7 @@ SCHEMAS = {
         "float eps, int norm_kind, ScalarType out_dtype, bool return_normed) -> (Tensor, Tensor, Tensor)"),
     "scaled_mm": (
         "scaled_mm(Tensor a, Tensor w, Tensor a_scale, Tensor w_scale, Tensor? bias, "
-        "ScalarType out_dtype, int activation, bool return_acc) -> (Tensor, Tensor)"),
+        "ScalarType out_dtype, int activation, bool return_acc, bool exact=False) -> (Tensor, Tensor)"),
     "gate_residual": "gate_residual(Tensor residual, Tensor branch, Tensor gate_table, Tensor indices) -> Tensor",
     "swiglu_quant": (
         "swiglu_quant(Tensor u, bool gate_first, ScalarType out_dtype, int scale_mode, bool return_act) "
@@ -119,8 +119,9 @@ def _mm_check(a, w, a_scale, w_scale, bias, out_dtype, activation):
     _require(K % 16 == 0 and Nf % 16 == 0, "scaled_mm: K and N must be multiples of 16")
 
 
-def _mm_meta(a, w, a_scale, w_scale, bias, out_dtype, activation, return_acc):
+def _mm_meta(a, w, a_scale, w_scale, bias, out_dtype, activation, return_acc, exact=False):
     _mm_check(a, w, a_scale, w_scale, bias, out_dtype, activation)
+    _require(not exact or a.dtype == torch.float8_e4m3fn, "scaled_mm: exact accumulation applies to FP8 operands")
     M, Nf = a.shape[0], w.shape[0]
     acc_dtype = torch.float32 if a.dtype == torch.float8_e4m3fn else torch.int32
     acc = torch.empty((M, Nf) if return_acc else (0,), dtype=acc_dtype, device=a.device)
@@ -245,9 +246,9 @@ def _norm_gpu(x, weight, scale, shift, indices, eps, norm_kind, out_dtype, retur
     return q, s, normed
 
 
-def _mm_gpu(a, w, a_scale, w_scale, bias, out_dtype, activation, return_acc):
+def _mm_gpu(a, w, a_scale, w_scale, bias, out_dtype, activation, return_acc, exact=False):
     _on_gpu(a, w, a_scale, w_scale, bias)
-    out, acc = _mm_meta(a, w, a_scale, w_scale, bias, out_dtype, activation, return_acc)
+    out, acc = _mm_meta(a, w, a_scale, w_scale, bias, out_dtype, activation, return_acc, exact)
     M, K = a.shape
     Nf = w.shape[0]
     if M == 0:
@@ -259,7 +260,10 @@ def _mm_gpu(a, w, a_scale, w_scale, bias, out_dtype, activation, return_acc):
     bias = None if bias is None else bias.contiguous()
     sa_stride = 1 if a_scale.numel() == M and M > 1 else 0
     sw_stride = 1 if w_scale.numel() == Nf and Nf > 1 else 0
-    fn = "xgen_scaled_mm_fp8" if a.dtype == torch.float8_e4m3fn else "xgen_quant_matmul_int8"
+    if a.dtype == torch.float8_e4m3fn:
+        fn = "xgen_scaled_mm_fp8_exact" if exact else "xgen_scaled_mm_fp8"
+    else:
+        fn = "xgen_quant_matmul_int8"
     st = getattr(N.lib(), fn)(
         a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0), M, Nf, K, a_scale.data_ptr(), sa_stride,
         w_scale.data_ptr(), sw_stride, N.ptr(bias), N.DTYPE_NONE if bias is None else N.dtype_code(bias.dtype),
