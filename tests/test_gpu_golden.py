@@ -2,7 +2,11 @@
 w8a8_path.safetensors): quantized bytes and scales bit-exact, INT8
 accumulators bit-exact, FP8 accumulators within the MFMA accumulation bound,
 fused front end within the pre-quant contract, bf16 GEMM outputs within
-rel-L2 1e-3.  No oracle code runs here: the fixture is the reference."""
+rel-L2 1e-3.  No oracle code runs here.  The fixture holds the oracle's
+outputs frozen at the time it was written (tests/golden/make_golden.py;
+tests/test_golden_oracle.py checks the oracle still reproduces them): this is a
+regression check of the kernels against stored vectors, while parity with the
+reference rests on the oracle's own pins (tests/test_oracle_*.py)."""
 from pathlib import Path
 
 import pytest

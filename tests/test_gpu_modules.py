@@ -133,9 +133,20 @@ def test_shared_qkv_quant_matmul(cuda, kind):
     xs = x.reshape(1, 130, 512).cuda()
     q, s = xops.quantize_rows(xs.reshape(-1, 512), torch.float8_e4m3fn if kind == "fp8" else torch.int8)
     outs = [quant_matmul(q, s, m, xs.shape) for m in layers]
+    # the shared bytes and scales are the oracle's quantizer's
+    q_ref, s_ref = (R.quantize_rows_fp8 if kind == "fp8" else R.quantize_rows_int8)(x)
+    assert torch.equal(q.cpu().view(torch.uint8), q_ref.view(torch.uint8)) and torch.equal(s.cpu(), s_ref)
     for m, o in zip(layers, outs):
         assert o.shape == (1, 130, 256)
         assert torch.equal(o, m(xs))
+        # each projection against the oracle linear on the shared (q, scale)
+        if kind == "fp8":
+            ref = R.w8a8_linear_fp8(q_ref, s_ref, m.weight.cpu(), m.weight_scale.cpu(), m.bias.cpu(),
+                                    accumulate=R.fp8_mfma_accumulate)
+        else:
+            ref = R.w8a8_linear_int8(q_ref, s_ref, m.weight.cpu(), m.antiquant_scale.cpu(), m.bias.cpu())
+        rel, cos = R.rel_l2(o.reshape(130, 256), ref), R.cosine(o.reshape(130, 256), ref)
+        assert rel <= 1e-3 and cos >= 0.9999, (rel, cos)
 
 
 @pytest.mark.parametrize("kind", ["fp8", "int8"])

@@ -31,13 +31,75 @@ def test_layer_norm_f64_invariants():
     assert torch.equal(R.layer_norm_f64(x, 1e-6), n.float().to(torch.bfloat16))
 
 
-def test_rms_norm_order_and_weight():
+@pytest.mark.parametrize("H", [512, 3072, 5376])
+@pytest.mark.parametrize("eps", [1e-5, 1e-6])
+@pytest.mark.parametrize("wdtype", [None, torch.bfloat16, torch.float32])
+def test_rms_norm_f64_matches_torch_rms_norm(H, eps, wdtype):
+    """rms_norm_f64 (the f2bc order x * rsqrt(mean(x^2) + eps) * w) against torch's own RMSNorm:
+    bit for bit when torch runs in float64 too, and within 1 bf16 ulp (>= 99.9% equal) of
+    torch's bf16 F.rms_norm.  Rows scaled by 2^-12 make eps dominate mean(x^2) (a dropped or
+    misplaced eps fails), one row of zeros normalises to zeros.  (A float32 weight is compared
+    in float64 only: torch's bf16 path takes a bf16 weight.)"""
+    g = torch.Generator().manual_seed(H + int(eps * 1e7))
+    x = torch.randn((48, H), generator=g)
+    x[:8] *= 2.0 ** -12
+    x[8] = 0
+    x[9:12] *= 40
+    x = x.to(torch.bfloat16)
+    w = None if wdtype is None else (1 + 0.1 * torch.randn(H, generator=g)).to(wdtype)
+    ours = R.rms_norm_f64(x, eps, w)
+    ref64 = F.rms_norm(x.double(), (H,), None if w is None else w.double(), eps).float().to(torch.bfloat16)
+    assert torch.equal(ours.view(torch.int16), ref64.view(torch.int16))
+    if wdtype != torch.float32:  # torch's bf16 module form (nn.RMSNorm in bf16: bf16 weight)
+        ref16 = F.rms_norm(x, (H,), w, eps)
+        ulps = R.bf16_ulp_diff(ours, ref16)
+        assert ulps.max() <= 1 and (ulps == 0).float().mean() >= 0.999
+    # eps matters on the small rows: without it they would normalise to unit RMS
+    no_eps = (x[:8].double() / torch.sqrt((x[:8].double() ** 2).mean(-1, keepdim=True)))
+    assert (ours[:8].double().pow(2).mean(-1) < 0.5 * no_eps.pow(2).mean(-1)).all()
+
+
+def test_rms_norm_f64_invariants():
+    """Unit mean square without weight (eps negligible); invariant to scaling the row by 2^k."""
     torch.manual_seed(2)
-    x = torch.randn(16, 512, dtype=torch.bfloat16)
-    w = torch.randn(512, dtype=torch.bfloat16)
-    v = x.double()
-    expected = (v * torch.rsqrt((v * v).mean(-1, keepdim=True) + 1e-5) * w.double()).float().to(torch.bfloat16)
-    assert R.bf16_ulp_diff(R.rms_norm_f64(x, 1e-5, w), expected).max() <= 1
+    x = (torch.randn(32, 1024) * 3).to(torch.bfloat16)
+    n = R.rms_norm_f64(x, 1e-6).double()
+    assert torch.allclose(n.pow(2).mean(-1), torch.ones(32, dtype=torch.float64), atol=1e-2)
+    assert torch.equal(R.rms_norm_f64(x * 8, 1e-12), R.rms_norm_f64(x, 1e-12))
+
+
+def test_fp8_linear_epilogue_equals_torch_scaled_mm():
+    """w8a8_linear_fp8 with per-tensor scales == CPU torch._scaled_mm(a, w.T, scale_a, scale_b,
+    bias, out_dtype=bf16) bit for bit (h3_fp8.py:63-66).  Operands are e4m3 codes of exponents
+    -3..3 with K = 64, so every partial sum is exact in float32 whatever the summation order: the
+    comparison isolates the dequant-and-bias epilogue.  Scales are not powers of two."""
+    g = torch.Generator().manual_seed(11)
+    for M, N, out_dtype in ((64, 256, torch.bfloat16), (37, 80, torch.bfloat16), (16, 48, torch.float16)):
+        def codes(rows):
+            mag = torch.randint(0x20, 0x58, (rows, 64), generator=g, dtype=torch.int32)  # exponent field 4..10
+            sign = torch.randint(0, 2, (rows, 64), generator=g, dtype=torch.int32) << 7
+            return (mag | sign).to(torch.uint8).view(torch.float8_e4m3fn)
+        qa, qw = codes(M), codes(N)
+        sa = torch.rand((), generator=g) * 0.01 + 1e-3
+        sw = torch.rand((), generator=g) * 0.01 + 1e-3
+        for bias in (None, (torch.randn(N, generator=g) * 0.1).to(torch.bfloat16)):
+            ref = torch._scaled_mm(qa, qw.t(), scale_a=sa, scale_b=sw, bias=bias, out_dtype=out_dtype)
+            ours = R.w8a8_linear_fp8(qa, sa, qw, sw, bias, out_dtype)
+            assert torch.equal(ours, ref)
+
+
+def test_fp8_linear_matches_torch_scaled_mm_general_operands():
+    """General row-quantized operands (K = 3,072): CPU _scaled_mm sums in float32 in its own
+    order, the oracle exactly; outputs equal on >= 99.99% of elements, all within 1 ulp."""
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn((64, 3072), generator=g).to(torch.bfloat16)
+    w = (torch.randn((512, 3072), generator=g) * 0.02).to(torch.bfloat16)
+    b = (torch.randn(512, generator=g) * 0.01).to(torch.bfloat16)
+    qa, sa = R.quantize_per_tensor(x)
+    qw, sw = R.quantize_per_tensor(w)
+    ref = torch._scaled_mm(qa, qw.t(), scale_a=sa, scale_b=sw, bias=b, out_dtype=torch.bfloat16)
+    ulps = R.bf16_ulp_diff(R.w8a8_linear_fp8(qa, sa, qw, sw, b), ref)
+    assert ulps.max() <= 1 and (ulps == 0).float().mean() >= 0.9999
 
 
 def test_modulate_eager_equals_explicit_rounding():
