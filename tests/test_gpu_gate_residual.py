@@ -98,7 +98,7 @@ def test_module_forward_gate_residual(cuda, kind):
     gate = (torch.randn((3, Nf), generator=g) * 0.5).to(torch.bfloat16).to(cuda)
     idx = torch.randint(3, (S,), generator=g).to(cuda)
     m = (H3FP8Linear(w, b, weight_scaling="channel", activation_scaling="token") if kind == "fp8"
-         else WeightQuantLinearModule(w, b))
+         else WeightQuantLinearModule(w, b)).to(cuda)
     fused = m.forward_gate_residual(x, residual, gate, idx)
     assert torch.equal(u16(fused), u16(gate_residual(residual, m(x), gate, idx)))
 

@@ -40,6 +40,8 @@ def test_per_tensor_module_matches_oracle(cuda):
     weight = torch.randn(512, 256, dtype=torch.bfloat16) * 0.02
     bias = torch.randn(512, dtype=torch.bfloat16) * 0.01
     layer = H3FP8Linear(weight, bias)
+    assert layer.weight.device.type == "cpu"  # buffers stay on the weight's device (h3_fp8.py:22-25)
+    layer = layer.cuda()
     qw, sw = R.quantize_per_tensor(weight)
     assert torch.equal(layer.weight.cpu().view(torch.uint8), qw.view(torch.uint8))
     assert torch.equal(layer.weight_scale.cpu(), sw)
@@ -56,7 +58,7 @@ def test_per_tensor_module_matches_oracle(cuda):
 def test_token_channel_module_c1(cuda, dtype):
     """C1: x [256,1024], W [1024,1024] per-channel, per-token activations."""
     inp = workloads.linear_inputs(256, 1024, 1024, seed=0)
-    layer = H3FP8Linear(inp.weight, inp.bias, weight_scaling="channel", activation_scaling="token")
+    layer = H3FP8Linear(inp.weight, inp.bias, weight_scaling="channel", activation_scaling="token").cuda()
     qw, sw = R.quantize_rows_fp8(inp.weight)
     assert torch.equal(layer.weight.cpu().view(torch.uint8), qw.view(torch.uint8))
     assert torch.equal(layer.weight_scale.cpu(), sw)
@@ -72,7 +74,7 @@ def test_token_channel_module_c1(cuda, dtype):
 
 def test_from_packed_reuses_bytes(cuda):
     inp = workloads.linear_inputs(64, 256, 128, seed=2)
-    a = H3FP8Linear(inp.weight, inp.bias)
+    a = H3FP8Linear(inp.weight, inp.bias).cuda()
     b = H3FP8Linear.from_packed(a.weight, a.weight_scale, a.bias)
     x = inp.x.cuda()
     assert torch.equal(a(x), b(x))
@@ -80,7 +82,10 @@ def test_from_packed_reuses_bytes(cuda):
 
 def test_int8_module_matches_oracle(cuda):
     inp = workloads.linear_inputs(300, 1024, 512, seed=4)
-    layer = WeightQuantLinearModule(inp.weight, inp.bias)
+    layer = WeightQuantLinearModule(inp.weight.cuda(), inp.bias)
+    # parameters are kept on the CPU after quantization, as the reference's (matmul.py:39-48)
+    assert layer.weight.device.type == "cpu" and layer.antiquant_scale.device.type == "cpu"
+    layer = layer.cuda()
     qw, sw = R.quantize_rows_int8(inp.weight)
     assert torch.equal(layer.weight.cpu(), qw) and torch.equal(layer.antiquant_scale.cpu(), sw)
     assert layer.in_features == 1024 and layer.out_features == 512
@@ -127,8 +132,8 @@ def test_shared_qkv_quant_matmul(cuda, kind):
     for _ in range(3):
         w = (torch.randn(256, 512, generator=g) * 0.02).to(torch.bfloat16)
         b = (torch.randn(256, generator=g) * 0.01).to(torch.bfloat16)
-        layers.append(H3FP8Linear(w, b, weight_scaling="channel", activation_scaling="token") if kind == "fp8"
-                      else WeightQuantLinearModule(w, b))
+        layers.append((H3FP8Linear(w, b, weight_scaling="channel", activation_scaling="token") if kind == "fp8"
+                       else WeightQuantLinearModule(w, b)).cuda())
     assert all(quant_linear(m, 512, torch.device("cuda", 0)) for m in layers)
     xs = x.reshape(1, 130, 512).cuda()
     q, s = xops.quantize_rows(xs.reshape(-1, 512), torch.float8_e4m3fn if kind == "fp8" else torch.int8)
@@ -160,11 +165,11 @@ def test_ffn_pair_gelu_requant(cuda, kind):
     wd = (torch.randn(d, 4 * d, generator=g) * 0.02).to(torch.bfloat16)
     bd = (torch.randn(d, generator=g) * 0.01).to(torch.bfloat16)
     if kind == "fp8":
-        up = H3FP8Linear(wu, bu, weight_scaling="channel", activation_scaling="token", activation="gelu_tanh")
-        down = H3FP8Linear(wd, bd, weight_scaling="channel", activation_scaling="token")
+        up = H3FP8Linear(wu, bu, weight_scaling="channel", activation_scaling="token", activation="gelu_tanh").cuda()
+        down = H3FP8Linear(wd, bd, weight_scaling="channel", activation_scaling="token").cuda()
         quant, lin = R.quantize_rows_fp8, R.w8a8_linear_fp8
     else:
-        up, down = WeightQuantLinearModule(wu, bu), WeightQuantLinearModule(wd, bd)
+        up, down = WeightQuantLinearModule(wu, bu).cuda(), WeightQuantLinearModule(wd, bd).cuda()
         quant, lin = R.quantize_rows_int8, R.w8a8_linear_int8
     xc = x.cuda()
     if kind == "fp8":

@@ -75,7 +75,7 @@ def test_h3_ffn_int8(cuda):
     x = torch.randn((1, M, d), generator=g).to(torch.bfloat16).to(cuda)
     wu = (torch.randn((2 * F, d), generator=g) * 0.02).to(torch.bfloat16)
     wd = (torch.randn((d, F), generator=g) * 0.02).to(torch.bfloat16)
-    up, down = WeightQuantLinearModule(wu, None), WeightQuantLinearModule(wd, None)
+    up, down = WeightQuantLinearModule(wu, None).to(cuda), WeightQuantLinearModule(wd, None).to(cuda)
     u = up(x)
     q, s = swiglu_quantize_reuse(u)
     y, _ = xops.scaled_mm(q, down.weight, s, down.antiquant_scale, None, torch.bfloat16, 0, False)

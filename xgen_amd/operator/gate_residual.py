@@ -14,9 +14,15 @@ from __future__ import annotations
 
 import torch
 
+from .. import _native as N
 from .. import ops as _ops  # noqa: F401  (registers torch.ops.xgen_amd)
 
 xops = torch.ops.xgen_amd
+
+
+def library_path():
+    """The library holding the kernel (gate_residual.py:7-8; XGEN_AMD_LIBRARY overrides it)."""
+    return N.library_path()
 
 
 def gate_residual(residual, branch, gate_table, indices, *, tile=5376, blocks=40):

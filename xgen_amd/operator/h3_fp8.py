@@ -36,6 +36,7 @@ _ACCUMULATIONS = ("mfma", "exact")
 
 
 def _device_weight(value: torch.Tensor) -> torch.Tensor:
+    """The weight on a HIP device, where the quantizer kernels run (a CPU weight is copied there)."""
     if value.dtype not in (torch.bfloat16, torch.float16):
         raise ValueError("xgen_amd FP8 weight quantization requires a BF16/FP16 weight")
     if not value.is_cuda:
@@ -45,17 +46,22 @@ def _device_weight(value: torch.Tensor) -> torch.Tensor:
     return value.detach().contiguous()
 
 
+def _on(device, *tensors):
+    return tuple(t.to(device) for t in tensors)
+
+
 def quantize_per_tensor(value: torch.Tensor):
-    """(e4m3fn tensor, float32 0-dim scale) with scale = max(amax/448, FLT_MIN) (h3_fp8.py:9-12)."""
-    return quantize_activation(_device_weight(value))
+    """(e4m3fn tensor, float32 0-dim scale) with scale = max(amax/448, FLT_MIN) (h3_fp8.py:9-12),
+    on the device `value` is on (quantized by the HIP kernels)."""
+    return _on(value.device, *quantize_activation(_device_weight(value)))
 
 
 def quantize_per_channel(value: torch.Tensor):
     """quantize_per_tensor's arithmetic applied to each row of a 2-D weight:
-    (e4m3fn [N,K], float32 [N])."""
+    (e4m3fn [N,K], float32 [N]), on the device `value` is on."""
     if value.ndim != 2:
         raise ValueError("per-channel quantization requires a 2-D weight")
-    return quantize_activation_rows(_device_weight(value))
+    return _on(value.device, *quantize_activation_rows(_device_weight(value)))
 
 
 class H3FP8Linear(nn.Module):
@@ -77,7 +83,8 @@ class H3FP8Linear(nn.Module):
                          else quantize_per_channel(weight))
         self.register_buffer('weight', packed.contiguous())
         self.register_buffer('weight_scale', scale.reshape(-1) if weight_scaling == "channel" else scale)
-        self.register_buffer('bias', bias.detach().clone().to(packed.device) if bias is not None else None)
+        # buffers stay on the weight's device, as the reference's (h3_fp8.py:22-25)
+        self.register_buffer('bias', bias.detach().clone() if bias is not None else None)
         self.activation_scaling = activation_scaling
         self.activation = activation
         self.accumulation = accumulation

@@ -29,6 +29,10 @@ def dynamic_quant(x: torch.Tensor):
 
 
 class WeightQuantLinearModule(nn.Module):
+    """Parameters are quantized on the HIP device and then kept on the CPU, as the reference's
+    (matmul.py:39-48: quantize on the accelerator, copy to CPU to lower its peak memory); the
+    model is moved to its device afterwards."""
+
     def __init__(self, weight, bias, name=None):
         super().__init__()
         w = weight.detach()
@@ -41,13 +45,15 @@ class WeightQuantLinearModule(nn.Module):
                 raise RuntimeError("xgen_amd INT8 weight quantization requires a HIP device")
             w = w.cuda()
         quant_weight, weight_scale = dynamic_quant(w.contiguous())
-        self.register_parameter('weight', nn.Parameter(quant_weight, requires_grad=False))
-        self.register_parameter('antiquant_scale', nn.Parameter(weight_scale, requires_grad=False))
+        w_cpu, scale_cpu = quant_weight.cpu(), weight_scale.cpu()
+        del quant_weight, weight_scale
+        self.register_parameter('weight', nn.Parameter(w_cpu, requires_grad=False))
+        self.register_parameter('antiquant_scale', nn.Parameter(scale_cpu, requires_grad=False))
         if bias is not None:
-            self.register_parameter('bias', nn.Parameter(bias.detach().to(quant_weight.device), requires_grad=False))
+            self.register_parameter('bias', nn.Parameter(bias.detach().cpu(), requires_grad=False))
         else:
             self.register_parameter('bias', None)
-        self.out_features, self.in_features = quant_weight.shape
+        self.out_features, self.in_features = w_cpu.shape
         self.name = name
 
     def forward(self, x):

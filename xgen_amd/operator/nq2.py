@@ -25,6 +25,12 @@ from ..ops import xops
 _NORMS = {"rms": N.NORM_RMS, "layer": N.NORM_LAYER}
 
 
+def library_path(cached=False):
+    """The library holding the kernel (nq2.py:10-15 resolves one per `cached` variant; both
+    variants are the one HIP library here, XGEN_AMD_LIBRARY overriding its location)."""
+    return N.library_path()
+
+
 def norm_affine_quant(x, weight, scale, shift, indices, *, eps=1e-5, blocks=40, cached=False,
                       norm="rms", out_dtype=torch.int8, return_normed=False, scale_is_one_plus=False):
     if any(v is not None and v.requires_grad for v in (x, weight, scale, shift)):

@@ -12,15 +12,26 @@ violations (quant_meta, swiglu_quant_reuse_queued.asc:10-17).  `tile` and
 
 `swiglu_quant` is the general form: gate-first layout ([gate | hidden], as
 x_base/x_base/operator/h3_swiglu.py packs it), FP8 or INT8 output, and the
-bf16 activation itself on request.
+bf16 activation itself on request.  `gate_first_swiglu(x, *, with_amax)` is
+h3_swiglu.py:31-41's surface: the bf16 activation of a gate-first input and,
+on request, its NaN-propagating max |value| as a float32 0-dim tensor.
 """
 from __future__ import annotations
 
 import torch
 
+from .. import _native as N
 from .. import ops as _ops  # noqa: F401
 
 xops = torch.ops.xgen_amd
+
+
+def library_path(implementation='scalar'):
+    """The library holding the kernels (swiglu_quant.py:11-17 resolves one per implementation;
+    all three are the one HIP library here, XGEN_AMD_LIBRARY overriding its location)."""
+    if implementation not in ('scalar', 'vector', 'reuse'):
+        raise KeyError(implementation)
+    return N.library_path()
 
 
 def _checked(u, tile, blocks, scale_mode, tiles):
@@ -52,3 +63,20 @@ def swiglu_quant(u, *, gate_first=False, out_dtype=torch.int8, scale_mode=1, ret
         raise ValueError("swiglu_quant is inference-only")
     q, s, act = xops.swiglu_quant(u, gate_first, out_dtype, scale_mode, return_act)
     return (q, s, act) if return_act else (q, s)
+
+
+def gate_first_swiglu(x, *, with_amax=False):
+    """x bf16 [..., 2F] laid out [gate | value] -> bf16(bf16(gate / (1 + exp(-gate))) * value)
+    [..., F] (x_base/x_base/operator/h3_swiglu.py:15-41, eager bf16 rounding of the activation);
+    with_amax also returns max |result| (NaN propagates) as a float32 0-dim tensor."""
+    if x.requires_grad:
+        raise ValueError("gate_first_swiglu is inference-only")
+    if x.dtype != torch.bfloat16 or x.shape[-1] % 2:
+        raise ValueError("gate_first_swiglu: BF16 input with an even last dimension required")
+    lead, F = x.shape[:-1], x.shape[-1] // 2
+    u = x.reshape(1, -1, 2 * F) if x.dim() != 3 else x
+    _, _, act = xops.swiglu_quant(u, True, torch.float8_e4m3fn, 1, True)
+    out = act.reshape(*lead, F)
+    if with_amax:
+        return out, xops.abs_peak(act)
+    return out
