@@ -434,6 +434,18 @@ def cpu_fake_quant_linear_fp8(x: torch.Tensor, qw: torch.Tensor, sw: torch.Tenso
     return y.to(torch.bfloat16)
 
 
+def cpu_fake_quant_linear_int8(x: torch.Tensor, qw: torch.Tensor, sw: torch.Tensor, bias) -> torch.Tensor:
+    """CPU INT8 W8A8 linear (the reported CPU baseline, INT8 form): per-row INT8 quantization
+    (quantize_rows_int8), exact int32 accumulation by torch._int_mm, float32 dequant
+    acc * sx * sw + bias, bf16."""
+    qa, sa = quantize_rows_int8(x)
+    acc = torch._int_mm(qa, qw.t().contiguous())
+    y = acc.float() * (sa[:, None] * sw.reshape(1, -1).float())
+    if bias is not None:
+        y = y + bias.float()
+    return y.to(torch.bfloat16)
+
+
 # ----------------------------------------------------------------------------- metrics
 def rel_l2(a: torch.Tensor, b: torch.Tensor) -> float:
     a, b = a.detach().cpu().double(), b.detach().cpu().double()
