@@ -107,6 +107,20 @@ int xgen_fp8_tensor_scale(int in_dtype, const void *x, int64_t numel, float *sca
                           void *workspace, size_t workspace_bytes, hipStream_t stream);
 
 /*
+ * xgen_fp8_tensor_scale without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops that
+ * forbid hipMalloc).  No counterpart in the reference: an MI355X-side variant
+ * of the entry point above.  Its partial maxima live in a file-scope device
+ * array of the library (4 KB per GPU, kept for the life of the process), whose
+ * address is resolved on the first call on each device (the current device,
+ * which must be the stream's).  It calls no hipMalloc / hipFree.  Every call
+ * on one GPU shares that array: calls that overlap on one GPU (concurrent
+ * streams, threads) race and must be serialised by the caller.  Arguments and
+ * results as xgen_fp8_tensor_scale; any numel > 0 fits the scratch.
+ */
+int xgen_fp8_tensor_scale_noalloc(int in_dtype, const void *x, int64_t numel, float *scale, hipStream_t stream);
+
+/*
  * FP8 pack with a device-resident per-tensor scale
  * (_pack, x_base/x_base/operator/h3_fp8_quant.py:9-15):
  * q[i] = e4m3fn_rne(clamp(x[i] / scale[0], -448, 448)) over numel contiguous elements.

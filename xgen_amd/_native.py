@@ -48,6 +48,7 @@ SIGNATURES = {
     "xgen_abs_peak_workspace_bytes": (_c_size, [_c_i64]),
     "xgen_abs_peak": (_c_int, [_c_int, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_size, _c_ptr]),
     "xgen_fp8_tensor_scale": (_c_int, [_c_int, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_size, _c_ptr]),
+    "xgen_fp8_tensor_scale_noalloc": (_c_int, [_c_int, _c_ptr, _c_i64, _c_ptr, _c_ptr]),
     "xgen_fp8_pack": (_c_int, [_c_int, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_ptr]),
     "xgen_norm_affine_quant": (_c_int, [
         _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_ptr, _c_int, _c_float,

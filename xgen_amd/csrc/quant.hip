@@ -12,6 +12,8 @@
 // propagating max |x| is an integer max over the 16-bit magnitudes, reduced
 // across the wave with cross-lane shuffles (and across the row's waves through
 // LDS); the row is then quantized from registers and written as 8-byte chunks.
+#include <mutex>
+
 #include "xgen_common.h"
 
 namespace xgen {
@@ -356,6 +358,58 @@ extern "C" int xgen_fp8_tensor_scale(int in_dtype, const void *x, int64_t numel,
   if (st != XGEN_OK) return st;
   return in_dtype == XGEN_DTYPE_BF16 ? abs_peak_typed<XGEN_DTYPE_BF16>(x, numel, scale, 1, workspace, stream)
                                      : abs_peak_typed<XGEN_DTYPE_F16>(x, numel, scale, 1, workspace, stream);
+}
+
+// Scratch of the allocation-free per-tensor scale: the per-workgroup partial
+// maxima (at most kPeakBlocksMax of them, 4 KB).  Each GPU holds its own copy
+// for the life of the process.  Host code never passes the name itself to a
+// kernel (on the host it is a stand-in, not a device address): it uses the
+// address hipGetSymbolAddress returns on each device, resolved once per device.
+static __device__ __align__(256) uint32_t scratch[kPeakBlocksMax];
+constexpr size_t kScratchBytes = sizeof(scratch);
+
+namespace xgen {
+namespace {
+
+// Device address of `scratch` on the current device (resolved on the first call there).
+int scratch_on_current_device(const char *fn, void **out) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void *addr[kMaxDevices];
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(XGEN_ERR_HIP, "%s: no current HIP device (or device index above %d)", fn, kMaxDevices - 1);
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(XGEN_ERR_HIP, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", fn, dev,
+                  hipGetErrorString(e));
+    addr[dev] = p;
+  }
+  *out = addr[dev];
+  return XGEN_OK;
+}
+
+}  // namespace
+}  // namespace xgen
+
+extern "C" int xgen_fp8_tensor_scale_noalloc(int in_dtype, const void *x, int64_t numel, float *scale,
+                                             hipStream_t stream) {
+  const char *fn = "xgen_fp8_tensor_scale_noalloc";
+  void *ws = nullptr;
+  int st = scratch_on_current_device(fn, &ws);
+  if (st != XGEN_OK) return st;
+  // the partials a call needs never exceed the scratch (peak_blocks caps them), but check anyway
+  if (numel > 0 && xgen_abs_peak_workspace_bytes(numel) > kScratchBytes)
+    return fail(XGEN_ERR_UNSUPPORTED, "%s: %zu bytes of partial maxima exceed the %zu-byte scratch", fn,
+                xgen_abs_peak_workspace_bytes(numel), kScratchBytes);
+  st = check_peak_args(fn, in_dtype, x, numel, scale, ws, kScratchBytes);
+  if (st != XGEN_OK) return st;
+  // every partial the final reduction reads is written by this call first: nothing to clear
+  return in_dtype == XGEN_DTYPE_BF16 ? abs_peak_typed<XGEN_DTYPE_BF16>(x, numel, scale, 1, ws, stream)
+                                     : abs_peak_typed<XGEN_DTYPE_F16>(x, numel, scale, 1, ws, stream);
 }
 
 extern "C" int xgen_fp8_pack(int in_dtype, const void *x, int64_t numel, const float *scale, void *q,
