@@ -43,16 +43,50 @@ namespace xgen {
 
 namespace {
 
-constexpr int BM = 256, BN = 256;
-constexpr int BK = 64;                        // K bytes per pipeline stage
-constexpr int kStages = 4;                    // LDS ring depth
-constexpr int kTileBytes = 256 * BK;          // one operand tile of one stage: 16 KB
-constexpr int kStageBytes = 2 * kTileBytes;   // activations + weights: 32 KB
+constexpr int BK = 64;  // K bytes per pipeline stage
 // instruction classes of __builtin_amdgcn_sched_group_barrier
 constexpr int kMfma = 0x008, kVmemRead = 0x020, kDsRead = 0x100;
 
-// Waves per workgroup (along M and N) of the production configuration.
-constexpr int kWavesM = 2, kWavesN = 4;
+// Tiling of one kernel instance: a BM x BN output tile per workgroup of
+// WM x WN waves, a ring of STAGES LDS slots, WGS workgroups resident per CU.
+template <int BM_, int BN_, int WM_, int WN_, int STAGES_, int WGS_>
+struct Tiling {
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, kStages = STAGES_, kWgsPerCu = WGS_;
+  static constexpr int kWaves = WM * WN, kThreads = 64 * kWaves;
+  static constexpr int FM = BM / WM / 32;  // activation (token) fragments per wave
+  static constexpr int FN = BN / WN / 32;  // weight (feature) fragments per wave
+  static constexpr int kTileA = BM * BK, kTileW = BN * BK;  // operand tiles of one stage
+  static constexpr int kStageBytes = kTileA + kTileW;
+  // DMA: wave w fills rows [w * kRows*, (w + 1) * kRows*) of both tiles, 16 rows (1 KB) per load
+  static constexpr int kRowsA = BM / kWaves, kRowsW = BN / kWaves;
+  static constexpr int kLoadsA = kRowsA / 16, kLoadsW = kRowsW / 16;
+  static constexpr int kLoadsPerStage = kLoadsA + kLoadsW;  // per thread
+  // One parameter set: [sa f32 x BM][sw f32 x BN][bias f32 x BN].  The bias
+  // arrives as stored (bf16 / f16 / f32) at the start of its row and is
+  // converted to f32 in place in the epilogue.
+  static constexpr int kParamBytes = 4 * (BM + 2 * BN);
+  // A tile's parameters are loaded with its first stage, issued kStages stages
+  // ahead, and read in its epilogue; the set is reloaded kParamSets tiles later.
+  // With KT stages per tile that reload is issued after the epilogue when
+  // (kParamSets - 1) * KT >= kStages, for every KT >= 1.
+  static constexpr int kParamSets = kStages + 1;
+  static constexpr int kLdsBytes = kStages * kStageBytes + kParamSets * kParamBytes;
+  static_assert(kRowsA % 16 == 0 && kRowsW % 16 == 0, "DMA rows");
+  static_assert(kWaves >= 3, "the parameter loads use waves 0, 1 and 2");
+  static_assert(BM * 4 <= 1024 && BN * 4 <= 1024, "one DMA load per parameter row");
+  // load q of a stage is a weight load if ((q + 1) * kLoadsW) / L > (q * kLoadsW) / L:
+  // the two operands' loads interleave in proportion
+  static constexpr __device__ bool load_is_w(int q) {
+    return ((q + 1) * kLoadsW) / kLoadsPerStage > (q * kLoadsW) / kLoadsPerStage;
+  }
+  static constexpr __device__ int load_index(int q) {
+    return load_is_w(q) ? (q * kLoadsW) / kLoadsPerStage : q - (q * kLoadsW) / kLoadsPerStage;
+  }
+};
+
+// Production tiling: 256 x 256 tiles, 8 waves (2 per SIMD) of 128 x 64 each,
+// a 4-deep ring (148 KB of LDS), one workgroup per CU.
+typedef Tiling<256, 256, 2, 4, 4, 1> TileMain;
 
 struct GemmArgs {
   const uint8_t *a;
@@ -70,6 +104,7 @@ struct GemmArgs {
   void *acc_out;
   int tiles_m, tiles_n, per_xcd;
   int group_m;  // tile-rows per group of the tile order
+  int kt4;      // stages per tile of the one-wave-per-SIMD kernel (a multiple of 4)
   uint32_t a_bytes, w_bytes;
   // gated residual epilogue (GATED kernels only)
   const uint8_t *residual;
@@ -81,7 +116,7 @@ struct GemmArgs {
   uint32_t seq;
 };
 
-// LDS layout of one operand tile of one stage: 256 rows x 64 bytes (4 chunks
+// LDS layout of one operand tile of one stage: rows of 64 bytes (4 chunks
 // of 16 bytes).  Chunk c of row r is stored at chunk position c ^ ((r >> 2) & 3).
 // gfx950's LDS has 64 banks (256 bytes per cycle): the 16 lanes one 128-bit
 // access serves (rows r..r+15, one logical chunk) then hit 16 distinct 16-byte
@@ -228,6 +263,7 @@ __device__ __forceinline__ float bias_at(const uint8_t *bias, int dtype, int n) 
 }
 
 // Output tile -> (m0, n0): tiles are walked in groups of group_m tile-rows.
+template <int BM, int BN>
 __device__ __forceinline__ void tile_origin(int pid, int tiles_m, int tiles_n, int group_m, int &m0, int &n0) {
   const int group_size = group_m * tiles_n;
   const int group = pid / group_size;
@@ -238,12 +274,13 @@ __device__ __forceinline__ void tile_origin(int pid, int tiles_m, int tiles_n, i
   n0 = (in_group / gm) * BN;
 }
 
-// Persistent kernel: one workgroup per CU.  The tiles of XCD x (workgroups
-// x, x+8, ... run there) are the contiguous range [x*per_xcd, (x+1)*per_xcd),
-// dealt round-robin to that XCD's workgroups, so the tiles running at once on
-// one XCD are neighbours in its L2.  The stage sequence of all of a
-// workgroup's tiles is one stream: the DMA ring runs across tile boundaries,
-// so a tile's epilogue overlaps the loads of the next tile's first stages.
+// Persistent kernel: C::kWgsPerCu workgroups per CU.  The tiles of XCD x
+// (workgroups x, x+8, ... run there) are the contiguous range [x*per_xcd,
+// (x+1)*per_xcd), dealt round-robin to that XCD's workgroups, so the tiles
+// running at once on one XCD are neighbours in its L2.  The stage sequence of
+// all of a workgroup's tiles is one stream: the DMA ring runs across tile
+// boundaries, so a tile's epilogue overlaps the loads of the next tile's first
+// stages.
 //
 // Epilogue.  gfx9 has a single in-order vector-memory counter, so a global
 // load in the epilogue would also wait for the DMA still in flight.  The
@@ -251,28 +288,18 @@ __device__ __forceinline__ void tile_origin(int pid, int tiles_m, int tiles_n, i
 // LDS by the same DMA path, with the tile's first stage (kParamSets buffers,
 // indexed by tile), and are read with LDS loads.  Outputs are transposed
 // through the ring slot just consumed (free until the next barrier) so every
-// store writes full 128-byte row segments.
-// One parameter set: [sa f32 x 256][sw f32 x 256][bias as loaded, <= 1 KB][bias f32 x 256].
-constexpr int kParamBytes = 1024;  // 256 x 4 bytes: one parameter row of a tile
-constexpr int kParamSetBytes = 4 * kParamBytes;
-// A tile's parameters are loaded with its first stage, issued kStages stages
-// ahead, and read in its epilogue; the set is reloaded kParamSets tiles later.
-// With KT stages per tile that reload is issued after the epilogue when
-// (kParamSets - 1) * KT >= kStages, for every KT >= 1.
-constexpr int kParamSets = kStages + 1;
-constexpr int kLdsBytes = kStages * kStageBytes + kParamSets * kParamSetBytes;
-
+// store writes full row segments.
+//
 // GATED: the bf16 output y feeds out = bf16(residual + bf16(y * gate[indices[m % seq]])).
-template <int KIND, int ACT, int OUT_DT, bool ACC_OUT, int WM, int WN, bool GATED = false>
-__global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) {
+template <int KIND, int ACT, int OUT_DT, bool ACC_OUT, class C, bool GATED = false>
+__global__ __attribute__((amdgpu_flat_work_group_size(C::kThreads, C::kThreads),
+                          amdgpu_waves_per_eu(C::kWaves * C::kWgsPerCu / 4, C::kWaves * C::kWgsPerCu / 4)))
+void gemm_w8a8_kernel(GemmArgs p) {
   typedef Mfma<KIND> T;
-  constexpr int kWaves = WM * WN;
-  constexpr int FM = BM / WM / 32;               // activation (token) fragments per wave
-  constexpr int FN = BN / WN / 32;               // weight (feature) fragments per wave
-  constexpr int kRowsPerWave = 256 / kWaves;     // DMA rows per operand per wave
-  constexpr int kWaveLoads = kRowsPerWave / 16;  // 1 KB DMA loads per operand per wave
-  constexpr int kLoadsPerStage = 2 * kWaveLoads; // per thread
-  static_assert(kRowsPerWave % 16 == 0, "DMA rows");
+  constexpr int BM = C::BM, BN = C::BN, WM = C::WM, WN = C::WN, kStages = C::kStages;
+  constexpr int kWaves = C::kWaves, FM = C::FM, FN = C::FN;
+  constexpr int kLoadsPerStage = C::kLoadsPerStage;
+  constexpr int kStageBytes = C::kStageBytes, kParamBytes = C::kParamBytes;
   // epilogue transpose: one 32-row block of the wave's outputs, kRowBytes per row
   constexpr int kRowBytes = FN * 32 * 2;
   constexpr int kRowsPerLine = 256 / kRowBytes;      // rows sharing one 256-byte line of banks
@@ -281,7 +308,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) 
   constexpr int kRowsPerRead = 64 / kLanesPerRow;    // rows per 16-byte-per-lane read
   static_assert((kRowBytes == 128 || kRowBytes == 256) && kWaves * 32 * kRowBytes <= kStageBytes,
                 "epilogue transpose layout");
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[kLdsBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[C::kLdsBytes];
 
   // --- this workgroup's tiles ------------------------------------------------
   const int ntiles = p.tiles_m * p.tiles_n;
@@ -313,22 +340,20 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) 
 
   // --- global -> LDS DMA ------------------------------------------------------
   // A 16-byte DMA load writes LDS at (wave base + lane * 16), so one wave-load
-  // fills 1 KB = 16 rows x 64 bytes.  Wave w fills rows
-  // [w * kRowsPerWave, (w + 1) * kRowsPerWave) of both operand tiles; lane l
-  // lands on row base + (l >> 2), physical chunk l & 3, i.e. logical chunk
-  // (l & 3) ^ ((row >> 2) & 3) = (l & 3) ^ ((l >> 4) & 3), fetched from global.
+  // fills 1 KB = 16 rows x 64 bytes.  Lane l lands on row base + (l >> 2),
+  // physical chunk l & 3, i.e. logical chunk (l & 3) ^ ((row >> 2) & 3) =
+  // (l & 3) ^ ((l >> 4) & 3), fetched from global.
   const int dma_chunk = (lane & 3) ^ ((lane >> 4) & 3);
-  uint32_t offa[kWaveLoads], offw[kWaveLoads];
+  // Byte offsets of this lane's first A and W rows in my current tile; load l
+  // adds l * 16 rows.  Rows past M (N) need no test: their offsets lie past the
+  // end of the buffer resource (the host checks they fit in 32 bits), where
+  // the buffer loads read zeros.
+  uint32_t offa = 0, offw = 0;
   int dma_m0 = 0, dma_n0 = 0;
-  auto set_dma_tile = [&](int i) {  // row offsets of my i-th tile
-    tile_origin(t_first + i * wgs_per_xcd, p.tiles_m, p.tiles_n, p.group_m, dma_m0, dma_n0);
-#pragma unroll
-    for (int l = 0; l < kWaveLoads; ++l) {
-      const int r = wave * kRowsPerWave + l * 16 + (lane >> 2);
-      const int ma = dma_m0 + r, nw = dma_n0 + r;
-      offa[l] = ma < p.M ? (uint32_t)ma * (uint32_t)p.lda + dma_chunk * 16 : kOutOfRange;
-      offw[l] = nw < p.N ? (uint32_t)nw * (uint32_t)p.ldw + dma_chunk * 16 : kOutOfRange;
-    }
+  auto set_dma_tile = [&](int i) {
+    tile_origin<BM, BN>(t_first + i * wgs_per_xcd, p.tiles_m, p.tiles_n, p.group_m, dma_m0, dma_n0);
+    offa = (uint32_t)(dma_m0 + wave * C::kRowsA + (lane >> 2)) * (uint32_t)p.lda + dma_chunk * 16;
+    offw = (uint32_t)(dma_n0 + wave * C::kRowsW + (lane >> 2)) * (uint32_t)p.ldw + dma_chunk * 16;
   };
   // The load stream: the next stage to load is issue_g (slot issue_g %
   // kStages), stage issue_kt of my tile issue_i.  Past my last stage the
@@ -337,29 +362,37 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) 
   int issue_g = 0, issue_kt = 0, issue_i = 0;
   auto issue_params = [&]() {  // a tile's epilogue parameters ride with its first stage
     if (issue_kt != 0 || issue_g >= G) return;
-    uint8_t *prm = smem + kStages * kStageBytes + (issue_i % kParamSets) * kParamSetBytes;
-    if (wave == 0 && p.sa_stride) dma_load16(rsa, prm, (uint32_t)dma_m0 * 4 + lane * 16);
-    if (wave == 1 && p.sw_stride) dma_load16(rsw, prm + kParamBytes, (uint32_t)dma_n0 * 4 + lane * 16);
-    if (wave == 2 && p.bias) dma_load16(rb, prm + 2 * kParamBytes, (uint32_t)(dma_n0 * bias_elem) + lane * 16);
+    uint8_t *prm = smem + kStages * kStageBytes + (issue_i % C::kParamSets) * kParamBytes;
+    // lanes past a row's bytes stay idle (their 16 bytes would land in the next row)
+    if (wave == 0 && p.sa_stride && lane * 16 < BM * 4)
+      dma_load16(rsa, prm, (uint32_t)dma_m0 * 4 + lane * 16);
+    if (wave == 1 && p.sw_stride && lane * 16 < BN * 4)
+      dma_load16(rsw, prm + BM * 4, (uint32_t)dma_n0 * 4 + lane * 16);
+    if (wave == 2 && p.bias && lane * 16 < BN * bias_elem)
+      dma_load16(rb, prm + (BM + BN) * 4, (uint32_t)(dma_n0 * bias_elem) + lane * 16);
   };
   // operand load q (0 .. kLoadsPerStage-1) of stage issue_g
   struct Issue {
     uint8_t *base;
-    int k0;
-    bool kin;
+    uint32_t oa, ow;  // this stage's offsets of load 0, or out of range
   };
   auto issue_setup = [&]() {
     const int k0 = issue_kt * BK;
     // K tail and the stages past my last: out of range -> zeros
-    return Issue{smem + (issue_g % kStages) * kStageBytes + wave * kRowsPerWave * BK, k0,
-                 issue_g < G && k0 + dma_chunk * 16 < p.K};
+    const bool kin = issue_g < G && k0 + dma_chunk * 16 < p.K;
+    uint32_t oa = kin ? offa + k0 : kOutOfRange, ow = kin ? offw + k0 : kOutOfRange;
+    // opaque to the optimizer, so the offsets of loads 1.. are formed per stage
+    // (one add each) rather than hoisted out of the loop into registers
+    asm volatile("" : "+v"(oa), "+v"(ow));
+    return Issue{smem + (issue_g % kStages) * kStageBytes, oa, ow};
   };
+  // (kOutOfRange + l * 16 * ld stays out of range: the host keeps (M + 512) * lda below 2^32.)
   auto issue_load = [&](const Issue &is, int q) {
-    const int l = q >> 1;
-    if (q & 1)
-      dma_load16(rw, is.base + kTileBytes + l * 16 * BK, is.kin ? offw[l] + is.k0 : kOutOfRange);
+    const int l = C::load_index(q);
+    if (C::load_is_w(q))
+      dma_load16(rw, is.base + C::kTileA + (wave * C::kRowsW + l * 16) * BK, is.ow + (uint32_t)(l * 16 * p.ldw));
     else
-      dma_load16(ra, is.base + l * 16 * BK, is.kin ? offa[l] + is.k0 : kOutOfRange);
+      dma_load16(ra, is.base + (wave * C::kRowsA + l * 16) * BK, is.oa + (uint32_t)(l * 16 * p.lda));
   };
   auto issue_advance = [&]() {
     ++issue_g;
@@ -414,18 +447,17 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) 
     lds_barrier();
     issue_params();
     const Issue is = issue_setup();
-    const uint8_t *nx = slot_of(g + 1), *nw = nx + kTileBytes;
+    const uint8_t *nx = slot_of(g + 1), *nw = nx + C::kTileA;
 #pragma unroll
     for (int ks = 0; ks < T::kSteps; ++ks)
 #pragma unroll
       for (int f = 0; f < FN; ++f) wf[c ^ 1][ks][f] = T::load(nw, row_w + f * 32, ks, lane);
     // The operand loads of stage g + kStages are spread over the MFMAs: issued
     // together, the workgroup's loads queue up in the address unit, and a wave
-    // whose load waits there cannot issue its MFMAs either.
+    // whose load waits there cannot issue its MFMAs either.  Slot s (one
+    // activation fragment's MFMAs) issues loads [first(s), first(s + 1)).
     constexpr int kSlots = T::kSteps * FM;
-    constexpr int kEvery = kSlots >= kLoadsPerStage ? kSlots / kLoadsPerStage : 1;
-    constexpr int kPerSlot = kSlots >= kLoadsPerStage ? 1 : kLoadsPerStage / kSlots;
-    static_assert(kSlots % kLoadsPerStage == 0 || kLoadsPerStage % kSlots == 0, "load spacing");
+    auto first = [](int s) { return (s * kLoadsPerStage + kSlots - 1) / kSlots; };
 #pragma unroll
     for (int ks = 0; ks < T::kSteps; ++ks)
 #pragma unroll
@@ -434,20 +466,20 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) 
         for (int i = 0; i < FN; ++i) acc[i][j] = T::mma(wf[c][ks][i], xf[ks][j], acc[i][j]);
         xf[ks][j] = T::load(nx, row_x + j * 32, ks, lane);
         const int slot = ks * FM + j;
-        if (slot % kEvery == 0)
 #pragma unroll
-          for (int u = 0; u < kPerSlot; ++u) issue_load(is, slot / kEvery * kPerSlot + u);
+        for (int q = first(slot); q < first(slot + 1); ++q) issue_load(is, q);
       }
     // Keep that order in the schedule: the weight reads, then per activation
-    // fragment its MFMAs, its refill and (every kEvery fragments) one load.
-    // (Left alone the scheduler issues most MFMAs first and the reads of the
-    // next stage too late.)
+    // fragment its MFMAs, its refill and its share of the loads.  (Left alone
+    // the scheduler issues most MFMAs first and the reads of the next stage
+    // too late.)
     __builtin_amdgcn_sched_group_barrier(kDsRead, T::kReads * T::kSteps * FN, 0);
 #pragma unroll
     for (int k = 0; k < kSlots; ++k) {
       __builtin_amdgcn_sched_group_barrier(kMfma, FN * T::kMfmaPerMma, 0);
       __builtin_amdgcn_sched_group_barrier(kDsRead, T::kReads, 0);
-      if (k % kEvery == 0) __builtin_amdgcn_sched_group_barrier(kVmemRead, kPerSlot, 0);
+#pragma unroll
+      for (int q = first(k); q < first(k + 1); ++q) __builtin_amdgcn_sched_group_barrier(kVmemRead, 1, 0);
     }
     issue_advance();
     if (++kt < KT) return;
@@ -456,38 +488,56 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) 
     // acc[i][j] element e: feature n = n0 + wn*(BN/WN) + i*32 + (e/4)*8 + (lane/32)*4 + e%4,
     //                      token   m = m0 + wm*(BM/WM) + j*32 + lane%32.
     int m0, n0;
-    tile_origin(t_first + tile_i * wgs_per_xcd, p.tiles_m, p.tiles_n, p.group_m, m0, n0);
-    uint8_t *prm = smem + kStages * kStageBytes + (tile_i % kParamSets) * kParamSetBytes;
+    tile_origin<BM, BN>(t_first + tile_i * wgs_per_xcd, p.tiles_m, p.tiles_n, p.group_m, m0, n0);
+    // The lane index, opaque to the optimizer: the epilogue's LDS addresses are
+    // formed here, not hoisted out of the stage loop into registers it needs.
+    int el = lane;
+    asm volatile("" : "+v"(el));
+    uint8_t *prm = smem + kStages * kStageBytes + (tile_i % C::kParamSets) * kParamBytes;
     float *psa = reinterpret_cast<float *>(prm);
-    float *psw = reinterpret_cast<float *>(prm + kParamBytes);
-    float *pbf = reinterpret_cast<float *>(prm + 3 * kParamBytes);
-    // The transpose area: this wave's 4 KB of slot (g+1) % kStages, whose
+    float *psw = reinterpret_cast<float *>(prm + BM * 4);
+    float *pbf = reinterpret_cast<float *>(prm + (BM + BN) * 4);
+    // The bias as stored, read before the barrier that precedes its in-place
+    // conversion to f32 (the parameter DMA completed stages ago).
+    float bias_v[(BN + C::kThreads - 1) / C::kThreads];
+#pragma unroll
+    for (int u = 0; u * C::kThreads < BN; ++u) {
+      const int t = tid + u * C::kThreads;
+      bias_v[u] = p.bias && t < BN ? bias_at(reinterpret_cast<const uint8_t *>(pbf), p.bias_dtype, t) : 0.0f;
+    }
+    // The transpose area: this wave's 32 rows of slot (g+1) % kStages, whose
     // fragments every wave must have read first.  Its next DMA is issued after
     // the barrier of stage g+1.
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     lds_barrier();
     // Parameters as float rows: per-tensor scales broadcast, bias converted
     // (zeros without one), so the loops below read them without branches.
-    if (tid < 256) {
-      if (!p.sa_stride) psa[tid] = sa0;
-    } else {
-      const int t = tid - 256;
-      if (!p.sw_stride) psw[t] = sw0;
-      pbf[t] = p.bias ? bias_at(prm + 2 * kParamBytes, p.bias_dtype, t) : 0.0f;
+#pragma unroll
+    for (int u = 0; u * C::kThreads < BM; ++u) {
+      const int t = tid + u * C::kThreads;
+      if (!p.sa_stride && t < BM) psa[t] = sa0;
+    }
+#pragma unroll
+    for (int u = 0; u * C::kThreads < BN; ++u) {
+      const int t = tid + u * C::kThreads;
+      if (t < BN) {
+        if (!p.sw_stride) psw[t] = sw0;
+        pbf[t] = bias_v[u];
+      }
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);
     lds_barrier();
     uint8_t *xb = smem + ((g + 1) % kStages) * kStageBytes + wave * 32 * kRowBytes;
 #pragma unroll
     for (int j = 0; j < FM; ++j) {
-      const int ml = wm * (BM / WM) + j * 32 + (lane & 31);
+      const int ml = wm * (BM / WM) + j * 32 + (el & 31);
       const float sam = psa[ml];
-      const int wrow = lane & 31;
+      const int wrow = el & 31;
 #pragma unroll
       for (int i = 0; i < FN; ++i)
 #pragma unroll
         for (int gq = 0; gq < 4; ++gq) {
-          const int nl = wn * (BN / WN) + i * 32 + gq * 8 + (lane >> 5) * 4;
+          const int nl = wn * (BN / WN) + i * 32 + gq * 8 + (el >> 5) * 4;
           const f32x4 sw4 = *reinterpret_cast<const f32x4 *>(psw + nl);
           const f32x4 b4 = *reinterpret_cast<const f32x4 *>(pbf + nl);
           const float swv[4] = {sw4.x, sw4.y, sw4.z, sw4.w}, bv[4] = {b4.x, b4.y, b4.z, b4.w};
@@ -501,7 +551,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) 
           // row wrow, 8-byte chunk c8 (4 outputs) of the wave's row, XOR-swizzled
           // by the row's index among the rows of its bank line: conflict-free
           // 64-bit writes
-          const int c8 = i * 8 + gq * 2 + (lane >> 5);
+          const int c8 = i * 8 + gq * 2 + (el >> 5);
           *reinterpret_cast<u32x2 *>(xb + wrow * kRowBytes + ((c8 ^ ((wrow / kRowsPerLine) & (kChunks8 - 1))) << 3)) =
               u32x2{pack_out<OUT_DT>(y[0], y[1]), pack_out<OUT_DT>(y[2], y[3])};
           if constexpr (ACC_OUT) {
@@ -523,7 +573,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) 
       // store them as full row segments (LDS operations of a wave complete in order)
 #pragma unroll
       for (int q = 0; q < 32 / kRowsPerRead; ++q) {
-        const int row = q * kRowsPerRead + lane / kLanesPerRow, c16 = lane % kLanesPerRow;
+        const int row = q * kRowsPerRead + el / kLanesPerRow, c16 = el % kLanesPerRow;
         const int sw4 = (row / kRowsPerLine) & (kChunks8 - 1);
         u32x4 v = *reinterpret_cast<const u32x4 *>(xb + row * kRowBytes + ((c16 ^ (sw4 >> 1)) << 4));
         if (sw4 & 1) v = u32x4{v.z, v.w, v.x, v.y};
@@ -559,7 +609,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) 
   lds_barrier();
   issue_next();
   {
-    const uint8_t *sx = slot_of(0), *sw = sx + kTileBytes;
+    const uint8_t *sx = slot_of(0), *sw = sx + C::kTileA;
 #pragma unroll
     for (int ks = 0; ks < T::kSteps; ++ks) {
 #pragma unroll
@@ -577,27 +627,408 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_w8a8_kernel(GemmArgs p) 
   wait_vmcnt<0>();
 }
 
-// one persistent workgroup per CU (a multiple of the 8 XCDs), never more than the tiles need
+// C::kWgsPerCu persistent workgroups per CU (a multiple of the 8 XCDs), never
+// more than the tiles need
+template <class C>
 dim3 gemm_grid(const GemmArgs &a) {
   const int ntiles = a.tiles_m * a.tiles_n;
-  int wgs = device_cu_count() / 8 * 8;
+  int wgs = device_cu_count() * C::kWgsPerCu / 8 * 8;
   const int need = ((ntiles + 7) / 8) * 8;
   if (wgs > need) wgs = need;
   if (wgs < 8) wgs = 8;
   return dim3((unsigned)wgs);
 }
 
-template <int KIND, int ACT, int OUT_DT>
+template <int KIND, int ACT, int OUT_DT, class C>
 void launch_gemm(const GemmArgs &a, bool acc_out, hipStream_t stream) {
-  const dim3 grid = gemm_grid(a), block(64 * kWavesM * kWavesN);
-  if (acc_out) gemm_w8a8_kernel<KIND, ACT, OUT_DT, true, kWavesM, kWavesN><<<grid, block, 0, stream>>>(a);
-  else gemm_w8a8_kernel<KIND, ACT, OUT_DT, false, kWavesM, kWavesN><<<grid, block, 0, stream>>>(a);
+  const dim3 grid = gemm_grid<C>(a), block(C::kThreads);
+  if (acc_out) gemm_w8a8_kernel<KIND, ACT, OUT_DT, true, C><<<grid, block, 0, stream>>>(a);
+  else gemm_w8a8_kernel<KIND, ACT, OUT_DT, false, C><<<grid, block, 0, stream>>>(a);
+}
+
+template <int KIND, class C>
+void launch_gemm_gated(const GemmArgs &a, hipStream_t stream) {
+  gemm_w8a8_kernel<KIND, XGEN_ACT_NONE, XGEN_DTYPE_BF16, false, C, true>
+      <<<gemm_grid<C>(a), dim3(C::kThreads), 0, stream>>>(a);
+}
+
+// ---------------------------------------------------------------------------
+// FP8 / INT8 kernel with one wave per SIMD.  Four waves (2 x 2) share a
+// 256 x 256 output tile; each wave owns a 128 x 128 block, 4 x 4 MFMA
+// fragments whose 256 accumulators live in AGPRs, and issues 16 MFMAs (FP8;
+// 32 for INT8) per 64-byte K stage from its own instruction stream, so the
+// stage's barrier syncs four waves and the LDS read traffic is 1 KB per
+// MFMA (two waves per SIMD at 128 x 64 read 1.5 KB).
+// ---------------------------------------------------------------------------
+namespace w4 {
+constexpr int kWaves = 4, kThreads = 256;
+constexpr int kSlots = 4;                      // LDS ring depth, 64-byte K stages
+constexpr int kTileBytes = 256 * BK;           // one operand tile of one stage: 16 KB
+constexpr int kSlotBytes = 2 * kTileBytes;     // activations + weights: 32 KB
+constexpr int kRowsPerWave = 256 / kWaves;     // DMA rows per operand per wave
+constexpr int kLoads = kRowsPerWave / 16;      // 1 KB DMA loads per operand per wave per stage
+constexpr int kLoadsPerStage = 2 * kLoads;     // per thread
+// One parameter set: [sa f32 x 256][sw f32 x 256][bias as stored: <= 1 KB].
+// A full 1 KB DMA load per row, so a 2-byte bias row's second half takes the
+// next bytes (or zeros) without leaving its row.
+constexpr int kParamBytes = 3 * 1024;
+// Tiles have a multiple of 4 stages, so the next tile's parameters (issued 4
+// stages ahead of its first stage) are never issued before this tile's
+// epilogue has read its set: two sets alternate.
+constexpr int kParamSets = 2;
+// Each wave's epilogue first copies its 128 tokens' and 128 features'
+// parameters into a private area as f32 rows (per-tensor scales broadcast, the
+// bias converted, zeros without one): [sa x 128][sw x 128][bias x 128].
+constexpr int kPrivBytes = 3 * 128 * 4;
+constexpr int kLdsBytes = kSlots * kSlotBytes + kParamSets * kParamBytes + kWaves * kPrivBytes;
+constexpr int kWaveRows = 128;                 // rows of a wave's block, both dimensions
+constexpr int kXpose = 32 * 256;               // a wave's epilogue transpose rows: 32 x 256 bytes
+}  // namespace w4
+
+// Loads [first(s), first(s + 1)) of n loads spread over `slots` MFMA slots.
+__host__ __device__ constexpr int spread_first(int s, int n, int slots) { return (s * n + slots - 1) / slots; }
+
+// The MFMAs of the one-wave-per-SIMD kernel, with their accumulators pinned
+// to AGPRs ("+a"): left to the register allocator, 256 accumulators plus the
+// double-buffered fragments are shuffled between the register files and
+// spilled.  The compiler sees these as opaque, so the kernel itself keeps the
+// MFMA result hazards: a tile's first MFMA per accumulator adds an
+// inline-constant zero (no VALU writes to accumulators at all), and the
+// epilogue reads accumulators only after mfma_drain's wait states behind the
+// tile's last MFMA.  Operand registers are written only by LDS loads, which
+// the compiler's wait counts order before the MFMA that reads them; a buffer
+// is reloaded only after the barrier that follows its last MFMA.
+template <int KIND>
+struct MfmaA;
+template <>
+struct MfmaA<kFp8> {
+  static __device__ __forceinline__ void mma(f32x16 &c, const i32x8 &w, const i32x8 &x) {
+    asm volatile("v_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, %0" : "+a"(c) : "v"(w), "v"(x));
+  }
+  // c = w x (the accumulator's first product: an inline-constant zero addend)
+  static __device__ __forceinline__ void mma0(f32x16 &c, const i32x8 &w, const i32x8 &x) {
+    asm volatile("v_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, 0" : "=a"(c) : "v"(w), "v"(x));
+  }
+};
+template <>
+struct MfmaA<kInt8> {
+  static __device__ __forceinline__ void mma(i32x16 &c, const i32x4 &w, const i32x4 &x) {
+    asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+a"(c) : "v"(w), "v"(x));
+  }
+  static __device__ __forceinline__ void mma0(i32x16 &c, const i32x4 &w, const i32x4 &x) {
+    asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, 0" : "=a"(c) : "v"(w), "v"(x));
+  }
+};
+// 24 wait states after the last MFMAs before any accumulator is read by VALU
+// (16-pass MFMAs need 18 on gfx950).  Every accumulator is an operand, so no
+// read of one is scheduled above it.
+template <class A>
+__device__ __forceinline__ void mfma_drain(A (&acc)[4][4]) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7"
+               : "+a"(acc[0][0]), "+a"(acc[1][0]), "+a"(acc[2][0]), "+a"(acc[3][0]), "+a"(acc[0][1]),
+                 "+a"(acc[1][1]), "+a"(acc[2][1]), "+a"(acc[3][1]));
+  asm volatile("" : "+a"(acc[0][2]), "+a"(acc[1][2]), "+a"(acc[2][2]), "+a"(acc[3][2]), "+a"(acc[0][3]),
+                    "+a"(acc[1][3]), "+a"(acc[2][3]), "+a"(acc[3][3]));
+}
+
+template <int KIND, int ACT, int OUT_DT, bool ACC_OUT, bool GATED>
+__global__ __attribute__((amdgpu_flat_work_group_size(w4::kThreads, w4::kThreads), amdgpu_waves_per_eu(1, 1)))
+void gemm_w4_kernel(GemmArgs p) {
+  using namespace w4;
+  typedef Mfma<KIND> T;
+  typedef typename T::frag_t frag_t;
+  constexpr int FM = 4, FN = 4, KS = T::kSteps;
+  constexpr int kMfmas = KS * FM * FN;                 // per stage per wave
+  constexpr int kReads = T::kReads * KS * (FM + FN);   // ds_read_b128 per stage per wave
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kLdsBytes];
+
+  // --- this workgroup's tiles (as gemm_w8a8_kernel) ---------------------------
+  const int ntiles = p.tiles_m * p.tiles_n;
+  const int xcd = blockIdx.x & 7, local = blockIdx.x >> 3, wgs_per_xcd = gridDim.x >> 3;
+  const int t_first = xcd * p.per_xcd + local;
+  const int t_end = min((xcd + 1) * p.per_xcd, ntiles);
+  const int n_my = t_first < t_end ? (t_end - t_first + wgs_per_xcd - 1) / wgs_per_xcd : 0;
+  if (n_my == 0) return;
+  const int KT = p.kt4;  // stages per tile: a multiple of 4; stages past K read zeros
+  const int G = n_my * KT;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(p.a), (short)0, (int)p.a_bytes, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(p.w), (short)0, (int)p.w_bytes, kBufferFlags);
+  const int bias_elem = p.bias_dtype == XGEN_DTYPE_F32 ? 4 : 2;
+  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(p.sa), (short)0, p.M * 4, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(p.sw), (short)0, p.N * 4, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void *>(p.bias), (short)0, p.bias ? p.N * bias_elem : 0, kBufferFlags);
+  const float sa0 = p.sa_stride ? 0.0f : p.sa[0];  // per-tensor scales
+  const float sw0 = p.sw_stride ? 0.0f : p.sw[0];
+
+  // --- global -> LDS DMA (layout as gemm_w8a8_kernel: chunk c of row r at
+  // c ^ ((r >> 2) & 3); wave w fills rows [64 w, 64 w + 64) of both tiles) ---
+  const int dma_chunk = (lane & 3) ^ ((lane >> 4) & 3);
+  uint32_t offa = 0, offw = 0;  // byte offsets of this lane's first rows in the DMA's tile
+  int dma_m0 = 0, dma_n0 = 0;
+  auto set_dma_tile = [&](int i) {
+    tile_origin<256, 256>(t_first + i * wgs_per_xcd, p.tiles_m, p.tiles_n, p.group_m, dma_m0, dma_n0);
+    offa = (uint32_t)(dma_m0 + wave * kRowsPerWave + (lane >> 2)) * (uint32_t)p.lda + dma_chunk * 16;
+    offw = (uint32_t)(dma_n0 + wave * kRowsPerWave + (lane >> 2)) * (uint32_t)p.ldw + dma_chunk * 16;
+  };
+  int dma_h = 0, dma_k = 0, dma_i = 0;  // next stage to load: stage dma_k of my tile dma_i
+  // this stage's load offsets (load 0 of each operand), or out of range
+  struct Issue {
+    uint32_t oa, ow;
+    uint32_t lds;  // offset of this wave's DMA area of slot 0 (the loads' LDS addresses are formed from it per stage)
+  };
+  auto issue_begin = [&](int slot) {
+    if (dma_k == 0 && dma_h < G) {  // the tile's epilogue parameters ride with its first stage
+      uint8_t *prm = smem + kSlots * kSlotBytes + (dma_i & 1) * kParamBytes;
+      if (wave == 0 && p.sa_stride) dma_load16(rsa, prm, (uint32_t)dma_m0 * 4 + lane * 16);
+      if (wave == 1 && p.sw_stride) dma_load16(rsw, prm + 1024, (uint32_t)dma_n0 * 4 + lane * 16);
+      if (wave == 2 && p.bias) dma_load16(rb, prm + 2048, (uint32_t)(dma_n0 * bias_elem) + lane * 16);
+    }
+    const int k0 = dma_k * BK;
+    const bool kin = dma_h < G && k0 + dma_chunk * 16 < p.K;
+    uint32_t oa = kin ? offa + k0 : kOutOfRange, ow = kin ? offw + k0 : kOutOfRange;
+    uint32_t lds = (uint32_t)wave * kRowsPerWave * BK;
+    asm volatile("" : "+v"(oa), "+v"(ow), "+s"(lds));  // keep the per-load adds per stage (registers)
+    (void)slot;
+    return Issue{oa, ow, lds};
+  };
+  // load q of the stage going to `slot`: A loads are even q, W loads odd q
+  // (kOutOfRange + l * 16 * ld stays out of range: the host keeps (M + 512) * lda below 2^32)
+  auto issue_load = [&](const Issue &is, int slot, int q) {
+    const int l = q >> 1;
+    uint8_t *dst = smem + is.lds + slot * kSlotBytes + l * 16 * BK;
+    if (q & 1) dma_load16(rw, dst + kTileBytes, is.ow + (uint32_t)(l * 16 * p.ldw));
+    else dma_load16(ra, dst, is.oa + (uint32_t)(l * 16 * p.lda));
+  };
+  auto issue_end = [&]() {
+    ++dma_h;
+    if (++dma_k == KT) {
+      dma_k = 0;
+      if (++dma_i < n_my) set_dma_tile(dma_i);
+    }
+  };
+
+  // --- fragments ---------------------------------------------------------------
+  const int row_x = wm * kWaveRows + (lane & 31);
+  const int row_w = wn * kWaveRows + (lane & 31);
+  frag_t xf[2][KS][FM], wf[2][KS][FN];  // [register buffer][k step][fragment]
+  auto read_x = [&](int b, int slot, int ks, int j) {
+    xf[b][ks][j] = T::load(smem + slot * kSlotBytes, row_x + j * 32, ks, lane);
+  };
+  auto read_w = [&](int b, int slot, int ks, int i) {
+    wf[b][ks][i] = T::load(smem + slot * kSlotBytes + kTileBytes, row_w + i * 32, ks, lane);
+  };
+
+  // defined by each tile's first stage (mma0), read by its epilogue
+  typename T::acc_t acc[FN][FM];
+
+  // --- epilogue: parameters, dequant + bias (+ GELU), transpose, row stores ---
+  int tile_i = 0;
+  auto epilogue = [&]() {
+    int m0, n0;
+    tile_origin<256, 256>(t_first + tile_i * wgs_per_xcd, p.tiles_m, p.tiles_n, p.group_m, m0, n0);
+    const uint8_t *prm = smem + kSlots * kSlotBytes + (tile_i & 1) * kParamBytes;
+    // the lane index, opaque: the epilogue's addresses are formed here, not
+    // hoisted into registers the stage loop needs
+    int el = lane;
+    asm volatile("" : "+v"(el));
+    const int wrow = el & 31, half = el >> 5;
+    // this wave's parameters as f32 rows (a wave's LDS operations complete in
+    // order: its reads below see these writes)
+    float *priv = reinterpret_cast<float *>(smem + kSlots * kSlotBytes + kParamSets * kParamBytes + wave * kPrivBytes);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int t = h * 64 + el;
+      const int ma = wm * kWaveRows + t, nb = wn * kWaveRows + t;
+      priv[t] = p.sa_stride ? reinterpret_cast<const float *>(prm)[ma] : sa0;
+      priv[128 + t] = p.sw_stride ? reinterpret_cast<const float *>(prm + 1024)[nb] : sw0;
+      priv[256 + t] = p.bias ? bias_at(prm + 2048, p.bias_dtype, nb) : 0.0f;
+    }
+    uint8_t *xb = smem + wave * kXpose;  // slot 0: read by every wave before the barrier below
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+      const int ml = wm * kWaveRows + j * 32 + wrow;
+      const float sam = priv[j * 32 + wrow];
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          const int nw = i * 32 + gq * 8 + half * 4;  // feature within the wave's block
+          const int nl = wn * kWaveRows + nw;
+          const f32x4 sw4 = *reinterpret_cast<const f32x4 *>(priv + 128 + nw);
+          const f32x4 b4 = *reinterpret_cast<const f32x4 *>(priv + 256 + nw);
+          float y[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float a = T::to_f32(acc[i][j][gq * 4 + e]);
+            y[e] = __builtin_fmaf(a, sam * sw4[e], b4[e]);
+            if constexpr (ACT == XGEN_ACT_GELU_TANH) y[e] = gelu_tanh(round_out<OUT_DT>(y[e]));
+          }
+          // row wrow, 8-byte chunk c8 of its 256 bytes, at c8 ^ wrow: the 32
+          // lanes of each half write 32 distinct bank pairs
+          const int c8 = i * 8 + gq * 2 + half;
+          *reinterpret_cast<u32x2 *>(xb + wrow * 256 + ((c8 ^ wrow) << 3)) =
+              u32x2{pack_out<OUT_DT>(y[0], y[1]), pack_out<OUT_DT>(y[2], y[3])};
+          if constexpr (ACC_OUT) {
+            const int m = m0 + ml, n = n0 + nl;
+            if (m < p.M && n < p.N) {
+              if constexpr (KIND != kInt8) {
+                const f32x4 v = {acc[i][j][gq * 4 + 0], acc[i][j][gq * 4 + 1], acc[i][j][gq * 4 + 2],
+                                 acc[i][j][gq * 4 + 3]};
+                *reinterpret_cast<f32x4 *>(static_cast<float *>(p.acc_out) + (int64_t)m * p.N + n) = v;
+              } else {
+                const i32x4 v = {acc[i][j][gq * 4 + 0], acc[i][j][gq * 4 + 1], acc[i][j][gq * 4 + 2],
+                                 acc[i][j][gq * 4 + 3]};
+                *reinterpret_cast<i32x4 *>(static_cast<int32_t *>(p.acc_out) + (int64_t)m * p.N + n) = v;
+              }
+            }
+          }
+        }
+      // read back 4 whole rows per instruction (16 lanes x 16 bytes per row)
+      // and store them as 256-byte row segments; a wave's LDS operations
+      // complete in order, so the reads see its writes above
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int row = q * 4 + (el >> 4), c16 = el & 15;
+        u32x4 v = *reinterpret_cast<const u32x4 *>(xb + row * 256 + (((2 * c16) ^ (row & ~1)) << 3));
+        if (row & 1) v = u32x4{v.z, v.w, v.x, v.y};
+        const int m = m0 + wm * kWaveRows + j * 32 + row;
+        const int n = n0 + wn * kWaveRows + c16 * 8;
+        if (m < p.M && n < p.N) {
+          if constexpr (GATED) {
+            const int64_t gi = p.indices[(uint32_t)m % p.seq];
+            if (gi >= 0 && gi < p.gate_rows) {
+              const u32x4 r = *reinterpret_cast<const u32x4 *>(p.residual + ((int64_t)m * p.ld_residual + n) * 2);
+              const u32x4 t = *reinterpret_cast<const u32x4 *>(p.gate + (gi * p.gate_stride + n) * 2);
+              v = gate_residual8(r, v, t);
+            } else {
+              v = u32x4{0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};  // index outside the table: NaN
+            }
+          }
+          *reinterpret_cast<u32x4 *>(static_cast<uint16_t *>(p.out) + (int64_t)m * p.ldo + n) = v;
+        }
+      }
+    }
+    ++tile_i;
+  };
+
+  // --- one stage, slot U = g % 4 ---------------------------------------------
+  // At the top: this thread's DMA of stage g+1 has landed (at most the loads of
+  // stages g+2 and g+3 outstanding) and its fragment reads of stage g are in
+  // registers; the barrier publishes every wave's DMA of stage g+1 and retires
+  // every wave's reads of slot U, which then takes the DMA of stage g+4.
+  // During the stage: the MFMAs of stage g (register buffer U & 1), the reads
+  // of stage g+1 (slot U+1, buffer (U+1) & 1) and the DMA of stage g+4 (slot U),
+  // interleaved.
+  auto stage = [&](auto U, auto FRESH) {
+    constexpr int u = decltype(U)::value;
+    constexpr bool fresh = decltype(FRESH)::value;  // the tile's first stage
+    constexpr int cb = u & 1, nb = cb ^ 1, ns = (u + 1) & 3;
+    wait_vmcnt<2 * kLoadsPerStage>();
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    lds_barrier();
+    const Issue is = issue_begin(u);
+    // The MFMAs are volatile asm statements, so the loads written between them
+    // stay in this order: per MFMA, its share of the next stage's fragment
+    // reads (weights first) and of the DMA loads.
+#pragma unroll
+    for (int s = 0; s < kMfmas; ++s) {
+      const int ks = s / (FM * FN), j = (s / FN) % FM, i = s % FN;
+      if (fresh && ks == 0) MfmaA<KIND>::mma0(acc[i][j], wf[cb][ks][i], xf[cb][ks][j]);
+      else MfmaA<KIND>::mma(acc[i][j], wf[cb][ks][i], xf[cb][ks][j]);
+#pragma unroll
+      for (int r = spread_first(s, kReads / T::kReads, kMfmas); r < spread_first(s + 1, kReads / T::kReads, kMfmas); ++r) {
+        const int rks = r / (FM + FN), f = r % (FM + FN);
+        if (f < FN) read_w(nb, ns, rks, f);
+        else read_x(nb, ns, rks, f - FN);
+      }
+#pragma unroll
+      for (int q = spread_first(s, kLoadsPerStage, kMfmas); q < spread_first(s + 1, kLoadsPerStage, kMfmas); ++q)
+        issue_load(is, u, q);
+    }
+    issue_end();
+  };
+  typedef std::integral_constant<int, 0> S0;
+  typedef std::integral_constant<int, 1> S1;
+  typedef std::integral_constant<int, 2> S2;
+  typedef std::integral_constant<int, 3> S3;
+  typedef std::integral_constant<bool, true> Fresh;
+  typedef std::integral_constant<bool, false> Acc;
+
+  // --- prologue: stages 0..3 in flight, stage 0's fragments in registers -------
+  set_dma_tile(0);
+  {
+    Issue is = issue_begin(0);
+#pragma unroll
+    for (int q = 0; q < kLoadsPerStage; ++q) issue_load(is, 0, q);
+    issue_end();
+    is = issue_begin(1);
+#pragma unroll
+    for (int q = 0; q < kLoadsPerStage; ++q) issue_load(is, 1, q);
+    issue_end();
+    is = issue_begin(2);
+#pragma unroll
+    for (int q = 0; q < kLoadsPerStage; ++q) issue_load(is, 2, q);
+    issue_end();
+    wait_vmcnt<2 * kLoadsPerStage>();
+    lds_barrier();
+    is = issue_begin(3);
+#pragma unroll
+    for (int q = 0; q < kLoadsPerStage; ++q) issue_load(is, 3, q);
+    issue_end();
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+      for (int i = 0; i < FN; ++i) read_w(0, 0, ks, i);
+#pragma unroll
+      for (int j = 0; j < FM; ++j) read_x(0, 0, ks, j);
+    }
+  }
+  // --- main loop: per tile, its stages four at a time (static slots and
+  // register buffers), then its epilogue ------------------------------------
+  for (int t = 0; t < n_my; ++t) {
+    stage(S0(), Fresh());
+    stage(S1(), Acc());
+    stage(S2(), Acc());
+    stage(S3(), Acc());
+    for (int c = 4; c < KT; c += 4) {
+      stage(S0(), Acc());
+      stage(S1(), Acc());
+      stage(S2(), Acc());
+      stage(S3(), Acc());
+    }
+    // every wave's reads of slot 0 (the next tile's first stage) are done
+    // before it becomes the transpose area; its next DMA is issued after the
+    // barrier at the top of the next stage
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    lds_barrier();
+    mfma_drain(acc);
+    epilogue();
+  }
+  // the loads of the stages past my last may still be writing LDS
+  wait_vmcnt<0>();
+}
+
+template <int KIND, int ACT, int OUT_DT>
+void launch_gemm_w4(const GemmArgs &a, bool acc_out, hipStream_t stream) {
+  const dim3 grid = gemm_grid<TileMain>(a), block(w4::kThreads);
+  if (acc_out) gemm_w4_kernel<KIND, ACT, OUT_DT, true, false><<<grid, block, 0, stream>>>(a);
+  else gemm_w4_kernel<KIND, ACT, OUT_DT, false, false><<<grid, block, 0, stream>>>(a);
 }
 
 template <int KIND>
-void launch_gemm_gated(const GemmArgs &a, hipStream_t stream) {
-  gemm_w8a8_kernel<KIND, XGEN_ACT_NONE, XGEN_DTYPE_BF16, false, kWavesM, kWavesN, true>
-      <<<gemm_grid(a), dim3(64 * kWavesM * kWavesN), 0, stream>>>(a);
+void launch_gemm_w4_gated(const GemmArgs &a, hipStream_t stream) {
+  gemm_w4_kernel<KIND, XGEN_ACT_NONE, XGEN_DTYPE_BF16, false, true>
+      <<<gemm_grid<TileMain>(a), dim3(w4::kThreads), 0, stream>>>(a);
 }
 
 struct GateParams {  // the gated residual epilogue's inputs (null residual: plain GEMM)
@@ -650,6 +1081,9 @@ int gemm_entry(const char *fn, const void *a, int64_t lda, const void *w, int64_
   const int64_t a_bytes = (M - 1) * lda + K, w_bytes = (N - 1) * ldw + K;
   if (a_bytes >= (int64_t)kOutOfRange || w_bytes >= (int64_t)kOutOfRange)
     return fail(XGEN_ERR_UNSUPPORTED, "%s: operands above 2 GiB", fn);
+  // the DMA offsets of the rows past M / N of the last tiles stay below 2^32
+  if ((uint64_t)(M + 512) * (uint64_t)lda >= (1ull << 32) || (uint64_t)(N + 512) * (uint64_t)ldw >= (1ull << 32))
+    return fail(XGEN_ERR_UNSUPPORTED, "%s: operand rows too long for 32-bit offsets", fn);
 
   GemmArgs g;
   g.a = static_cast<const uint8_t *>(a);
@@ -668,8 +1102,9 @@ int gemm_entry(const char *fn, const void *a, int64_t lda, const void *w, int64_
   g.out = out;
   g.ldo = ldo;
   g.acc_out = acc_out;
-  g.tiles_m = (int)((M + BM - 1) / BM);
-  g.tiles_n = (int)((N + BN - 1) / BN);
+  typedef TileMain C;
+  g.tiles_m = (int)((M + C::BM - 1) / C::BM);
+  g.tiles_n = (int)((N + C::BN - 1) / C::BN);
   g.per_xcd = (g.tiles_m * g.tiles_n + 7) / 8;
   // The 32 tiles one XCD runs at once span group_m tile-rows.  Measured at
   // M=15,624: 4 rows beat 8 for outputs of 24-63 tile-columns (QKV N=9,216
@@ -686,15 +1121,29 @@ int gemm_entry(const char *fn, const void *a, int64_t lda, const void *w, int64_
   g.gate_rows = gp.gate_rows;
   g.indices = gp.indices;
   g.seq = (uint32_t)gp.seq;
+  g.kt4 = (int)(((K + BK - 1) / BK + 3) / 4 * 4);
   const bool with_acc = acc_out != nullptr;
+  if constexpr (KIND != kFp8Exact) {
+    // FP8 and INT8: the one-wave-per-SIMD kernel
+    if (gated) {
+      launch_gemm_w4_gated<KIND>(g, stream);
+    } else if (activation == XGEN_ACT_NONE) {
+      if (out_dtype == XGEN_DTYPE_BF16) launch_gemm_w4<KIND, XGEN_ACT_NONE, XGEN_DTYPE_BF16>(g, with_acc, stream);
+      else launch_gemm_w4<KIND, XGEN_ACT_NONE, XGEN_DTYPE_F16>(g, with_acc, stream);
+    } else {
+      if (out_dtype == XGEN_DTYPE_BF16) launch_gemm_w4<KIND, XGEN_ACT_GELU_TANH, XGEN_DTYPE_BF16>(g, with_acc, stream);
+      else launch_gemm_w4<KIND, XGEN_ACT_GELU_TANH, XGEN_DTYPE_F16>(g, with_acc, stream);
+    }
+    return launch_status(fn);
+  }
   if (gated) {
-    launch_gemm_gated<KIND>(g, stream);
+    launch_gemm_gated<KIND, C>(g, stream);
   } else if (activation == XGEN_ACT_NONE) {
-    if (out_dtype == XGEN_DTYPE_BF16) launch_gemm<KIND, XGEN_ACT_NONE, XGEN_DTYPE_BF16>(g, with_acc, stream);
-    else launch_gemm<KIND, XGEN_ACT_NONE, XGEN_DTYPE_F16>(g, with_acc, stream);
+    if (out_dtype == XGEN_DTYPE_BF16) launch_gemm<KIND, XGEN_ACT_NONE, XGEN_DTYPE_BF16, C>(g, with_acc, stream);
+    else launch_gemm<KIND, XGEN_ACT_NONE, XGEN_DTYPE_F16, C>(g, with_acc, stream);
   } else {
-    if (out_dtype == XGEN_DTYPE_BF16) launch_gemm<KIND, XGEN_ACT_GELU_TANH, XGEN_DTYPE_BF16>(g, with_acc, stream);
-    else launch_gemm<KIND, XGEN_ACT_GELU_TANH, XGEN_DTYPE_F16>(g, with_acc, stream);
+    if (out_dtype == XGEN_DTYPE_BF16) launch_gemm<KIND, XGEN_ACT_GELU_TANH, XGEN_DTYPE_BF16, C>(g, with_acc, stream);
+    else launch_gemm<KIND, XGEN_ACT_GELU_TANH, XGEN_DTYPE_F16, C>(g, with_acc, stream);
   }
   return launch_status(fn);
 }
