@@ -105,6 +105,7 @@ struct GemmArgs {
   int tiles_m, tiles_n, per_xcd;
   int group_m;  // tile-rows per group of the tile order
   int kt4;      // stages per tile of the one-wave-per-SIMD kernel (a multiple of 4)
+  uint32_t out_bytes;  // bytes of the output rows: (M - 1) * ldo * 2 + N * 2
   uint32_t a_bytes, w_bytes;
   // gated residual epilogue (GATED kernels only)
   const uint8_t *residual;
@@ -676,13 +677,12 @@ constexpr int kParamBytes = 3 * 1024;
 // stages ahead of its first stage) are never issued before this tile's
 // epilogue has read its set: two sets alternate.
 constexpr int kParamSets = 2;
-// Each wave's epilogue first copies its 128 tokens' and 128 features'
-// parameters into a private area as f32 rows (per-tensor scales broadcast, the
-// bias converted, zeros without one): [sa x 128][sw x 128][bias x 128].
-constexpr int kPrivBytes = 3 * 128 * 4;
-constexpr int kLdsBytes = kSlots * kSlotBytes + kParamSets * kParamBytes + kWaves * kPrivBytes;
 constexpr int kWaveRows = 128;                 // rows of a wave's block, both dimensions
-constexpr int kXpose = 32 * 256;               // a wave's epilogue transpose rows: 32 x 256 bytes
+// A wave's epilogue transpose area, its own (no barrier): 32 rows of 128
+// bytes, half of its block's 128 features at a time.
+constexpr int kXpose = 32 * 128;
+constexpr int kXposeBase = kSlots * kSlotBytes + kParamSets * kParamBytes;
+constexpr int kLdsBytes = kXposeBase + kWaves * kXpose;  // 150 KB
 }  // namespace w4
 
 // Loads [first(s), first(s + 1)) of n loads spread over `slots` MFMA slots.
@@ -769,6 +769,8 @@ void gemm_w4_kernel(GemmArgs p) {
       const_cast<void *>(p.bias), (short)0, p.bias ? p.N * bias_elem : 0, kBufferFlags);
   const float sa0 = p.sa_stride ? 0.0f : p.sa[0];  // per-tensor scales
   const float sw0 = p.sw_stride ? 0.0f : p.sw[0];
+  // the output rows as a buffer: stores at kOutOfRange are dropped
+  const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(p.out, (short)0, (int)p.out_bytes, kBufferFlags);
 
   // --- global -> LDS DMA (layout as gemm_w8a8_kernel: chunk c of row r at
   // c ^ ((r >> 2) & 3); wave w fills rows [64 w, 64 w + 64) of both tiles) ---
@@ -791,7 +793,8 @@ void gemm_w4_kernel(GemmArgs p) {
       uint8_t *prm = smem + kSlots * kSlotBytes + (dma_i & 1) * kParamBytes;
       if (wave == 0 && p.sa_stride) dma_load16(rsa, prm, (uint32_t)dma_m0 * 4 + lane * 16);
       if (wave == 1 && p.sw_stride) dma_load16(rsw, prm + 1024, (uint32_t)dma_n0 * 4 + lane * 16);
-      if (wave == 2 && p.bias) dma_load16(rb, prm + 2048, (uint32_t)(dma_n0 * bias_elem) + lane * 16);
+      // (without a bias the resource is empty: the row reads as zeros)
+      if (wave == 2) dma_load16(rb, prm + 2048, (uint32_t)(dma_n0 * bias_elem) + lane * 16);
     }
     const int k0 = dma_k * BK;
     const bool kin = dma_h < G && k0 + dma_chunk * 16 < p.K;
@@ -831,90 +834,138 @@ void gemm_w4_kernel(GemmArgs p) {
   // defined by each tile's first stage (mma0), read by its epilogue
   typename T::acc_t acc[FN][FM];
 
-  // --- epilogue: parameters, dequant + bias (+ GELU), transpose, row stores ---
+  // --- epilogue: dequant + bias (+ GELU), transpose, row stores ---------------
+  // acc[i][j] element e: feature n = n0 + wn*128 + i*32 + (e/4)*8 + (lane/32)*4 + e%4,
+  //                      token   m = m0 + wm*128 + j*32 + lane%32.
   int tile_i = 0;
   auto epilogue = [&]() {
     int m0, n0;
     tile_origin<256, 256>(t_first + tile_i * wgs_per_xcd, p.tiles_m, p.tiles_n, p.group_m, m0, n0);
     const uint8_t *prm = smem + kSlots * kSlotBytes + (tile_i & 1) * kParamBytes;
+    const float *psa = reinterpret_cast<const float *>(prm);
+    const float *psw = reinterpret_cast<const float *>(prm + 1024);
+    const uint8_t *pb = prm + 2048;
     // the lane index, opaque: the epilogue's addresses are formed here, not
     // hoisted into registers the stage loop needs
     int el = lane;
     asm volatile("" : "+v"(el));
     const int wrow = el & 31, half = el >> 5;
-    // this wave's parameters as f32 rows (a wave's LDS operations complete in
-    // order: its reads below see these writes)
-    float *priv = reinterpret_cast<float *>(smem + kSlots * kSlotBytes + kParamSets * kParamBytes + wave * kPrivBytes);
+    uint8_t *xb = smem + kXposeBase + wave * kXpose;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int t = h * 64 + el;
-      const int ma = wm * kWaveRows + t, nb = wn * kWaveRows + t;
-      priv[t] = p.sa_stride ? reinterpret_cast<const float *>(prm)[ma] : sa0;
-      priv[128 + t] = p.sw_stride ? reinterpret_cast<const float *>(prm + 1024)[nb] : sw0;
-      priv[256 + t] = p.bias ? bias_at(prm + 2048, p.bias_dtype, nb) : 0.0f;
-    }
-    uint8_t *xb = smem + wave * kXpose;  // slot 0: read by every wave before the barrier below
+    for (int h = 0; h < 2; ++h) {  // features [64 h, 64 h + 64) of the wave's block
+      // this lane's 32 features' scales and bias of this half, as f32:
+      // [ii][gq] = features wn*128 + (2h + ii)*32 + gq*8 + half*4 .. +3
+      // (one uniform branch per parameter kind around all of a half's reads,
+      // so they issue together and are waited for once)
+      f32x4 swr[2][4], bir[2][4];
+      const int nl0 = wn * kWaveRows + 2 * h * 32 + half * 4;  // + ii*32 + gq*8
+      if (p.sw_stride) {
 #pragma unroll
-    for (int j = 0; j < FM; ++j) {
-      const int ml = wm * kWaveRows + j * 32 + wrow;
-      const float sam = priv[j * 32 + wrow];
+        for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
-      for (int i = 0; i < FN; ++i)
+          for (int gq = 0; gq < 4; ++gq) swr[ii][gq] = *reinterpret_cast<const f32x4 *>(psw + nl0 + ii * 32 + gq * 8);
+      } else {
 #pragma unroll
-        for (int gq = 0; gq < 4; ++gq) {
-          const int nw = i * 32 + gq * 8 + half * 4;  // feature within the wave's block
-          const int nl = wn * kWaveRows + nw;
-          const f32x4 sw4 = *reinterpret_cast<const f32x4 *>(priv + 128 + nw);
-          const f32x4 b4 = *reinterpret_cast<const f32x4 *>(priv + 256 + nw);
-          float y[4];
+        for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float a = T::to_f32(acc[i][j][gq * 4 + e]);
-            y[e] = __builtin_fmaf(a, sam * sw4[e], b4[e]);
-            if constexpr (ACT == XGEN_ACT_GELU_TANH) y[e] = gelu_tanh(round_out<OUT_DT>(y[e]));
-          }
-          // row wrow, 8-byte chunk c8 of its 256 bytes, at c8 ^ wrow: the 32
-          // lanes of each half write 32 distinct bank pairs
-          const int c8 = i * 8 + gq * 2 + half;
-          *reinterpret_cast<u32x2 *>(xb + wrow * 256 + ((c8 ^ wrow) << 3)) =
-              u32x2{pack_out<OUT_DT>(y[0], y[1]), pack_out<OUT_DT>(y[2], y[3])};
-          if constexpr (ACC_OUT) {
-            const int m = m0 + ml, n = n0 + nl;
-            if (m < p.M && n < p.N) {
-              if constexpr (KIND != kInt8) {
-                const f32x4 v = {acc[i][j][gq * 4 + 0], acc[i][j][gq * 4 + 1], acc[i][j][gq * 4 + 2],
-                                 acc[i][j][gq * 4 + 3]};
-                *reinterpret_cast<f32x4 *>(static_cast<float *>(p.acc_out) + (int64_t)m * p.N + n) = v;
-              } else {
-                const i32x4 v = {acc[i][j][gq * 4 + 0], acc[i][j][gq * 4 + 1], acc[i][j][gq * 4 + 2],
-                                 acc[i][j][gq * 4 + 3]};
-                *reinterpret_cast<i32x4 *>(static_cast<int32_t *>(p.acc_out) + (int64_t)m * p.N + n) = v;
+          for (int gq = 0; gq < 4; ++gq) swr[ii][gq] = f32x4{sw0, sw0, sw0, sw0};
+      }
+      if (p.bias_dtype == XGEN_DTYPE_F32) {
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq) bir[ii][gq] = *reinterpret_cast<const f32x4 *>(pb + (nl0 + ii * 32 + gq * 8) * 4);
+      } else {
+        // 2-byte bias (or none: the set's bias row then holds zeros, which
+        // decode to 0.0 either way)
+        u32x2 raw[2][4];
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq) raw[ii][gq] = *reinterpret_cast<const u32x2 *>(pb + (nl0 + ii * 32 + gq * 8) * 2);
+        if (p.bias_dtype == XGEN_DTYPE_F16) {
+#pragma unroll
+          for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq) {
+              const u32x2 w2 = raw[ii][gq];
+              bir[ii][gq] = f32x4{Half2<XGEN_DTYPE_F16>::lo(w2.x), Half2<XGEN_DTYPE_F16>::hi(w2.x),
+                                  Half2<XGEN_DTYPE_F16>::lo(w2.y), Half2<XGEN_DTYPE_F16>::hi(w2.y)};
+            }
+        } else {
+#pragma unroll
+          for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq) {
+              const u32x2 w2 = raw[ii][gq];
+              bir[ii][gq] = f32x4{Half2<XGEN_DTYPE_BF16>::lo(w2.x), Half2<XGEN_DTYPE_BF16>::hi(w2.x),
+                                  Half2<XGEN_DTYPE_BF16>::lo(w2.y), Half2<XGEN_DTYPE_BF16>::hi(w2.y)};
+            }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < FM; ++j) {
+        const int ml = wm * kWaveRows + j * 32 + wrow;
+        const float sam = p.sa_stride ? psa[ml] : sa0;
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq) {
+            const int i = 2 * h + ii;
+            float y[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float a = T::to_f32(acc[i][j][gq * 4 + e]);
+              y[e] = __builtin_fmaf(a, sam * swr[ii][gq][e], bir[ii][gq][e]);
+              if constexpr (ACT == XGEN_ACT_GELU_TANH) y[e] = gelu_tanh(round_out<OUT_DT>(y[e]));
+            }
+            // row wrow, 8-byte chunk c8 of its 128 bytes at c8 ^ ((wrow >> 1) & 15):
+            // each half-wave writes 32 distinct bank pairs
+            const int c8 = ii * 8 + gq * 2 + half;
+            *reinterpret_cast<u32x2 *>(xb + wrow * 128 + ((c8 ^ ((wrow >> 1) & 15)) << 3)) =
+                u32x2{pack_out<OUT_DT>(y[0], y[1]), pack_out<OUT_DT>(y[2], y[3])};
+            if constexpr (ACC_OUT) {
+              const int m = m0 + ml, n = n0 + wn * kWaveRows + i * 32 + gq * 8 + half * 4;
+              if (m < p.M && n < p.N) {
+                if constexpr (KIND != kInt8) {
+                  const f32x4 v = {acc[i][j][gq * 4 + 0], acc[i][j][gq * 4 + 1], acc[i][j][gq * 4 + 2],
+                                   acc[i][j][gq * 4 + 3]};
+                  *reinterpret_cast<f32x4 *>(static_cast<float *>(p.acc_out) + (int64_t)m * p.N + n) = v;
+                } else {
+                  const i32x4 v = {acc[i][j][gq * 4 + 0], acc[i][j][gq * 4 + 1], acc[i][j][gq * 4 + 2],
+                                   acc[i][j][gq * 4 + 3]};
+                  *reinterpret_cast<i32x4 *>(static_cast<int32_t *>(p.acc_out) + (int64_t)m * p.N + n) = v;
+                }
               }
             }
           }
-        }
-      // read back 4 whole rows per instruction (16 lanes x 16 bytes per row)
-      // and store them as 256-byte row segments; a wave's LDS operations
-      // complete in order, so the reads see its writes above
+        // read back 8 whole rows per instruction (8 lanes x 16 bytes per row) and
+        // store them as 128-byte row segments; a wave's LDS operations complete
+        // in order, so the reads see the writes above and the next writes follow
+        // these reads
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int row = q * 4 + (el >> 4), c16 = el & 15;
-        u32x4 v = *reinterpret_cast<const u32x4 *>(xb + row * 256 + (((2 * c16) ^ (row & ~1)) << 3));
-        if (row & 1) v = u32x4{v.z, v.w, v.x, v.y};
-        const int m = m0 + wm * kWaveRows + j * 32 + row;
-        const int n = n0 + wn * kWaveRows + c16 * 8;
-        if (m < p.M && n < p.N) {
+        for (int q = 0; q < 4; ++q) {
+          const int row = q * 8 + (el >> 3), c16 = el & 7;
+          const int sw4 = (row >> 1) & 15;
+          u32x4 v = *reinterpret_cast<const u32x4 *>(xb + row * 128 + ((c16 ^ (sw4 >> 1)) << 4));
+          if (sw4 & 1) v = u32x4{v.z, v.w, v.x, v.y};
+          const int m = m0 + wm * kWaveRows + j * 32 + row;
+          const int n = n0 + wn * kWaveRows + h * 64 + c16 * 8;
+          const bool in = m < p.M && n < p.N;
           if constexpr (GATED) {
-            const int64_t gi = p.indices[(uint32_t)m % p.seq];
-            if (gi >= 0 && gi < p.gate_rows) {
-              const u32x4 r = *reinterpret_cast<const u32x4 *>(p.residual + ((int64_t)m * p.ld_residual + n) * 2);
-              const u32x4 t = *reinterpret_cast<const u32x4 *>(p.gate + (gi * p.gate_stride + n) * 2);
-              v = gate_residual8(r, v, t);
-            } else {
-              v = u32x4{0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};  // index outside the table: NaN
+            if (in) {
+              const int64_t gi = p.indices[(uint32_t)m % p.seq];
+              if (gi >= 0 && gi < p.gate_rows) {
+                const u32x4 r = *reinterpret_cast<const u32x4 *>(p.residual + ((int64_t)m * p.ld_residual + n) * 2);
+                const u32x4 t = *reinterpret_cast<const u32x4 *>(p.gate + (gi * p.gate_stride + n) * 2);
+                v = gate_residual8(r, v, t);
+              } else {
+                v = u32x4{0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};  // index outside the table: NaN
+              }
             }
           }
-          *reinterpret_cast<u32x4 *>(static_cast<uint16_t *>(p.out) + (int64_t)m * p.ldo + n) = v;
+          __builtin_amdgcn_raw_buffer_store_b128(v, ro, in ? ((uint32_t)m * (uint32_t)p.ldo + (uint32_t)n) * 2 : kOutOfRange,
+                                                 0, 0);
         }
       }
     }
@@ -929,9 +980,10 @@ void gemm_w4_kernel(GemmArgs p) {
   // During the stage: the MFMAs of stage g (register buffer U & 1), the reads
   // of stage g+1 (slot U+1, buffer (U+1) & 1) and the DMA of stage g+4 (slot U),
   // interleaved.
-  auto stage = [&](auto U, auto FRESH) {
+  auto stage = [&](auto U, auto FRESH, auto READ) {
     constexpr int u = decltype(U)::value;
     constexpr bool fresh = decltype(FRESH)::value;  // the tile's first stage
+    constexpr bool read = decltype(READ)::value;    // not the tile's last stage
     constexpr int cb = u & 1, nb = cb ^ 1, ns = (u + 1) & 3;
     wait_vmcnt<2 * kLoadsPerStage>();
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
@@ -945,11 +997,13 @@ void gemm_w4_kernel(GemmArgs p) {
       const int ks = s / (FM * FN), j = (s / FN) % FM, i = s % FN;
       if (fresh && ks == 0) MfmaA<KIND>::mma0(acc[i][j], wf[cb][ks][i], xf[cb][ks][j]);
       else MfmaA<KIND>::mma(acc[i][j], wf[cb][ks][i], xf[cb][ks][j]);
+      if constexpr (read) {
 #pragma unroll
-      for (int r = spread_first(s, kReads / T::kReads, kMfmas); r < spread_first(s + 1, kReads / T::kReads, kMfmas); ++r) {
-        const int rks = r / (FM + FN), f = r % (FM + FN);
-        if (f < FN) read_w(nb, ns, rks, f);
-        else read_x(nb, ns, rks, f - FN);
+        for (int r = spread_first(s, kReads / T::kReads, kMfmas); r < spread_first(s + 1, kReads / T::kReads, kMfmas); ++r) {
+          const int rks = r / (FM + FN), f = r % (FM + FN);
+          if (f < FN) read_w(nb, ns, rks, f);
+          else read_x(nb, ns, rks, f - FN);
+        }
       }
 #pragma unroll
       for (int q = spread_first(s, kLoadsPerStage, kMfmas); q < spread_first(s + 1, kLoadsPerStage, kMfmas); ++q)
@@ -957,12 +1011,24 @@ void gemm_w4_kernel(GemmArgs p) {
     }
     issue_end();
   };
+  // stage 0's fragments (slot 0, register buffer 0)
+  auto read_first = [&]() {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+      for (int i = 0; i < FN; ++i) read_w(0, 0, ks, i);
+#pragma unroll
+      for (int j = 0; j < FM; ++j) read_x(0, 0, ks, j);
+    }
+  };
   typedef std::integral_constant<int, 0> S0;
   typedef std::integral_constant<int, 1> S1;
   typedef std::integral_constant<int, 2> S2;
   typedef std::integral_constant<int, 3> S3;
   typedef std::integral_constant<bool, true> Fresh;
   typedef std::integral_constant<bool, false> Acc;
+  typedef std::integral_constant<bool, true> Rd;
+  typedef std::integral_constant<bool, false> NoRd;
 
   // --- prologue: stages 0..3 in flight, stage 0's fragments in registers -------
   set_dma_tile(0);
@@ -985,34 +1051,32 @@ void gemm_w4_kernel(GemmArgs p) {
 #pragma unroll
     for (int q = 0; q < kLoadsPerStage; ++q) issue_load(is, 3, q);
     issue_end();
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-#pragma unroll
-      for (int i = 0; i < FN; ++i) read_w(0, 0, ks, i);
-#pragma unroll
-      for (int j = 0; j < FM; ++j) read_x(0, 0, ks, j);
-    }
+    read_first();
   }
   // --- main loop: per tile, its stages four at a time (static slots and
-  // register buffers), then its epilogue ------------------------------------
+  // register buffers), then its epilogue.  The tile's last stage does not read
+  // the next tile's first fragments: its epilogue does, after the transposes,
+  // so no fragment registers are held through it. -----------------------------
   for (int t = 0; t < n_my; ++t) {
-    stage(S0(), Fresh());
-    stage(S1(), Acc());
-    stage(S2(), Acc());
-    stage(S3(), Acc());
-    for (int c = 4; c < KT; c += 4) {
-      stage(S0(), Acc());
-      stage(S1(), Acc());
-      stage(S2(), Acc());
-      stage(S3(), Acc());
+    stage(S0(), Fresh(), Rd());
+    if (KT > 4) {
+      stage(S1(), Acc(), Rd());
+      stage(S2(), Acc(), Rd());
+      stage(S3(), Acc(), Rd());
+      for (int c = 8; c < KT; c += 4) {
+        stage(S0(), Acc(), Rd());
+        stage(S1(), Acc(), Rd());
+        stage(S2(), Acc(), Rd());
+        stage(S3(), Acc(), Rd());
+      }
+      stage(S0(), Acc(), Rd());
     }
-    // every wave's reads of slot 0 (the next tile's first stage) are done
-    // before it becomes the transpose area; its next DMA is issued after the
-    // barrier at the top of the next stage
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    lds_barrier();
+    stage(S1(), Acc(), Rd());
+    stage(S2(), Acc(), Rd());
+    stage(S3(), Acc(), NoRd());
     mfma_drain(acc);
     epilogue();
+    if (t + 1 < n_my) read_first();
   }
   // the loads of the stages past my last may still be writing LDS
   wait_vmcnt<0>();
@@ -1122,6 +1186,10 @@ int gemm_entry(const char *fn, const void *a, int64_t lda, const void *w, int64_
   g.indices = gp.indices;
   g.seq = (uint32_t)gp.seq;
   g.kt4 = (int)(((K + BK - 1) / BK + 3) / 4 * 4);
+  const int64_t out_bytes = ((M - 1) * ldo + N) * 2;
+  if (out_bytes >= (int64_t)kOutOfRange)
+    return fail(XGEN_ERR_UNSUPPORTED, "%s: output above 2 GiB", fn);
+  g.out_bytes = (uint32_t)out_bytes;
   const bool with_acc = acc_out != nullptr;
   if constexpr (KIND != kFp8Exact) {
     // FP8 and INT8: the one-wave-per-SIMD kernel
