@@ -237,11 +237,10 @@ __device__ __forceinline__ void wait_vmcnt() {
 // GELU with the tanh approximation, via tanh(z) = 2*sigmoid(2z) - 1:
 // 0.5*x*(1 + tanh(z)) = x / (1 + exp(-2z)),  z = sqrt(2/pi) * (x + 0.044715 x^3).
 __device__ __forceinline__ float gelu_tanh(float x) {
-  constexpr float kBeta = 0.7978845608028654f;  // sqrt(2/pi)
-  constexpr float kKappa = 0.044715f;
-  constexpr float kNeg2Log2e = -2.0f * 1.4426950408889634f;
-  const float z = x * __builtin_fmaf(kBeta * kKappa, x * x, kBeta);
-  const float t = __builtin_amdgcn_exp2f(z * kNeg2Log2e);
+  // -2 z log2(e) = x (c0 + c1 x^2): the exponent of exp(-2z) in base 2
+  constexpr float kC0 = (float)(-2.0 * 1.4426950408889634 * 0.7978845608028654);
+  constexpr float kC1 = (float)(-2.0 * 1.4426950408889634 * 0.7978845608028654 * 0.044715);
+  const float t = __builtin_amdgcn_exp2f(x * __builtin_fmaf(kC1, x * x, kC0));
   return x * __builtin_amdgcn_rcpf(1.0f + t);
 }
 
@@ -679,8 +678,11 @@ constexpr int kParamBytes = 3 * 1024;
 constexpr int kParamSets = 2;
 constexpr int kWaveRows = 128;                 // rows of a wave's block, both dimensions
 // A wave's epilogue transpose area, its own (no barrier): 32 rows of 128
-// bytes, half of its block's 128 features at a time.
-constexpr int kXpose = 32 * 128;
+// bytes (half of its block's 128 features at a time), rows 136 bytes apart:
+// row r starts at bank 34 r mod 64, so the 32 rows' 8-byte writes of one
+// chunk cover all 64 banks once.
+constexpr int kXposeRow = 136;
+constexpr int kXpose = 32 * kXposeRow;
 constexpr int kXposeBase = kSlots * kSlotBytes + kParamSets * kParamBytes;
 constexpr int kLdsBytes = kXposeBase + kWaves * kXpose;  // 150 KB
 }  // namespace w4
@@ -851,6 +853,14 @@ void gemm_w4_kernel(GemmArgs p) {
     asm volatile("" : "+v"(el));
     const int wrow = el & 31, half = el >> 5;
     uint8_t *xb = smem + kXposeBase + wave * kXpose;
+    // this lane's write position (row wrow, 8-byte chunk half + constant), and
+    // read position (16 bytes: row (el >> 3) + 8 q, chunk el & 7)
+    uint8_t *xw = xb + wrow * kXposeRow + half * 8;
+    const uint8_t *xr = xb + (el >> 3) * kXposeRow + (el & 7) * 16;
+    // rows of the tile are in range everywhere but in the last tile-row;
+    // columns everywhere unless N is not a multiple of 256
+    const bool full = m0 + 256 <= p.M && n0 + 256 <= p.N;
+    const int rr = el >> 3;  // this lane's read row (+ 8 q)
 #pragma unroll
     for (int h = 0; h < 2; ++h) {  // features [64 h, 64 h + 64) of the wave's block
       // this lane's 32 features' scales and bias of this half, as f32:
@@ -919,10 +929,8 @@ void gemm_w4_kernel(GemmArgs p) {
               y[e] = __builtin_fmaf(a, sam * swr[ii][gq][e], bir[ii][gq][e]);
               if constexpr (ACT == XGEN_ACT_GELU_TANH) y[e] = gelu_tanh(round_out<OUT_DT>(y[e]));
             }
-            // row wrow, 8-byte chunk c8 of its 128 bytes at c8 ^ ((wrow >> 1) & 15):
-            // each half-wave writes 32 distinct bank pairs
-            const int c8 = ii * 8 + gq * 2 + half;
-            *reinterpret_cast<u32x2 *>(xb + wrow * 128 + ((c8 ^ ((wrow >> 1) & 15)) << 3)) =
+            // row wrow, 8-byte chunk ii*8 + gq*2 + half
+            *reinterpret_cast<u32x2 *>(xw + (ii * 8 + gq * 2) * 8) =
                 u32x2{pack_out<OUT_DT>(y[0], y[1]), pack_out<OUT_DT>(y[2], y[3])};
             if constexpr (ACC_OUT) {
               const int m = m0 + ml, n = n0 + wn * kWaveRows + i * 32 + gq * 8 + half * 4;
@@ -939,19 +947,26 @@ void gemm_w4_kernel(GemmArgs p) {
               }
             }
           }
-        // read back 8 whole rows per instruction (8 lanes x 16 bytes per row) and
-        // store them as 128-byte row segments; a wave's LDS operations complete
-        // in order, so the reads see the writes above and the next writes follow
-        // these reads
+        // read back 8 whole rows per instruction (8 lanes x 16 bytes per row, as
+        // two 8-byte reads: rows are 8-byte aligned) and store them as 128-byte
+        // row segments; a wave's LDS operations complete in order, so the reads
+        // see the writes above and the next writes follow these reads
+        const int mrow = m0 + wm * kWaveRows + j * 32 + rr;               // + 8 q
+        const int ncol = n0 + wn * kWaveRows + h * 64 + (el & 7) * 8;
+        const uint32_t obase = ((uint32_t)mrow * (uint32_t)p.ldo + (uint32_t)ncol) * 2;
+        // all reads first, so they are waited for once
+        u32x4 rows[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const int row = q * 8 + (el >> 3), c16 = el & 7;
-          const int sw4 = (row >> 1) & 15;
-          u32x4 v = *reinterpret_cast<const u32x4 *>(xb + row * 128 + ((c16 ^ (sw4 >> 1)) << 4));
-          if (sw4 & 1) v = u32x4{v.z, v.w, v.x, v.y};
-          const int m = m0 + wm * kWaveRows + j * 32 + row;
-          const int n = n0 + wn * kWaveRows + h * 64 + c16 * 8;
-          const bool in = m < p.M && n < p.N;
+          const u32x2 lo = *reinterpret_cast<const u32x2 *>(xr + q * 8 * kXposeRow);
+          const u32x2 hi = *reinterpret_cast<const u32x2 *>(xr + q * 8 * kXposeRow + 8);
+          rows[q] = u32x4{lo.x, lo.y, hi.x, hi.y};
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          u32x4 v = rows[q];
+          const int m = mrow + q * 8, n = ncol;
+          const bool in = full || (m < p.M && n < p.N);
           if constexpr (GATED) {
             if (in) {
               const int64_t gi = p.indices[(uint32_t)m % p.seq];
@@ -964,8 +979,7 @@ void gemm_w4_kernel(GemmArgs p) {
               }
             }
           }
-          __builtin_amdgcn_raw_buffer_store_b128(v, ro, in ? ((uint32_t)m * (uint32_t)p.ldo + (uint32_t)n) * 2 : kOutOfRange,
-                                                 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b128(v, ro, in ? obase + (uint32_t)(q * 8 * p.ldo * 2) : kOutOfRange, 0, 0);
         }
       }
     }
