@@ -672,10 +672,10 @@ constexpr int kLoadsPerStage = 2 * kLoads;     // per thread
 // A full 1 KB DMA load per row, so a 2-byte bias row's second half takes the
 // next bytes (or zeros) without leaving its row.
 constexpr int kParamBytes = 3 * 1024;
-// Tiles have a multiple of 4 stages, so the next tile's parameters (issued 4
-// stages ahead of its first stage) are never issued before this tile's
-// epilogue has read its set: two sets alternate.
-constexpr int kParamSets = 2;
+// A tile's epilogue runs during the next tile's first stage, and tile t+3's
+// parameters are issued 4 stages before its first stage, i.e. at the earliest
+// (4-stage tiles) during tile t+2's first stage: three sets rotate.
+constexpr int kParamSets = 3;
 constexpr int kWaveRows = 128;                 // rows of a wave's block, both dimensions
 // A wave's epilogue transpose area, its own (no barrier): 32 rows of 128
 // bytes (half of its block's 128 features at a time), rows 136 bytes apart:
@@ -684,7 +684,7 @@ constexpr int kWaveRows = 128;                 // rows of a wave's block, both d
 constexpr int kXposeRow = 136;
 constexpr int kXpose = 32 * kXposeRow;
 constexpr int kXposeBase = kSlots * kSlotBytes + kParamSets * kParamBytes;
-constexpr int kLdsBytes = kXposeBase + kWaves * kXpose;  // 150 KB
+constexpr int kLdsBytes = kXposeBase + kWaves * kXpose;  // 154 KB
 }  // namespace w4
 
 // Loads [first(s), first(s + 1)) of n loads spread over `slots` MFMA slots.
@@ -792,7 +792,7 @@ void gemm_w4_kernel(GemmArgs p) {
   };
   auto issue_begin = [&](int slot) {
     if (dma_k == 0 && dma_h < G) {  // the tile's epilogue parameters ride with its first stage
-      uint8_t *prm = smem + kSlots * kSlotBytes + (dma_i & 1) * kParamBytes;
+      uint8_t *prm = smem + kSlots * kSlotBytes + (dma_i % kParamSets) * kParamBytes;
       if (wave == 0 && p.sa_stride) dma_load16(rsa, prm, (uint32_t)dma_m0 * 4 + lane * 16);
       if (wave == 1 && p.sw_stride) dma_load16(rsw, prm + 1024, (uint32_t)dma_n0 * 4 + lane * 16);
       // (without a bias the resource is empty: the row reads as zeros)
@@ -839,11 +839,13 @@ void gemm_w4_kernel(GemmArgs p) {
   // --- epilogue: dequant + bias (+ GELU), transpose, row stores ---------------
   // acc[i][j] element e: feature n = n0 + wn*128 + i*32 + (e/4)*8 + (lane/32)*4 + e%4,
   //                      token   m = m0 + wm*128 + j*32 + lane%32.
+  // on_block(i, j, b) runs once block (i, j)'s accumulators have been read
+  // (b = its position 0..15 in the epilogue's order)
   int tile_i = 0;
-  auto epilogue = [&]() {
+  auto epilogue = [&](auto on_block) {
     int m0, n0;
     tile_origin<256, 256>(t_first + tile_i * wgs_per_xcd, p.tiles_m, p.tiles_n, p.group_m, m0, n0);
-    const uint8_t *prm = smem + kSlots * kSlotBytes + (tile_i & 1) * kParamBytes;
+    const uint8_t *prm = smem + kSlots * kSlotBytes + (tile_i % kParamSets) * kParamBytes;
     const float *psa = reinterpret_cast<const float *>(prm);
     const float *psw = reinterpret_cast<const float *>(prm + 1024);
     const uint8_t *pb = prm + 2048;
@@ -922,6 +924,9 @@ void gemm_w4_kernel(GemmArgs p) {
 #pragma unroll
           for (int gq = 0; gq < 4; ++gq) {
             const int i = 2 * h + ii;
+            // pin block (i, j)'s accumulator reads here (not hoisted, which
+            // would hold them all in VGPRs at once)
+            if (gq == 0) asm volatile("" : "+a"(acc[i][j]));
             float y[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
@@ -946,6 +951,7 @@ void gemm_w4_kernel(GemmArgs p) {
                 }
               }
             }
+            if (gq == 3) on_block(2 * h + ii, j, h * 8 + j * 2 + ii);
           }
         // read back 8 whole rows per instruction (8 lanes x 16 bytes per row, as
         // two 8-byte reads: rows are 8-byte aligned) and store them as 128-byte
@@ -1035,6 +1041,36 @@ void gemm_w4_kernel(GemmArgs p) {
       for (int j = 0; j < FM; ++j) read_x(0, 0, ks, j);
     }
   };
+  // The next tile's first stage (slot 0, register buffer 0; DMA of stage 4;
+  // reads stage 1 into buffer 1) with this tile's epilogue: each block's first
+  // MFMA(s) of the next tile are issued as soon as the epilogue has read that
+  // block's accumulators, so the matrix core works through the epilogue.
+  // Stage 1's fragments are read at the end, keeping their registers free
+  // through the epilogue.
+  auto stage0_with_epilogue = [&]() {
+    wait_vmcnt<2 * kLoadsPerStage>();
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    lds_barrier();
+    const Issue is = issue_begin(0);
+    epilogue([&](int i, int j, int b) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        if (ks == 0) MfmaA<KIND>::mma0(acc[i][j], wf[0][ks][i], xf[0][ks][j]);
+        else MfmaA<KIND>::mma(acc[i][j], wf[0][ks][i], xf[0][ks][j]);
+      }
+#pragma unroll
+      for (int q = spread_first(b, kLoadsPerStage, 16); q < spread_first(b + 1, kLoadsPerStage, 16); ++q)
+        issue_load(is, 0, q);
+    });
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+      for (int i = 0; i < FN; ++i) read_w(1, 1, ks, i);
+#pragma unroll
+      for (int j = 0; j < FM; ++j) read_x(1, 1, ks, j);
+    }
+    issue_end();
+  };
   typedef std::integral_constant<int, 0> S0;
   typedef std::integral_constant<int, 1> S1;
   typedef std::integral_constant<int, 2> S2;
@@ -1071,8 +1107,8 @@ void gemm_w4_kernel(GemmArgs p) {
   // register buffers), then its epilogue.  The tile's last stage does not read
   // the next tile's first fragments: its epilogue does, after the transposes,
   // so no fragment registers are held through it. -----------------------------
+  stage(S0(), Fresh(), Rd());  // the first tile's first stage; the others' run with the epilogues
   for (int t = 0; t < n_my; ++t) {
-    stage(S0(), Fresh(), Rd());
     if (KT > 4) {
       stage(S1(), Acc(), Rd());
       stage(S2(), Acc(), Rd());
@@ -1089,8 +1125,11 @@ void gemm_w4_kernel(GemmArgs p) {
     stage(S2(), Acc(), Rd());
     stage(S3(), Acc(), NoRd());
     mfma_drain(acc);
-    epilogue();
-    if (t + 1 < n_my) read_first();
+    // after the last tile too (one epilogue instance: a second one costs the
+    // register allocator its fit): the "next tile" is then stages past the
+    // stream's end, whose loads read zeros, and its MFMAs' results are unused
+    read_first();
+    stage0_with_epilogue();
   }
   // the loads of the stages past my last may still be writing LDS
   wait_vmcnt<0>();
