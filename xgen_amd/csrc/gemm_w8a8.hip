@@ -985,7 +985,10 @@ void gemm_w4_kernel(GemmArgs p) {
               }
             }
           }
-          __builtin_amdgcn_raw_buffer_store_b128(v, ro, in ? obase + (uint32_t)(q * 8 * p.ldo * 2) : kOutOfRange, 0, 0);
+          // non-temporal: the output streams past the caches the operands are re-read from
+          // (measured: FFN down 4.7%, FFN up 2% faster; QKV unchanged)
+          __builtin_amdgcn_raw_buffer_store_b128(v, ro, in ? obase + (uint32_t)(q * 8 * p.ldo * 2) : kOutOfRange, 0,
+                                                 kCachePolicyNT);
         }
       }
     }
