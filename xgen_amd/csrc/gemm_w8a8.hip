@@ -19,14 +19,13 @@
 //
 // out[m, n] = act(cvt(acc[m, n] * (sa[m] * sw[n]) + bias[n])),  acc = sum_k a[m,k] w[n,k]
 //
-// Tiling: a 256x256 output tile per workgroup of WM x WN waves; each wave owns
-// a (256/WM) x (256/WN) block of 32x32 MFMA tiles with accumulators in AGPRs.
-// With 8 waves (2 per SIMD) one wave issues MFMAs while the other waits on
-// LDS or the barrier.  K advances in stages of 64 bytes through a ring of 4
-// LDS slots (4 x (16 KB activations + 16 KB weights)); operands go global ->
-// LDS by bounds-checked buffer loads on the LDS-DMA path (no VGPR staging;
-// rows past M/N and the K tail read as zero), issued 3 stages ahead of the
-// MFMAs that consume them, one barrier per stage.
+// Tiling (FP8 and INT8): a 256x256 output tile per workgroup of 4 waves, one
+// per SIMD, each owning a 128x128 block (4x4 MFMA fragments, accumulators in
+// AGPRs).  K advances in pairs of 64-byte sub-stages: bounds-checked buffer
+// loads on the LDS-DMA path (no VGPR staging; rows past M/N and the K tail
+// read as zero) move 128 bytes of K per row into a ring of two 64 KB pair
+// slots, one pair ahead, one barrier per pair.  The FP8-exact kind runs on an
+// 8-wave kernel (2 per SIMD, 128x64 each, 64-byte stages in a 4-slot ring).
 //
 // The MFMA's A operand is the weight tile and its B operand the activation
 // tile, so each lane's accumulator column is one token and its 4 consecutive
@@ -35,7 +34,7 @@
 //
 // Workgroup -> tile mapping: the dispatcher places consecutive workgroup ids
 // on the 8 XCDs round-robin; ids are remapped so each XCD owns a contiguous
-// range of tiles, walked in groups of 8 tile-rows, so concurrently running
+// range of tiles, walked in groups of 4 or 8 tile-rows, so concurrently running
 // tiles on one XCD share activation rows and weight columns in its L2.
 #include "xgen_common.h"
 
@@ -662,19 +661,23 @@ void launch_gemm_gated(const GemmArgs &a, hipStream_t stream) {
 // ---------------------------------------------------------------------------
 namespace w4 {
 constexpr int kWaves = 4, kThreads = 256;
-constexpr int kSlots = 4;                      // LDS ring depth, 64-byte K stages
-constexpr int kTileBytes = 256 * BK;           // one operand tile of one stage: 16 KB
-constexpr int kSlotBytes = 2 * kTileBytes;     // activations + weights: 32 KB
 constexpr int kRowsPerWave = 256 / kWaves;     // DMA rows per operand per wave
-constexpr int kLoads = kRowsPerWave / 16;      // 1 KB DMA loads per operand per wave per stage
-constexpr int kLoadsPerStage = 2 * kLoads;     // per thread
+// K pairs: the DMA moves 128 bytes of K per row (a whole cache line: half the
+// L2 requests of 64-byte rows) into a ring of two pair slots; each pair is two
+// 64-byte sub-stages of MFMAs, and one barrier per pair publishes the next.
+constexpr int kPairTile = 256 * 128;            // one operand of one pair: 32 KB
+constexpr int kPairSlotBytes = 2 * kPairTile;   // activations + weights: 64 KB
+constexpr int kPairSlots = 2;
+constexpr int kPairLoads = kRowsPerWave / 8;    // 1 KB loads (8 rows) per operand per wave per pair
+constexpr int kLoadsPerPair = 2 * kPairLoads;   // 16 per thread
 // One parameter set: [sa f32 x 256][sw f32 x 256][bias as stored: <= 1 KB].
 // A full 1 KB DMA load per row, so a 2-byte bias row's second half takes the
 // next bytes (or zeros) without leaving its row.
 constexpr int kParamBytes = 3 * 1024;
-// A tile's epilogue runs during the next tile's first stage, and tile t+3's
-// parameters are issued 4 stages before its first stage, i.e. at the earliest
-// (4-stage tiles) during tile t+2's first stage: three sets rotate.
+constexpr int kParamBase = kPairSlots * kPairSlotBytes;
+// A tile's epilogue runs during the next tile's first sub-stage, and tile
+// t+3's parameters are issued with its first pair, at the earliest (2-pair
+// tiles) during tile t+2's first pair: three sets rotate.
 constexpr int kParamSets = 3;
 constexpr int kWaveRows = 128;                 // rows of a wave's block, both dimensions
 // A wave's epilogue transpose area, its own (no barrier): 32 rows of 128
@@ -683,7 +686,7 @@ constexpr int kWaveRows = 128;                 // rows of a wave's block, both d
 // chunk cover all 64 banks once.
 constexpr int kXposeRow = 136;
 constexpr int kXpose = 32 * kXposeRow;
-constexpr int kXposeBase = kSlots * kSlotBytes + kParamSets * kParamBytes;
+constexpr int kXposeBase = kParamBase + kParamSets * kParamBytes;
 constexpr int kLdsBytes = kXposeBase + kWaves * kXpose;  // 154 KB
 }  // namespace w4
 
@@ -733,6 +736,23 @@ __device__ __forceinline__ void mfma_drain(A (&acc)[4][4]) {
                     "+a"(acc[1][3]), "+a"(acc[2][3]), "+a"(acc[3][3]));
 }
 
+// 128-byte rows: 16-byte chunk c of row r at c ^ ((r >> 1) & 7); the 16 lanes of
+// one 128-bit access (rows r..r+15, one chunk) hit 16 distinct bank groups.
+__device__ __forceinline__ int swz128(int row, int chunk) { return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4); }
+template <int KIND>
+__device__ __forceinline__ typename Mfma<KIND>::frag_t load_pair(const uint8_t *tile, int row, int half, int ks, int lane) {
+  if constexpr (KIND == kInt8) {
+    const u32x4 v = *reinterpret_cast<const u32x4 *>(tile + swz128(row, half * 4 + ks * 2 + (lane >> 5)));
+    return typename Mfma<KIND>::frag_t{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+  } else {
+    const int c0 = half * 4 + (lane >> 5) * 2;
+    const u32x4 lo = *reinterpret_cast<const u32x4 *>(tile + swz128(row, c0));
+    const u32x4 hi = *reinterpret_cast<const u32x4 *>(tile + swz128(row, c0 + 1));
+    return typename Mfma<KIND>::frag_t{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
+                                       (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+  }
+}
+
 template <int KIND, int ACT, int OUT_DT, bool ACC_OUT, bool GATED>
 __global__ __attribute__((amdgpu_flat_work_group_size(w4::kThreads, w4::kThreads), amdgpu_waves_per_eu(1, 1)))
 void gemm_w4_kernel(GemmArgs p) {
@@ -751,8 +771,7 @@ void gemm_w4_kernel(GemmArgs p) {
   const int t_end = min((xcd + 1) * p.per_xcd, ntiles);
   const int n_my = t_first < t_end ? (t_end - t_first + wgs_per_xcd - 1) / wgs_per_xcd : 0;
   if (n_my == 0) return;
-  const int KT = p.kt4;  // stages per tile: a multiple of 4; stages past K read zeros
-  const int G = n_my * KT;
+  const int KT = p.kt4;  // 64-byte sub-stages per tile: a multiple of 4; those past K read zeros
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -776,47 +795,53 @@ void gemm_w4_kernel(GemmArgs p) {
 
   // --- global -> LDS DMA (layout as gemm_w8a8_kernel: chunk c of row r at
   // c ^ ((r >> 2) & 3); wave w fills rows [64 w, 64 w + 64) of both tiles) ---
-  const int dma_chunk = (lane & 3) ^ ((lane >> 4) & 3);
-  uint32_t offa = 0, offw = 0;  // byte offsets of this lane's first rows in the DMA's tile
+  // lane l fills row (l >> 3) of an 8-row load, physical chunk l & 7: logical
+  // chunk (l & 7) ^ ((row >> 1) & 7), i.e. ^ (l >> 4) in even loads, ^ (4 | l >> 4) in odd
+  const int ch_e = (lane & 7) ^ (lane >> 4), ch_o = (lane & 7) ^ (4 | (lane >> 4));
+  uint32_t offa = 0, offw = 0;  // byte offsets of this lane's first row in the DMA's tile
   int dma_m0 = 0, dma_n0 = 0;
   auto set_dma_tile = [&](int i) {
     tile_origin<256, 256>(t_first + i * wgs_per_xcd, p.tiles_m, p.tiles_n, p.group_m, dma_m0, dma_n0);
-    offa = (uint32_t)(dma_m0 + wave * kRowsPerWave + (lane >> 2)) * (uint32_t)p.lda + dma_chunk * 16;
-    offw = (uint32_t)(dma_n0 + wave * kRowsPerWave + (lane >> 2)) * (uint32_t)p.ldw + dma_chunk * 16;
+    offa = (uint32_t)(dma_m0 + wave * kRowsPerWave + (lane >> 3)) * (uint32_t)p.lda;
+    offw = (uint32_t)(dma_n0 + wave * kRowsPerWave + (lane >> 3)) * (uint32_t)p.ldw;
   };
-  int dma_h = 0, dma_k = 0, dma_i = 0;  // next stage to load: stage dma_k of my tile dma_i
+  const int KP = KT / 2;  // pairs per tile
+  const int GP = n_my * KP;
+  int dma_h = 0, dma_k = 0, dma_i = 0;  // next pair to load: pair dma_k of my tile dma_i
   // this stage's load offsets (load 0 of each operand), or out of range
   struct Issue {
-    uint32_t oa, ow;
+    uint32_t oe, oo, we, wo;  // this pair's offsets for even / odd loads, or out of range
     uint32_t lds;  // offset of this wave's DMA area of slot 0 (the loads' LDS addresses are formed from it per stage)
   };
   auto issue_begin = [&](int slot) {
-    if (dma_k == 0 && dma_h < G) {  // the tile's epilogue parameters ride with its first stage
-      uint8_t *prm = smem + kSlots * kSlotBytes + (dma_i % kParamSets) * kParamBytes;
+    if (dma_k == 0 && dma_h < GP) {  // the tile's epilogue parameters ride with its first pair
+      uint8_t *prm = smem + kParamBase + (dma_i % kParamSets) * kParamBytes;
       if (wave == 0 && p.sa_stride) dma_load16(rsa, prm, (uint32_t)dma_m0 * 4 + lane * 16);
       if (wave == 1 && p.sw_stride) dma_load16(rsw, prm + 1024, (uint32_t)dma_n0 * 4 + lane * 16);
       // (without a bias the resource is empty: the row reads as zeros)
       if (wave == 2) dma_load16(rb, prm + 2048, (uint32_t)(dma_n0 * bias_elem) + lane * 16);
     }
-    const int k0 = dma_k * BK;
-    const bool kin = dma_h < G && k0 + dma_chunk * 16 < p.K;
-    uint32_t oa = kin ? offa + k0 : kOutOfRange, ow = kin ? offw + k0 : kOutOfRange;
-    uint32_t lds = (uint32_t)wave * kRowsPerWave * BK;
-    asm volatile("" : "+v"(oa), "+v"(ow), "+s"(lds));  // keep the per-load adds per stage (registers)
+    const int k0 = dma_k * 128;
+    const bool live = dma_h < GP;
+    const bool ke = live && k0 + ch_e * 16 < p.K, ko = live && k0 + ch_o * 16 < p.K;
+    uint32_t oe = ke ? offa + k0 + ch_e * 16 : kOutOfRange, oo = ko ? offa + k0 + ch_o * 16 : kOutOfRange;
+    uint32_t we = ke ? offw + k0 + ch_e * 16 : kOutOfRange, wo = ko ? offw + k0 + ch_o * 16 : kOutOfRange;
+    uint32_t lds = (uint32_t)wave * kRowsPerWave * 128;
+    asm volatile("" : "+v"(oe), "+v"(oo), "+v"(we), "+v"(wo), "+s"(lds));
     (void)slot;
-    return Issue{oa, ow, lds};
+    return Issue{oe, oo, we, wo, lds};
   };
-  // load q of the stage going to `slot`: A loads are even q, W loads odd q
+  // load q of the pair going to pair slot `slot`: A loads are even q, W loads odd q
   // (kOutOfRange + l * 16 * ld stays out of range: the host keeps (M + 512) * lda below 2^32)
   auto issue_load = [&](const Issue &is, int slot, int q) {
-    const int l = q >> 1;
-    uint8_t *dst = smem + is.lds + slot * kSlotBytes + l * 16 * BK;
-    if (q & 1) dma_load16(rw, dst + kTileBytes, is.ow + (uint32_t)(l * 16 * p.ldw));
-    else dma_load16(ra, dst, is.oa + (uint32_t)(l * 16 * p.lda));
+    const int l = q >> 1;  // load l of the operand: rows 8 l .. 8 l + 7 of the wave's 64
+    uint8_t *dst = smem + is.lds + slot * kPairSlotBytes + l * 8 * 128;
+    if (q & 1) dma_load16(rw, dst + kPairTile, ((l & 1) ? is.wo : is.we) + (uint32_t)(l * 8 * p.ldw));
+    else dma_load16(ra, dst, ((l & 1) ? is.oo : is.oe) + (uint32_t)(l * 8 * p.lda));
   };
   auto issue_end = [&]() {
     ++dma_h;
-    if (++dma_k == KT) {
+    if (++dma_k == KP) {
       dma_k = 0;
       if (++dma_i < n_my) set_dma_tile(dma_i);
     }
@@ -826,14 +851,15 @@ void gemm_w4_kernel(GemmArgs p) {
   const int row_x = wm * kWaveRows + (lane & 31);
   const int row_w = wn * kWaveRows + (lane & 31);
   frag_t xf[2][KS][FM], wf[2][KS][FN];  // [register buffer][k step][fragment]
-  auto read_x = [&](int b, int slot, int ks, int j) {
-    xf[b][ks][j] = T::load(smem + slot * kSlotBytes, row_x + j * 32, ks, lane);
+  // sub-stage slot s = 2 * pair slot + half
+  auto read_x = [&](int b, int s, int ks, int j) {
+    xf[b][ks][j] = load_pair<KIND>(smem + (s >> 1) * kPairSlotBytes, row_x + j * 32, s & 1, ks, lane);
   };
-  auto read_w = [&](int b, int slot, int ks, int i) {
-    wf[b][ks][i] = T::load(smem + slot * kSlotBytes + kTileBytes, row_w + i * 32, ks, lane);
+  auto read_w = [&](int b, int s, int ks, int i) {
+    wf[b][ks][i] = load_pair<KIND>(smem + (s >> 1) * kPairSlotBytes + kPairTile, row_w + i * 32, s & 1, ks, lane);
   };
 
-  // defined by each tile's first stage (mma0), read by its epilogue
+  // defined by each tile's first sub-stage (mma0), read by its epilogue
   typename T::acc_t acc[FN][FM];
 
   // --- epilogue: dequant + bias (+ GELU), transpose, row stores ---------------
@@ -845,7 +871,7 @@ void gemm_w4_kernel(GemmArgs p) {
   auto epilogue = [&](auto on_block) {
     int m0, n0;
     tile_origin<256, 256>(t_first + tile_i * wgs_per_xcd, p.tiles_m, p.tiles_n, p.group_m, m0, n0);
-    const uint8_t *prm = smem + kSlots * kSlotBytes + (tile_i % kParamSets) * kParamBytes;
+    const uint8_t *prm = smem + kParamBase + (tile_i % kParamSets) * kParamBytes;
     const float *psa = reinterpret_cast<const float *>(prm);
     const float *psw = reinterpret_cast<const float *>(prm + 1024);
     const uint8_t *pb = prm + 2048;
@@ -995,23 +1021,28 @@ void gemm_w4_kernel(GemmArgs p) {
     ++tile_i;
   };
 
-  // --- one stage, slot U = g % 4 ---------------------------------------------
-  // At the top: this thread's DMA of stage g+1 has landed (at most the loads of
-  // stages g+2 and g+3 outstanding) and its fragment reads of stage g are in
-  // registers; the barrier publishes every wave's DMA of stage g+1 and retires
-  // every wave's reads of slot U, which then takes the DMA of stage g+4.
-  // During the stage: the MFMAs of stage g (register buffer U & 1), the reads
-  // of stage g+1 (slot U+1, buffer (U+1) & 1) and the DMA of stage g+4 (slot U),
-  // interleaved.
+  // --- one 64-byte sub-stage g, U = g % 4: pair slot U >> 1, half U & 1 -------
+  // Its MFMAs use register buffer U & 1 (read during sub-stage g-1); during
+  // it the next sub-stage's fragments are read into the other buffer.  The
+  // second sub-stage of a pair (U odd) starts by waiting for this thread's
+  // DMA of the next pair (the only one outstanding), retiring its own reads;
+  // the barrier then publishes every wave's DMA of the next pair and retires
+  // every wave's reads of this pair's slot, which takes the DMA of the pair
+  // after next, spread over this sub-stage's MFMAs (all at once is measured
+  // slower: the loads queue in the address unit ahead of the MFMAs).
   auto stage = [&](auto U, auto FRESH, auto READ) {
     constexpr int u = decltype(U)::value;
-    constexpr bool fresh = decltype(FRESH)::value;  // the tile's first stage
+    constexpr bool fresh = decltype(FRESH)::value;  // the tile's first sub-stage
     constexpr bool read = decltype(READ)::value;    // not the tile's last stage
     constexpr int cb = u & 1, nb = cb ^ 1, ns = (u + 1) & 3;
-    wait_vmcnt<2 * kLoadsPerStage>();
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-    lds_barrier();
-    const Issue is = issue_begin(u);
+    constexpr bool odd = u & 1;  // the second sub-stage of a pair: barrier, and the DMA of pair + 2
+    Issue is{};
+    if constexpr (odd) {
+      wait_vmcnt<0>();
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      lds_barrier();
+      is = issue_begin(u >> 1);
+    }
     // The MFMAs are volatile asm statements, so the loads written between them
     // stay in this order: per MFMA, its share of the next stage's fragment
     // reads (weights first) and of the DMA loads.
@@ -1028,11 +1059,13 @@ void gemm_w4_kernel(GemmArgs p) {
           else read_x(nb, ns, rks, f - FN);
         }
       }
+      if constexpr (odd) {
 #pragma unroll
-      for (int q = spread_first(s, kLoadsPerStage, kMfmas); q < spread_first(s + 1, kLoadsPerStage, kMfmas); ++q)
-        issue_load(is, u, q);
+        for (int q = spread_first(s, kLoadsPerPair, kMfmas); q < spread_first(s + 1, kLoadsPerPair, kMfmas); ++q)
+          if (s < kMfmas) issue_load(is, u >> 1, q);
+      }
     }
-    issue_end();
+    if constexpr (odd) issue_end();
   };
   // stage 0's fragments (slot 0, register buffer 0)
   auto read_first = [&]() {
@@ -1044,26 +1077,19 @@ void gemm_w4_kernel(GemmArgs p) {
       for (int j = 0; j < FM; ++j) read_x(0, 0, ks, j);
     }
   };
-  // The next tile's first stage (slot 0, register buffer 0; DMA of stage 4;
-  // reads stage 1 into buffer 1) with this tile's epilogue: each block's first
-  // MFMA(s) of the next tile are issued as soon as the epilogue has read that
-  // block's accumulators, so the matrix core works through the epilogue.
-  // Stage 1's fragments are read at the end, keeping their registers free
-  // through the epilogue.
+  // The next tile's first sub-stage (pair slot 0 half 0, register buffer 0)
+  // with this tile's epilogue: each block's first MFMA(s) of the next tile are
+  // issued as soon as the epilogue has read that block's accumulators, so the
+  // matrix core works through the epilogue.  The second sub-stage's fragments
+  // are read at the end, keeping their registers free through the epilogue.
   auto stage0_with_epilogue = [&]() {
-    wait_vmcnt<2 * kLoadsPerStage>();
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-    lds_barrier();
-    const Issue is = issue_begin(0);
     epilogue([&](int i, int j, int b) {
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         if (ks == 0) MfmaA<KIND>::mma0(acc[i][j], wf[0][ks][i], xf[0][ks][j]);
         else MfmaA<KIND>::mma(acc[i][j], wf[0][ks][i], xf[0][ks][j]);
       }
-#pragma unroll
-      for (int q = spread_first(b, kLoadsPerStage, 16); q < spread_first(b + 1, kLoadsPerStage, 16); ++q)
-        issue_load(is, 0, q);
+      (void)b;
     });
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
@@ -1072,7 +1098,6 @@ void gemm_w4_kernel(GemmArgs p) {
 #pragma unroll
       for (int j = 0; j < FM; ++j) read_x(1, 1, ks, j);
     }
-    issue_end();
   };
   typedef std::integral_constant<int, 0> S0;
   typedef std::integral_constant<int, 1> S1;
@@ -1083,34 +1108,26 @@ void gemm_w4_kernel(GemmArgs p) {
   typedef std::integral_constant<bool, true> Rd;
   typedef std::integral_constant<bool, false> NoRd;
 
-  // --- prologue: stages 0..3 in flight, stage 0's fragments in registers -------
+  // --- prologue: pairs 0 and 1 in flight, sub-stage 0's fragments in registers -
   set_dma_tile(0);
   {
     Issue is = issue_begin(0);
 #pragma unroll
-    for (int q = 0; q < kLoadsPerStage; ++q) issue_load(is, 0, q);
+    for (int q = 0; q < kLoadsPerPair; ++q) issue_load(is, 0, q);
     issue_end();
     is = issue_begin(1);
 #pragma unroll
-    for (int q = 0; q < kLoadsPerStage; ++q) issue_load(is, 1, q);
+    for (int q = 0; q < kLoadsPerPair; ++q) issue_load(is, 1, q);
     issue_end();
-    is = issue_begin(2);
-#pragma unroll
-    for (int q = 0; q < kLoadsPerStage; ++q) issue_load(is, 2, q);
-    issue_end();
-    wait_vmcnt<2 * kLoadsPerStage>();
+    wait_vmcnt<kLoadsPerPair>();
     lds_barrier();
-    is = issue_begin(3);
-#pragma unroll
-    for (int q = 0; q < kLoadsPerStage; ++q) issue_load(is, 3, q);
-    issue_end();
     read_first();
   }
-  // --- main loop: per tile, its stages four at a time (static slots and
-  // register buffers), then its epilogue.  The tile's last stage does not read
-  // the next tile's first fragments: its epilogue does, after the transposes,
-  // so no fragment registers are held through it. -----------------------------
-  stage(S0(), Fresh(), Rd());  // the first tile's first stage; the others' run with the epilogues
+  // --- main loop: per tile, its sub-stages four at a time (static slots and
+  // register buffers), then its epilogue.  The tile's last sub-stage does not
+  // read the next tile's first fragments: they are read after it, so no
+  // fragment registers are held through the epilogue. ------------------------
+  stage(S0(), Fresh(), Rd());  // the first tile's first sub-stage; the others' run with the epilogues
   for (int t = 0; t < n_my; ++t) {
     if (KT > 4) {
       stage(S1(), Acc(), Rd());
