@@ -1243,12 +1243,12 @@ int gemm_entry(const char *fn, const void *a, int64_t lda, const void *w, int64_
   g.tiles_m = (int)((M + C::BM - 1) / C::BM);
   g.tiles_n = (int)((N + C::BN - 1) / C::BN);
   g.per_xcd = (g.tiles_m * g.tiles_n + 7) / 8;
-  // The 32 tiles one XCD runs at once span group_m tile-rows.  Measured at
-  // M=15,624: 4 rows beat 8 for outputs of 24-63 tile-columns (QKV N=9,216
-  // 0.9%, FFN up N=12,288 2.8% faster); 8 beat 4 for FFN down's 12 (1.7%), and
-  // for H3's FFN up (N=28,672: 112 tile-columns, 2.5%); 2, 3, 6, 12 and 16
-  // were no better.
-  g.group_m = g.tiles_n >= 24 && g.tiles_n < 64 ? 4 : 8;
+  // The 32 tiles one XCD runs at once span group_m tile-rows.  One wave per
+  // SIMD (FP8, INT8), measured at M=15,624: 8 rows beat 4 for QKV and FFN up by
+  // ~1% and tie for FFN down; 2 are 4-7% slower, 16 no better.  The 8-wave
+  // kernel (FP8-exact): 4 rows beat 8 for outputs of 24-63 tile-columns (QKV
+  // 0.9%, FFN up 2.8%), 8 beat 4 for FFN down's 12 (1.7%).
+  g.group_m = KIND != kFp8Exact || !(g.tiles_n >= 24 && g.tiles_n < 64) ? 8 : 4;
   g.a_bytes = (uint32_t)a_bytes;
   g.w_bytes = (uint32_t)w_bytes;
   g.residual = static_cast<const uint8_t *>(gp.residual);
