@@ -19,10 +19,9 @@
  *                            a subnormal amax) -> 0, as for a flushed zero row.
  *  oracle_check_fast_division   exhaustive check, for every (x, amax) pair of
  *                            16-bit inputs the row quantizers can see, that the
- *                            HIP kernels' division by the row scale
- *                            (a = |x|; q0 = a*r; e = fma(-q0, s, a);
- *                            q = fma(e, r, q0), r = 1/s, sign of x restored,
- *                            for amax >= 2^-100)
+ *                            HIP row quantizers' division by the row scale
+ *                            (r_hi = 1/s rounded toward zero, r_lo =
+ *                            RN((1 - s*r_hi) * r_hi), q = RN(x*r_hi + RN(x*r_lo)))
  *                            gives the same e4m3 byte as IEEE x / s.
  *  oracle_check_wire_division   the same check for the FP8 wire codec's scale
  *                            s = max(amax / 448, 1e-12) (phaa/fp8_transport.py:52),
@@ -145,19 +144,29 @@ void oracle_quant_rows_int8(int fmt, const uint16_t *x, int64_t rows, int64_t co
   }
 }
 
-/* The kernels divide the magnitude and copy the input's sign bit into the byte. */
-static float fast_div(float x, float s, float r) {
-  const float a = fabsf(x);
-  const float q0 = a * r;
-  const float e = fmaf(-q0, s, a);
-  return copysignf(fmaf(e, r, q0), x);
+/* The row quantizers' reciprocal pair: r_hi = RN(1/s), one ulp down when
+ * s * RN(1/s) > 1 (so r_hi <= 1/s), and r_lo = RN((1 - s*r_hi) * r_hi) >= 0
+ * (the residual is exact with an FMA). */
+static void row_reciprocal(float s, float *r_hi, float *r_lo) {
+  float r = 1.0f / s;
+  float e = fmaf(-s, r, 1.0f);
+  if (e < 0.0f) {
+    r = nextafterf(r, 0.0f);
+    e = fmaf(-s, r, 1.0f);
+  }
+  *r_hi = r;
+  *r_lo = e * r;
+}
+
+static float row_div(float x, float r_hi, float r_lo) {
+  const float t = x * r_lo;
+  return fmaf(x, r_hi, t);
 }
 
 /* Every positive finite amax bit pattern in [amax_lo, amax_hi] and every
  * finite x with |x| <= amax of format fmt (both signs, so signed zeros and
  * underflowing negative quotients are covered): count of e4m3 bytes that differ
- * between IEEE x / s and the HIP row quantizers' division, which takes
- * fast_div when amax >= 2^-100 and IEEE division otherwise. */
+ * between IEEE x / s and the HIP row quantizers' division row_div. */
 int64_t oracle_check_fast_division(int fmt, uint32_t amax_lo, uint32_t amax_hi) {
   int64_t bad = 0;
   for (uint32_t ab = amax_lo; ab <= amax_hi; ++ab) {
@@ -165,13 +174,13 @@ int64_t oracle_check_fast_division(int fmt, uint32_t amax_lo, uint32_t amax_hi) 
     if (!(amax > 0.0f) || isinf(amax) || isnan(amax)) continue;
     float s = amax / 448.0f;
     if (s < FLT_MIN) s = FLT_MIN;
-    const float r = 1.0f / s;
-    const int fast = amax >= 0x1p-100f;
+    float r_hi, r_lo;
+    row_reciprocal(s, &r_hi, &r_lo);
     for (uint32_t mag = 0; mag <= ab; ++mag) {
       for (uint32_t sign = 0; sign <= 0x8000u; sign += 0x8000u) {
         const float x = oracle_half_to_f32(fmt, (uint16_t)(mag | sign));
         float ref = x / s;
-        float got = fast ? fast_div(x, s, r) : x / s;
+        float got = row_div(x, r_hi, r_lo);
         ref = ref > 448.0f ? 448.0f : (ref < -448.0f ? -448.0f : ref);
         got = got > 448.0f ? 448.0f : (got < -448.0f ? -448.0f : got);
         if (oracle_e4m3_encode(ref) != oracle_e4m3_encode(got)) ++bad;
@@ -183,7 +192,8 @@ int64_t oracle_check_fast_division(int fmt, uint32_t amax_lo, uint32_t amax_hi) 
 
 /* Wire codec scale rule: every positive finite amax bit pattern in
  * [amax_lo, amax_hi] and every x with |x| <= amax (both signs); count of e4m3
- * bytes that differ between IEEE x / s and the fast division. */
+ * bytes that differ between IEEE x / s and the kernels' row_div at the wire's
+ * scale s = max(amax / 448, 1e-12). */
 int64_t oracle_check_wire_division(int fmt, uint32_t amax_lo, uint32_t amax_hi) {
   int64_t bad = 0;
   for (uint32_t ab = amax_lo; ab <= amax_hi; ++ab) {
@@ -191,12 +201,13 @@ int64_t oracle_check_wire_division(int fmt, uint32_t amax_lo, uint32_t amax_hi) 
     if (!(amax > 0.0f) || isinf(amax) || isnan(amax)) continue;
     float s = amax / 448.0f;
     if (s < 1.0e-12f) s = 1.0e-12f;
-    const float r = 1.0f / s;
+    float r_hi, r_lo;
+    row_reciprocal(s, &r_hi, &r_lo);
     for (uint32_t mag = 0; mag <= ab; ++mag) {
       for (uint32_t sign = 0; sign <= 0x8000u; sign += 0x8000u) {
         const float x = oracle_half_to_f32(fmt, (uint16_t)(mag | sign));
         float ref = x / s;
-        float got = fast_div(x, s, r);
+        float got = row_div(x, r_hi, r_lo);
         ref = ref > 448.0f ? 448.0f : (ref < -448.0f ? -448.0f : ref);
         got = got > 448.0f ? 448.0f : (got < -448.0f ? -448.0f : got);
         if (oracle_e4m3_encode(ref) != oracle_e4m3_encode(got)) ++bad;

@@ -172,7 +172,7 @@ def test_non_finite_rows_follow_nan_propagation():
 
 def test_wire_division_exhaustive_at_the_floor():
     """Every bf16 (x, amax) pair with amax up to 2^-29 (the 1e-12 scale floor is active below
-    448e-12): the kernels' Markstein division gives IEEE's e4m3 byte.  Above the floor the wire
+    448e-12): the kernels' division (div_by_row_scale) gives IEEE's e4m3 byte.  Above the floor the wire
     scale equals the row quantizer's, covered by test_fast_division_exhaustive; f16 amax never
     reaches the floor (smallest subnormal 2^-24)."""
     L = R.clib()

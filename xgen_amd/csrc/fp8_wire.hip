@@ -168,7 +168,7 @@ __device__ __forceinline__ float absmax_value(uint32_t bits) {
 }
 
 struct WireScale {
-  float s, r;
+  float s, r, r_lo;
   bool fast;
 };
 
@@ -178,10 +178,17 @@ __device__ __forceinline__ WireScale wire_scale(float amax) {
   float s = amax / kE4M3Max;
   s = (s < kScaleFloor) ? kScaleFloor : s;  // NaN kept
   q.s = canonical_nan(s);
-  q.r = 1.0f / s;
-  // Markstein division gives IEEE's e4m3 byte for every 16-bit (x, amax) pair
-  // at this scale floor (exhaustive oracle check); f32 inputs divide exactly.
+  // div_by_row_scale gives IEEE's e4m3 byte for every 16-bit (x, amax) pair,
+  // also at this scale floor (exhaustive oracle check); f32 inputs divide exactly.
   q.fast = DT != XGEN_DTYPE_F32 && __builtin_isfinite(s);
+  float r = 1.0f / s;
+  float e = __builtin_fmaf(-s, r, 1.0f);
+  if (q.fast && e < 0.0f) {  // r_hi <= 1/s: one ulp down
+    r = __uint_as_float(__float_as_uint(r) - 1u);
+    e = __builtin_fmaf(-s, r, 1.0f);
+  }
+  q.r = r;
+  q.r_lo = e * r;
   return q;
 }
 
@@ -204,11 +211,11 @@ __device__ __forceinline__ uint32_t quant4(const uint32_t *w, const WireScale &q
     v[2] = Half2<DT>::lo(w[1]), v[3] = Half2<DT>::hi(w[1]);
   }
   if constexpr (DT != XGEN_DTYPE_F32) {
-    if (q.fast) {
+    if (q.fast) {  // |x| <= amax: the quotient stays below 464, which v_cvt_pk_fp8_f32 rounds to 448 at most
       float a[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] = __builtin_fminf(div_by_scale_abs(__builtin_fabsf(v[i]), q.s, q.r), kE4M3Max);
-      return pack_e4m3x4(a[0], a[1], a[2], a[3]) | sign_bytes4(w[0], w[1]);
+      for (int i = 0; i < 4; ++i) a[i] = div_by_row_scale(v[i], q.r, q.r_lo);
+      return pack_e4m3x4(a[0], a[1], a[2], a[3]);
     }
   }
   return wire_byte_exact(v[0], q.s) | (wire_byte_exact(v[1], q.s) << 8) | (wire_byte_exact(v[2], q.s) << 16) |

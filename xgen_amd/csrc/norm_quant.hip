@@ -56,11 +56,21 @@ constexpr uint32_t kBf16OnePair = 0x3f803f80u;
 // infinite statistics) take the two-pass variance sum((x - mean)^2) / width.
 __device__ __forceinline__ bool needs_two_pass(float mean, float ex2) { return !(mean * mean <= 0.5f * ex2); }
 
+// Rows spread over WPR > 1 waves reduce across waves through LDS with one
+// barrier per reduction: each reduction of a row step has its own slots, and
+// the slots alternate between even and odd steps, so a wave writes a slot again
+// two steps later, after a barrier of the step in between that no wave passes
+// before it has read the slot.
+struct RedSlots {
+  float mom[8];    // per wave: sum, then sum of squares
+  float var[4];    // per wave: two-pass sum of squares / RMS sum of squares
+  uint32_t amax[4];
+};
+
 template <int WPR>
 __device__ __forceinline__ float row_sum(float v, int wave, int lane, float *red) {
   v = wave_sum_f32(v);
   if constexpr (WPR > 1) {
-    __syncthreads();  // red[] reuse
     if (lane == 0) red[wave] = v;
     __syncthreads();
     const int w0 = (wave / WPR) * WPR;
@@ -73,7 +83,7 @@ __device__ __forceinline__ float row_sum(float v, int wave, int lane, float *red
 
 // Sum and sum of squares of a row, reduced together.  two_pass_here: this row
 // needs the two-pass variance; two_pass_any: some row of the workgroup does
-// (the same value in every wave, so the second reduction's barriers stay in
+// (the same value in every wave, so the second reduction's barrier stays in
 // step; each row still uses only its own statistics).
 struct RowMoments {
   float s1, s2;
@@ -90,7 +100,6 @@ __device__ __forceinline__ RowMoments row_moments(float s1, float s2, int wave, 
     m.s1 = s1, m.s2 = s2;
     m.two_pass_here = m.two_pass_any = needs_two_pass(s1 * inv_w, s2 * inv_w);
   } else {
-    __syncthreads();  // red[] reuse
     if (lane == 0) red[wave] = s1, red[4 + wave] = s2;
     __syncthreads();
     m.two_pass_any = false;
@@ -111,7 +120,6 @@ template <int WPR>
 __device__ __forceinline__ uint32_t row_max_u32(uint32_t v, int wave, int lane, uint32_t *red) {
   v = wave_max_u32(v);
   if constexpr (WPR > 1) {
-    __syncthreads();
     if (lane == 0) red[wave] = v;
     __syncthreads();
     const int w0 = (wave / WPR) * WPR;
@@ -165,7 +173,7 @@ struct Weight8 {
 // the scale table already holds bf16(1 + scale).  WT: weight dtype (NONE,
 // BF16, F32).  NORMED: also store the pre-quantization rows.
 template <int NORM, int OUT, int WT, int WPR, int CH, bool NORMED>
-__device__ __forceinline__ void norm_rows(const NormArgs &a, float *red_f, uint32_t *red_u) {
+__device__ __forceinline__ void norm_rows(const NormArgs &a, RedSlots (&red)[2]) {
   constexpr bool kOnePlus = (NORM & XGEN_NORM_SCALE_ONE_PLUS) != 0;
   constexpr int kNorm = NORM & ~XGEN_NORM_SCALE_ONE_PLUS;
   constexpr int kRowsPerBlock = 4 / WPR;
@@ -225,6 +233,7 @@ __device__ __forceinline__ void norm_rows(const NormArgs &a, float *red_f, uint3
 
   u32x4 c[CH], cn[CH];
   int64_t g;
+  int parity = 0;  // LDS reduction slots of this step
   // one row (base: the workgroup's first row of this step)
   auto row_step = [&](int64_t base) {
     const uint32_t row = clamp_row(base + wave / WPR);
@@ -239,7 +248,8 @@ __device__ __forceinline__ void norm_rows(const NormArgs &a, float *red_f, uint3
     __builtin_amdgcn_sched_barrier(0);
 
     // statistics in fp32 (chunks past the row's end are zeros)
-    float rstd, mean = 0.0f;  // n = (x - mean) * rstd, as the eager LayerNorm computes it
+    float rstd, mean = 0.0f;
+    bool two_pass = false;
     if constexpr (kNorm == XGEN_NORM_LAYER) {
       float s1[2] = {0.0f, 0.0f}, s2[2] = {0.0f, 0.0f};
 #pragma unroll
@@ -251,7 +261,7 @@ __device__ __forceinline__ void norm_rows(const NormArgs &a, float *red_f, uint3
           s2[k & 1] = dot2_bf16(w[k], w[k], s2[k & 1]);
         }
       }
-      const RowMoments mo = row_moments<WPR>(s1[0] + s1[1], s2[0] + s2[1], wave, lane, red_f, inv_w);
+      const RowMoments mo = row_moments<WPR>(s1[0] + s1[1], s2[0] + s2[1], wave, lane, red[parity].mom, inv_w);
       // sum / width: the product with 1 / width plus one FMA correction, exact
       // whenever the quotient is representable (a constant row's mean is its value)
       const float mean0 = mo.s1 * inv_w;
@@ -271,9 +281,10 @@ __device__ __forceinline__ void norm_rows(const NormArgs &a, float *red_f, uint3
             }
           }
         }
-        const float var2 = row_sum<WPR>(acc2, wave, lane, red_f) * inv_w;
+        const float var2 = row_sum<WPR>(acc2, wave, lane, red[parity].var) * inv_w;
         if (mo.two_pass_here) var = var2;
       }
+      two_pass = mo.two_pass_here;
       rstd = __builtin_amdgcn_rsqf(var + a.eps);
     } else {
       float s2[2] = {0.0f, 0.0f};
@@ -283,75 +294,97 @@ __device__ __forceinline__ void norm_rows(const NormArgs &a, float *red_f, uint3
 #pragma unroll
         for (int k = 0; k < 4; ++k) s2[k & 1] = dot2_bf16(w[k], w[k], s2[k & 1]);
       }
-      const float ms = row_sum<WPR>(s2[0] + s2[1], wave, lane, red_f) * inv_w;
+      const float ms = row_sum<WPR>(s2[0] + s2[1], wave, lane, red[parity].var) * inv_w;
       rstd = __builtin_amdgcn_rsqf(ms + a.eps);
     }
+    const float neg_mean_rstd = -mean * rstd;
 
-    // normalise, modulate with the table row, keep m as packed bf16 (in c);
-    // bf16 roundings two at a time (one conversion per pair)
+    // normalise and modulate with the table row: m as fp32 values of bf16
+    // precision (each bf16 rounding is one v_cvt_pk_bf16_f32 whose other half
+    // is zero, so its word is the rounded value's fp32 bits).  LayerNorm rows
+    // with an ordinary variance take n = fma(x, rstd, -mean * rstd); rows that
+    // took the two-pass variance (a large common offset, constant rows) keep
+    // the eager (x - mean) * rstd, whose subtraction is exact there.
+    float m[CH][8];
+    auto modulate = [&](auto exact_tag) {
+      constexpr bool kExact = decltype(exact_tag)::value;
 #pragma unroll
-    for (int j = 0; j < CH; ++j) {
-      float xv[8], n[8];
-      unpack8<XGEN_DTYPE_BF16>(c[j], xv);
+      for (int j = 0; j < CH; ++j) {
+        // opaque copies: each of the two instances unpacks its own inputs (no
+        // common code is hoisted above the branch, where it would stay live)
+        u32x4 xj = c[j], sj = scw[j], tj = shw[j];
+        asm volatile("" : "+v"(xj), "+v"(sj), "+v"(tj));
+        const uint32_t xw[4] = {xj.x, xj.y, xj.z, xj.w};
+        const uint32_t scp[4] = {sj.x, sj.y, sj.z, sj.w};
+        const uint32_t shp[4] = {tj.x, tj.y, tj.z, tj.w};
 #pragma unroll
-      for (int i = 0; i < 8; ++i) n[i] = (kNorm == XGEN_NORM_LAYER ? xv[i] - mean : xv[i]) * rstd;
-      if constexpr (WT != XGEN_DTYPE_NONE) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) n[i] *= wt[j].get(i);
-      }
-      const uint32_t scp[4] = {scw[j].x, scw[j].y, scw[j].z, scw[j].w};
-      const uint32_t shp[4] = {shw[j].x, shw[j].y, shw[j].z, shw[j].w};
-      uint32_t pk[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float n0 = n[2 * i], n1 = n[2 * i + 1];
-        round_bf16x2(n0, n1);
-        float f0 = Half2<XGEN_DTYPE_BF16>::lo(scp[i]), f1 = Half2<XGEN_DTYPE_BF16>::hi(scp[i]);
-        if constexpr (!kOnePlus) {
-          f0 += 1.0f, f1 += 1.0f;
-          round_bf16x2(f0, f1);
+        for (int k = 0; k < 8; ++k) {
+          const int i = k >> 1;
+          auto half = [&](uint32_t w) {
+            return (k & 1) ? Half2<XGEN_DTYPE_BF16>::hi(w) : Half2<XGEN_DTYPE_BF16>::lo(w);
+          };
+          const float x = half(xw[i]);
+          float n;
+          if constexpr (kNorm == XGEN_NORM_RMS) n = x * rstd;
+          else if constexpr (kExact) n = (x - mean) * rstd;
+          else n = __builtin_fmaf(x, rstd, neg_mean_rstd);
+          if constexpr (WT != XGEN_DTYPE_NONE) n *= wt[j].get(k);
+          n = round_bf16(n);
+          float f = half(scp[i]);
+          if constexpr (!kOnePlus) f = round_bf16(1.0f + f);
+          const float pr = round_bf16(n * f);
+          float mv = round_bf16(pr + half(shp[i]));
+          asm volatile("" : "+v"(mv));  // the rounding stays in this instance (not sunk past the merge)
+          m[j][k] = mv;
         }
-        float p0 = n0 * f0, p1 = n1 * f1;
-        round_bf16x2(p0, p1);
-        pk[i] = pack_bf16x2(p0 + Half2<XGEN_DTYPE_BF16>::lo(shp[i]), p1 + Half2<XGEN_DTYPE_BF16>::hi(shp[i]));
       }
-      c[j] = u32x4{pk[0], pk[1], pk[2], pk[3]};
-    }
+    };
+    if (kNorm == XGEN_NORM_LAYER && two_pass) modulate(std::true_type{});
+    else modulate(std::false_type{});
     if (!full) {  // uniform: chunks past the row's end are zeros again (they stay out of the row max)
 #pragma unroll
       for (int j = 0; j < CH; ++j)
-        if (!chunk_ok(j)) c[j] = u32x4{0, 0, 0, 0};
-    }
-    u16x2 am = {0, 0};
 #pragma unroll
-    for (int j = 0; j < CH; ++j) am = absmax_chunk<XGEN_DTYPE_BF16>(c[j], am);
+        for (int k = 0; k < 8; ++k) m[j][k] = chunk_ok(j) ? m[j][k] : 0.0f;
+    }
+    // max |m| (NaN-propagating: v_maximum3_f32), as the bits of a float >= +0 or a NaN
+    float am = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CH; ++j)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) am = __builtin_elementwise_maximum(am, __builtin_fabsf(m[j][k]));
     // the table rows are consumed: the next row's go into the same registers
     __builtin_amdgcn_sched_barrier(0);
     load_tables(gn);
     __builtin_amdgcn_sched_barrier(0);
-    const uint32_t amax_bits = row_max_u32<WPR>(hmax_u16x2(am), wave, lane, red_u);
+    const uint32_t amax_bits = row_max_u32<WPR>(__float_as_uint(am) & 0x7fffffffu, wave, lane, red[parity].amax);
 
     // quantize from registers; a row whose index is outside the table is
     // poisoned (NaN scale; NaN bytes for E4M3, zeros for I8; zero normed row)
-    const float amax = Half2<XGEN_DTYPE_BF16>::from_absbits(amax_bits);
+    const float amax = __uint_as_float(amax_bits);
     const RowQuant p = (OUT == XGEN_DTYPE_E4M3) ? fp8_row_params(amax) : i8_row_params(amax);
     const u32x2 bad = (OUT == XGEN_DTYPE_E4M3) ? u32x2{0x7f7f7f7fu, 0x7f7f7f7fu} : u32x2{0u, 0u};
     const __amdgpu_buffer_rsrc_t rq = rsrc(a.q + (int64_t)row * a.width, a.width);
     const __amdgpu_buffer_rsrc_t rn = rsrc(NORMED ? a.normed + (int64_t)row * row_bytes : a.q, NORMED ? row_bytes : 0);
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
-      float v[8];
-      unpack8<XGEN_DTYPE_BF16>(c[j], v);
-      const u32x2 qb = g_ok ? quant8<OUT>(c[j], v, p) : bad;
+      const u32x2 qb = g_ok ? quant8<OUT>(m[j], p) : bad;
       // a chunk past the end: its offset stays past the row's bytes, the stores are dropped
       __builtin_amdgcn_raw_buffer_store_b64(qb, rq, in_off(j) >> 1, 0, 0);
-      if constexpr (NORMED)
-        __builtin_amdgcn_raw_buffer_store_b128(g_ok ? c[j] : u32x4{0, 0, 0, 0}, rn, in_off(j), 0, 0);
+      if constexpr (NORMED) {
+        uint32_t pk[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)  // the high halves of two fp32 words of bf16 precision
+          pk[i] = __builtin_amdgcn_perm(__float_as_uint(m[j][2 * i + 1]), __float_as_uint(m[j][2 * i]), 0x07060302u);
+        __builtin_amdgcn_raw_buffer_store_b128(g_ok ? u32x4{pk[0], pk[1], pk[2], pk[3]} : u32x4{0, 0, 0, 0}, rn,
+                                               in_off(j), 0, 0);
+      }
     }
     a.token_scale[row] = g_ok ? p.s : __builtin_nanf("");  // every lane of the row: the same value
 #pragma unroll
     for (int j = 0; j < CH; ++j) c[j] = cn[j];
     g = gn;
+    parity ^= 1;
   };
 
   int64_t base = (int64_t)blockIdx.x * kRowsPerBlock;
@@ -368,10 +401,9 @@ __device__ __forceinline__ void norm_rows(const NormArgs &a, float *red_f, uint3
 
 template <int NORM, int OUT, int WT, int WPR, int CH>
 __global__ __launch_bounds__(kThreads) void norm_affine_quant_kernel(NormArgs a) {
-  __shared__ float red_f[8];
-  __shared__ uint32_t red_u[4];
-  if (a.normed) norm_rows<NORM, OUT, WT, WPR, CH, true>(a, red_f, red_u);
-  else norm_rows<NORM, OUT, WT, WPR, CH, false>(a, red_f, red_u);
+  __shared__ RedSlots red[2];
+  if (a.normed) norm_rows<NORM, OUT, WT, WPR, CH, true>(a, red);
+  else norm_rows<NORM, OUT, WT, WPR, CH, false>(a, red);
 }
 
 template <int NORM, int OUT, int WT, int WPR, int CH>

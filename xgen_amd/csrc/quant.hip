@@ -89,7 +89,7 @@ __global__ __launch_bounds__(kThreads) void quant_rows_vec_kernel(
       float v[8];
       unpack8<DT>(c[j], v);
       // a chunk past the end: its offset stays past the row's bytes, the store is dropped
-      __builtin_amdgcn_raw_buffer_store_b64(quant8<OUT>(c[j], v, p), rq, in_off(j) >> 1, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b64(quant8<OUT>(v, p), rq, in_off(j) >> 1, 0, 0);
     }
     scale[row] = p.s;  // every lane of the row: the same value
 #pragma unroll
@@ -131,7 +131,7 @@ __global__ __launch_bounds__(kThreads) void quant_rows_generic_kernel(
     const float v = Half2<DT>::lo(w);
     uint32_t b;
     if constexpr (OUT == XGEN_DTYPE_E4M3) {
-      b = p.finite ? (pack_e4m3x4(clamp448(div_by_scale(v, p.s, p.mul)), 0.f, 0.f, 0.f) & 0xffu)
+      b = p.finite ? (pack_e4m3x4(div_by_row_scale(v, p.mul, p.mul_lo), 0.f, 0.f, 0.f) & 0xffu)
                    : e4m3_slow_byte(v, p.s);
     } else {
       b = p.finite ? q_i8(v, p.mul) : i8_slow_byte(v, p.mul);
@@ -262,6 +262,7 @@ __global__ __launch_bounds__(kThreads) void fp8_pack_kernel(const uint8_t *__res
   RowQuant p;
   p.s = scale[0];
   p.mul = 0.0f;
+  p.mul_lo = 0.0f;
   p.finite = false;
   const int64_t nchunks = numel >> 3;
   for (int64_t ci = (int64_t)blockIdx.x * kThreads + threadIdx.x; ci < nchunks;
@@ -269,7 +270,7 @@ __global__ __launch_bounds__(kThreads) void fp8_pack_kernel(const uint8_t *__res
     const u32x4 c = *reinterpret_cast<const u32x4 *>(x + ci * 16);
     float v[8];
     unpack8<DT>(c, v);
-    *reinterpret_cast<u32x2 *>(q + ci * 8) = quant8<XGEN_DTYPE_E4M3>(c, v, p);
+    *reinterpret_cast<u32x2 *>(q + ci * 8) = quant8<XGEN_DTYPE_E4M3>(v, p);
   }
   if (blockIdx.x == 0) {
     const uint16_t *xs = reinterpret_cast<const uint16_t *>(x);

@@ -108,7 +108,7 @@ __global__ __launch_bounds__(kThreads) void swiglu_quant_kernel(SwigluArgs a) {
         if (ci < nchunks) {
           float v[8];
           unpack8<XGEN_DTYPE_BF16>(h[j], v);
-          *reinterpret_cast<u32x2 *>(qr + (int64_t)ci * 8) = quant8<OUT>(h[j], v, p);
+          *reinterpret_cast<u32x2 *>(qr + (int64_t)ci * 8) = quant8<OUT>(v, p);
           if (ar) *reinterpret_cast<u32x4 *>(ar + (int64_t)ci * 16) = h[j];
         }
       }
@@ -230,7 +230,7 @@ __global__ __launch_bounds__(kLutThreads) void swiglu_quant_lut_kernel(SwigluArg
         if (ci < nchunks) {
           float v[8];
           unpack8<XGEN_DTYPE_BF16>(h[j], v);
-          *reinterpret_cast<u32x2 *>(qr + (int64_t)ci * 8) = quant8<OUT>(h[j], v, p);
+          *reinterpret_cast<u32x2 *>(qr + (int64_t)ci * 8) = quant8<OUT>(v, p);
           if (ar) *reinterpret_cast<u32x4 *>(ar + (int64_t)ci * 16) = h[j];
         }
       }

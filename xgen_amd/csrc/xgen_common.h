@@ -116,9 +116,11 @@ __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
   f32x2 v = {lo, hi};
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
 }
-// fp32 rounded to bf16 precision, returned as fp32.
+// fp32 rounded to bf16 precision (RNE), returned as fp32: one
+// v_cvt_pk_bf16_f32 with the value in the high half and +0 in the low half, so
+// the word is the rounded value's fp32 bit pattern.
 __device__ __forceinline__ float round_bf16(float x) {
-  return __uint_as_float(pack_bf16x2(x, 0.0f) << 16);
+  return __uint_as_float(pack_bf16x2(0.0f, x));
 }
 
 // Gated residual of one 16-byte chunk (8 bf16 values each of residual r,
@@ -150,7 +152,9 @@ __device__ __forceinline__ u32x4 gate_residual8(const u32x4 &r, const u32x4 &y, 
 // v_cvt_pk_fp8_f32 rounds to nearest even into e4m3fn (gfx950: OCP format).
 // Inputs here are always finite and within [-448, 448].
 __device__ __forceinline__ uint32_t pack_e4m3x4(float a, float b, float c, float d) {
-  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  // the first conversion's preserved high word is overwritten by the second:
+  // any register serves as its input (a's, which it consumes anyway; no v_mov 0)
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, __float_as_int(a), false);
   w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
   return (uint32_t)w;
 }
@@ -160,32 +164,17 @@ __device__ __forceinline__ float clamp448(float v) {
   return __builtin_amdgcn_fmed3f(v, -kE4M3Max, kE4M3Max);
 }
 
-// x / s for a finite positive normal s, given r = RN(1/s): q0 = RN(x*r),
-// e = x - q0*s (exact with an FMA unless it underflows), q = RN(q0 + e*r)
-// (Markstein's correction step).  With the amax gate of fp8_row_params the
-// e4m3 byte equals that of IEEE x / s for every (bf16|f16 x, amax) pair a row
-// quantizer can see (exhaustive oracle check).
-// The correction adds e = +0 to q0 = -0 for x = -0 (giving +0), so the sign
-// of x is restored: IEEE x / s keeps it for zero and underflowing quotients.
-__device__ __forceinline__ float div_by_scale(float x, float s, float r) {
-  float q0 = x * r;
-  float e = __builtin_fmaf(-q0, s, x);
-  return __builtin_copysignf(__builtin_fmaf(e, r, q0), x);
-}
-
-// The same division of a magnitude a >= 0 (result >= 0).  With round-to-
-// nearest-even each step commutes with negation, so div_by_scale(x) ==
-// copysign(div_by_scale_abs(|x|), x) bit for bit.
-__device__ __forceinline__ float div_by_scale_abs(float a, float s, float r) {
-  float q0 = a * r;
-  float e = __builtin_fmaf(-q0, s, a);
-  return __builtin_fmaf(e, r, q0);
-}
-
-// Sign bits of four 16-bit floats (bf16 or f16: bit 15 of each half of w0, w1)
-// placed at bit 7 of bytes 0..3: v_perm_b32 picks bytes 1, 3 of w0 and 1, 3 of w1.
-__device__ __forceinline__ uint32_t sign_bytes4(uint32_t w0, uint32_t w1) {
-  return __builtin_amdgcn_perm(w1, w0, 0x07050301u) & 0x80808080u;
+// The row quantizers' x / s in two operations: 1/s is carried as r_hi + r_lo
+// (r_hi = 1/s rounded toward zero, r_lo = RN((1 - s*r_hi) * r_hi) >= 0, together
+// about 46 bits) and q = RN(x*r_hi + RN(x*r_lo)).  For a finite scale the e4m3
+// byte equals that of IEEE x / s for every (bf16|f16 x, amax) pair a row
+// quantizer can see, both signs, at the row quantizers' scale floor FLT_MIN and
+// at the wire codec's 1e-12 (exhaustive oracle checks); r_lo >= 0 keeps
+// x = -0 at -0 (-0 * r_lo + -0 * r_hi), and a negative
+// quotient that rounds to zero in e4m3 is encoded -0 by v_cvt_pk_fp8_f32, as
+// IEEE x / s gives it.
+__device__ __forceinline__ float div_by_row_scale(float x, float r_hi, float r_lo) {
+  return __builtin_fmaf(x, r_hi, x * r_lo);
 }
 
 // INT8 lane value: rint_half_even(x * alpha) as a byte.
@@ -248,23 +237,28 @@ __device__ __forceinline__ float canonical_nan(float v) { return v == v ? v : __
 
 // Per-row quantization parameters derived from the row's max |x| (as fp32).
 struct RowQuant {
-  float s;      // stored scale
-  float mul;    // FP8: RN(1/s); INT8: alpha = RN(127/amax)
-  bool finite;  // FP8: scale finite (fast division valid)
+  float s;       // stored scale
+  float mul;     // FP8: 1/s rounded toward zero (r_hi of div_by_row_scale); INT8: alpha = RN(127/amax)
+  float mul_lo;  // FP8: r_lo of div_by_row_scale; INT8: unused (0)
+  bool finite;   // FP8: scale finite (fast division valid)
 };
-
-// Rows with max |x| below this use IEEE division: for smaller scales the FMA
-// residual of div_by_scale can underflow and the e4m3 byte can differ (found
-// only for amax <= 2^-105 by the oracle's exhaustive check).
-constexpr float kFastDivMinAmax = 0x1p-100f;
 
 __device__ __forceinline__ RowQuant fp8_row_params(float amax) {
   RowQuant p;
   float s = amax / kE4M3Max;
   s = (s < kFltMin) ? kFltMin : s;  // clamp_min keeps NaN
   p.s = canonical_nan(s);
-  p.mul = 1.0f / s;
-  p.finite = __builtin_isfinite(s) && amax >= kFastDivMinAmax;
+  p.finite = __builtin_isfinite(s);
+  // r = RN(1/s) is a positive normal for a finite s >= FLT_MIN; the residual
+  // 1 - s*r is exact with an FMA; a negative one means r > 1/s: one ulp down.
+  float r = 1.0f / s;
+  float e = __builtin_fmaf(-s, r, 1.0f);
+  if (p.finite && e < 0.0f) {
+    r = __uint_as_float(__float_as_uint(r) - 1u);
+    e = __builtin_fmaf(-s, r, 1.0f);
+  }
+  p.mul = r;
+  p.mul_lo = e * r;
   return p;
 }
 
@@ -272,6 +266,7 @@ __device__ __forceinline__ RowQuant i8_row_params(float amax) {
   RowQuant p;
   p.s = canonical_nan(amax * kInv127);
   p.mul = 127.0f / amax;
+  p.mul_lo = 0.0f;
   // amax == 0 or subnormal (alpha = inf), inf or NaN: products may be non-finite -> slow path.
   p.finite = amax > 0.0f && __builtin_isfinite(amax) && __builtin_isfinite(p.mul);
   return p;
@@ -293,24 +288,20 @@ __device__ __forceinline__ uint32_t e4m3_slow_byte(float x, float s) {
   return pack_e4m3x4(clamp448(v), 0.0f, 0.0f, 0.0f) & 0xffu;
 }
 
-// Quantizes one 16-byte chunk c of 8 bf16/f16 values (v = the same values as
-// fp32) into 8 bytes.  E4M3: the magnitude is divided and the sign bit is
-// copied from the 16-bit input (so -0 and negative values that round to zero
-// keep their sign, as IEEE x / s does).  No clamp is needed on the fast path:
-// |x| <= amax and s = RN(amax / 448) bound the quotient by 448 (1 + 2^-22),
-// below 464, and v_cvt_pk_fp8_f32 rounds such values to 448 (checked on the
-// GPU for every bf16 amax).
+// Quantizes 8 values (bf16/f16 values as fp32) into 8 bytes.  No clamp is
+// needed on the E4M3 fast path: |x| <= amax and s = RN(amax / 448) bound the
+// quotient by 448 (1 + 2^-22), below 464, and v_cvt_pk_fp8_f32 rounds such
+// values to 448 (checked on the GPU for every bf16 amax).
 template <int OUT>
-__device__ __forceinline__ u32x2 quant8(const u32x4 &c, const float (&v)[8], const RowQuant &p) {
+__device__ __forceinline__ u32x2 quant8(const float (&v)[8], const RowQuant &p) {
   u32x2 r;
   if constexpr (OUT == XGEN_DTYPE_E4M3) {
     if (p.finite) {
       float q[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        q[i] = div_by_scale_abs(__builtin_fabsf(v[i]), p.s, p.mul);
-      r.x = pack_e4m3x4(q[0], q[1], q[2], q[3]) | sign_bytes4(c.x, c.y);
-      r.y = pack_e4m3x4(q[4], q[5], q[6], q[7]) | sign_bytes4(c.z, c.w);
+      for (int i = 0; i < 8; ++i) q[i] = div_by_row_scale(v[i], p.mul, p.mul_lo);
+      r.x = pack_e4m3x4(q[0], q[1], q[2], q[3]);
+      r.y = pack_e4m3x4(q[4], q[5], q[6], q[7]);
     } else {
       uint32_t b[8];
 #pragma unroll
