@@ -1044,6 +1044,12 @@ void gemm_w4_kernel(GemmArgs p) {
   // every wave's reads of this pair's slot, which takes the DMA of the pair
   // after next, spread over this sub-stage's MFMAs (all at once is measured
   // slower: the loads queue in the address unit ahead of the MFMAs).
+  // vector-memory operations of one epilogue after the pending DMA: its 32 row
+  // stores (2 halves x 4 token blocks x 4 row groups, all issued, out-of-range
+  // ones included); the gated and accumulator-output forms issue a varying
+  // number and wait for all
+  constexpr int kEpiStores = (GATED || ACC_OUT) ? 0 : 2 * FM * 4;
+  bool epi_stores = false;
   auto stage = [&](auto U, auto FRESH, auto READ) {
     constexpr int u = decltype(U)::value;
     constexpr bool fresh = decltype(FRESH)::value;  // the tile's first sub-stage
@@ -1052,7 +1058,11 @@ void gemm_w4_kernel(GemmArgs p) {
     constexpr bool odd = u & 1;  // the second sub-stage of a pair: barrier, and the DMA of pair + 2
     Issue is{};
     if constexpr (odd) {
-      wait_vmcnt<0>();
+      // the DMA of the next pair; after an epilogue its row stores were issued
+      // later and need not have completed (the counter retires in issue order)
+      if (epi_stores) wait_vmcnt<kEpiStores>();
+      else wait_vmcnt<0>();
+      epi_stores = false;
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
       lds_barrier();
       is = issue_begin(u >> 1);
@@ -1164,6 +1174,7 @@ void gemm_w4_kernel(GemmArgs p) {
     // stream's end, whose loads read zeros, and its MFMAs' results are unused
     read_first();
     stage0_with_epilogue();
+    epi_stores = kEpiStores > 0;
   }
   // the loads of the stages past my last may still be writing LDS
   wait_vmcnt<0>();
