@@ -114,6 +114,7 @@ struct GemmArgs {
   int64_t gate_rows;
   const int64_t *indices;
   uint32_t seq;
+  uint32_t residual_bytes, gate_bytes;  // (M - 1) * ld_residual * 2 + N * 2, (gate_rows - 1) * gate_stride * 2 + N * 2
 };
 
 // LDS layout of one operand tile of one stage: rows of 64 bytes (4 chunks
@@ -792,6 +793,11 @@ void gemm_w4_kernel(GemmArgs p) {
   const float sw0 = p.sw_stride ? 0.0f : p.sw[0];
   // the output rows as a buffer: stores at kOutOfRange are dropped
   const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(p.out, (short)0, (int)p.out_bytes, kBufferFlags);
+  // the gated epilogue's residual rows and gate table (reads past them return zeros)
+  const __amdgpu_buffer_rsrc_t rres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(p.residual), (short)0, GATED ? (int)p.residual_bytes : 0, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t rgate = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(p.gate), (short)0, GATED ? (int)p.gate_bytes : 0, kBufferFlags);
 
   // --- global -> LDS DMA (layout as gemm_w8a8_kernel: chunk c of row r at
   // c ^ ((r >> 2) & 3); wave w fills rows [64 w, 64 w + 64) of both tiles) ---
@@ -897,7 +903,15 @@ void gemm_w4_kernel(GemmArgs p) {
     u32x4 prow[4];
     uint32_t pbase = 0;  // output byte offset of the pending rows (row rr, this lane's 8 columns)
     bool pcol = false;   // the pending columns lie below N
-    int pm = 0, pn = 0;  // the pending rows' first token and this lane's first column (GATED)
+    int pm = 0;          // the pending rows' first token (GATED)
+    // GATED: each step reads the AdaLN indices of its 4 token rows (mrow + 8 q) before
+    // its values are computed, and after its read-back issues the loads of its
+    // residual pieces, which its stores use during the next step; pgrow is the
+    // pending rows' gate-table row, kOutOfRange where the index lies outside it
+    u32x2 gidx[4];
+    uint32_t pgrow[4];
+    u32x4 pres[4];
+    int pn = 0;  // this lane's first pending column
     // rows past M need no check: their offsets lie past the output's last byte, where the
     // buffer drops stores (the host keeps (M + 256) * ldo * 2 below 2^32)
     auto store_pending = [&]() {
@@ -905,17 +919,13 @@ void gemm_w4_kernel(GemmArgs p) {
       for (int q = 0; q < 4; ++q) {
         u32x4 v = prow[q];
         if constexpr (GATED) {
-          const int m = pm + q * 8, n = pn;
-          if (pcol && m < p.M) {
-            const int64_t gi = p.indices[(uint32_t)m % p.seq];
-            if (gi >= 0 && gi < p.gate_rows) {
-              const u32x4 r = *reinterpret_cast<const u32x4 *>(p.residual + ((int64_t)m * p.ld_residual + n) * 2);
-              const u32x4 t = *reinterpret_cast<const u32x4 *>(p.gate + (gi * p.gate_stride + n) * 2);
-              v = gate_residual8(r, v, t);
-            } else {
-              v = u32x4{0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};  // index outside the table: NaN
-            }
-          }
+          // (the gate rows are small and cache-resident: read here)
+          const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(
+              rgate, pcol && pgrow[q] != kOutOfRange ? (pgrow[q] * (uint32_t)p.gate_stride + (uint32_t)pn) * 2
+                                                      : kOutOfRange, 0, 0);
+          if (pcol && pm + q * 8 < p.M)
+            v = pgrow[q] != kOutOfRange ? gate_residual8(pres[q], v, t)
+                                        : u32x4{0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};  // index outside the table: NaN
         }
         // non-temporal: the output streams past the caches the operands are re-read from
         // (measured: FFN down 4.7%, FFN up 2% faster; QKV unchanged)
@@ -979,6 +989,13 @@ void gemm_w4_kernel(GemmArgs p) {
       for (int j = 0; j < FM; ++j) {
         const int ml = wm * kWaveRows + j * 32 + wrow;
         const float sam = sam4[j];
+        if constexpr (GATED) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t m = (uint32_t)(m0 + wm * kWaveRows + j * 32 + rr + 8 * q);
+            gidx[q] = *reinterpret_cast<const u32x2 *>(p.indices + m % p.seq);
+          }
+        }
 #pragma unroll
         for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
@@ -1029,6 +1046,17 @@ void gemm_w4_kernel(GemmArgs p) {
         pcol = ncol < p.N;
         pm = mrow;
         pn = ncol;
+        if constexpr (GATED) {
+          // (out-of-range rows and columns read zeros, and their stores are dropped)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t m = (uint32_t)(mrow + 8 * q);
+            // an int64 index in [0, gate_rows): high word 0, low word below gate_rows (< 2^31)
+            pgrow[q] = gidx[q].y == 0 && gidx[q].x < (uint32_t)p.gate_rows ? gidx[q].x : kOutOfRange;
+            pres[q] = __builtin_amdgcn_raw_buffer_load_b128(
+                rres, pcol ? (m * (uint32_t)p.ld_residual + (uint32_t)ncol) * 2 : kOutOfRange, 0, 0);
+          }
+        }
       }
     }
     store_pending();
@@ -1239,6 +1267,10 @@ int gemm_entry(const char *fn, const void *a, int64_t lda, const void *w, int64_
     if (gp.ld_residual % 8 || gp.gate_stride % 8 || !aligned16(gp.residual) || !aligned16(gp.gate))
       return fail(XGEN_ERR_UNSUPPORTED, "%s: residual and gate rows must be 16-byte aligned", fn);
     if (M >= 0x7fffffffLL) return fail(XGEN_ERR_UNSUPPORTED, "%s: too many rows", fn);
+    // 32-bit offsets of the residual rows (past M included) and of the gate rows
+    if ((uint64_t)(M + 256) * (uint64_t)gp.ld_residual * 2 >= (1ull << 31) ||
+        (uint64_t)gp.gate_rows * (uint64_t)gp.gate_stride * 2 >= (1ull << 31))
+      return fail(XGEN_ERR_UNSUPPORTED, "%s: residual or gate table above 2 GiB", fn);
   }
   const int64_t a_bytes = (M - 1) * lda + K, w_bytes = (N - 1) * ldw + K;
   if (a_bytes >= (int64_t)kOutOfRange || w_bytes >= (int64_t)kOutOfRange)
@@ -1283,6 +1315,8 @@ int gemm_entry(const char *fn, const void *a, int64_t lda, const void *w, int64_
   g.gate_rows = gp.gate_rows;
   g.indices = gp.indices;
   g.seq = (uint32_t)gp.seq;
+  g.residual_bytes = gated ? (uint32_t)(((M - 1) * gp.ld_residual + N) * 2) : 0;
+  g.gate_bytes = gated ? (uint32_t)(((gp.gate_rows - 1) * gp.gate_stride + N) * 2) : 0;
   g.kt4 = (int)(((K + BK - 1) / BK + 3) / 4 * 4);
   const int64_t out_bytes = ((M - 1) * ldo + N) * 2;
   if (out_bytes >= (int64_t)kOutOfRange)
