@@ -124,6 +124,33 @@ def test_pack_with_caller_scale(cuda):
     assert torch.equal(u8(q), R.canonical_nan_e4m3(ref).view(torch.uint8))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_pack_every_input_value_at_peak_form_scales(cuda, dtype):
+    """fp8_pack's fast division applies to scales of the per-tensor kernel's form,
+    max(RN(a / 448), FLT_MIN) for an input value a (what fp8_tensor_scale gives, and a MAX
+    all-reduce of such scales): every 16-bit input value (NaN, +-Inf, -0, subnormals) against
+    IEEE division + clamp, with peaks above, below and equal to most inputs (values above a
+    are clamped), at the FLT_MIN floor, and for caller scales of other forms (IEEE path)."""
+    x = torch.arange(1 << 16, dtype=torch.int32).to(torch.int16).view(dtype)
+    xd = x.to(cuda)
+    peaks = [1.0, 3.0, 448.0, 1344.0, 0.0173, 2.0 ** -14, 1e-30, 0.0]
+    peaks.append(3.3e38 if dtype == torch.bfloat16 else 65504.0)
+    scales = []
+    for a in peaks:
+        src = torch.zeros(16, dtype=dtype)
+        src[5] = a
+        scales.append(xops.fp8_tensor_scale(src.to(cuda)))
+    scales.append(torch.tensor(0.0173, dtype=torch.float32, device=cuda))  # not of that form
+    scales.append(torch.tensor(1.0 / 3.0, dtype=torch.float32, device=cuda))
+    for scale in scales:
+        q = xops.fp8_pack(xd, scale)
+        ref = R.canonical_nan_e4m3((x.float() / scale.cpu()).clamp(-448, 448).to(torch.float8_e4m3fn))
+        got, want = u8(q), ref.view(torch.uint8)
+        bad = torch.nonzero(got != want)
+        assert bad.numel() == 0, (float(scale), x[bad[:4, 0]].tolist(), got[bad[:4, 0]].tolist(),
+                                  want[bad[:4, 0]].tolist())
+
+
 def test_full_size_requant_k12288(cuda):
     """The FFN-down requant at C3 size (M=15,624, K=12,288): the call moves 576 MB, more than the
     256 MB last-level cache, so the quantizer takes its non-temporal-load form.  Bytes and scales

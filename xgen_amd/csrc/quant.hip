@@ -251,32 +251,64 @@ __global__ __launch_bounds__(kThreads) void abs_peak_final_kernel(const uint32_t
   }
 }
 
-// q[i] = e4m3(clamp(x[i] / scale[0])) over a contiguous tensor.
+// True when s is a scale the per-tensor scale kernel produces from an input
+// value a: max(RN(a / 448), FLT_MIN) (a MAX over several such scales is one of
+// them).  a is recovered as s * 448 rounded to the input type: s is within half
+// an fp32 ulp of a / 448, far inside half a bf16 / f16 ulp of a.
+template <int DT>
+__device__ __forceinline__ bool peak_form_scale(float s) {
+  if (!(s >= kFltMin) || !__builtin_isfinite(s)) return false;
+  if (s == kFltMin) return true;
+  float a;
+  if constexpr (DT == XGEN_DTYPE_BF16) a = Half2<DT>::lo(pack_bf16x2(s * kE4M3Max, 0.0f) & 0xffffu);
+  else a = (float)(_Float16)(s * kE4M3Max);
+  return __builtin_isfinite(a) && fp8_row_params(a).s == s;
+}
+
+// q[i] = e4m3(clamp(x[i] / scale[0])) over a contiguous tensor.  For a scale of
+// the per-tensor kernel's form the division takes the row quantizers' two
+// operations, whose e4m3 byte equals IEEE division's for every input value not
+// above the peak a behind the scale (the oracle's exhaustive check over all
+// (x, a) pairs); larger values give quotients above 448 either way, which the
+// clamp maps to 448.  Any other scale, and chunks holding a NaN, use IEEE
+// division (NaN -> 0x7f).
 template <int DT>
 __global__ __launch_bounds__(kThreads) void fp8_pack_kernel(const uint8_t *__restrict__ x,
                                                             int64_t numel,
                                                             const float *__restrict__ scale,
                                                             uint8_t *__restrict__ q) {
-  // The scale may come from a caller (e.g. after a MAX all-reduce), so the
-  // quotient is not bounded by 448: IEEE division, NaN -> 0x7f, then clamp.
-  RowQuant p;
-  p.s = scale[0];
-  p.mul = 0.0f;
-  p.mul_lo = 0.0f;
-  p.finite = false;
+  const float s = scale[0];
+  const bool fast = peak_form_scale<DT>(s);
+  const RowQuant p = fp8_scale_params(s);
+  // a 16-bit magnitude above infinity's is a NaN
+  constexpr uint32_t kInfBits = DT == XGEN_DTYPE_BF16 ? 0x7f80u : 0x7c00u;
   const int64_t nchunks = numel >> 3;
   for (int64_t ci = (int64_t)blockIdx.x * kThreads + threadIdx.x; ci < nchunks;
        ci += (int64_t)gridDim.x * kThreads) {
     const u32x4 c = *reinterpret_cast<const u32x4 *>(x + ci * 16);
     float v[8];
     unpack8<DT>(c, v);
-    *reinterpret_cast<u32x2 *>(q + ci * 8) = quant8<XGEN_DTYPE_E4M3>(v, p);
+    u32x2 r;
+    if (fast && hmax_u16x2(absmax_chunk<DT>(c, u16x2{0, 0})) <= kInfBits) {
+      float qv[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qv[i] = clamp448(div_by_row_scale(v[i], p.mul, p.mul_lo));
+      r.x = pack_e4m3x4(qv[0], qv[1], qv[2], qv[3]);
+      r.y = pack_e4m3x4(qv[4], qv[5], qv[6], qv[7]);
+    } else {
+      uint32_t b[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) b[i] = e4m3_slow_byte(v[i], s);
+      r.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+      r.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+    }
+    *reinterpret_cast<u32x2 *>(q + ci * 8) = r;
   }
   if (blockIdx.x == 0) {
     const uint16_t *xs = reinterpret_cast<const uint16_t *>(x);
     for (int64_t i = (nchunks << 3) + threadIdx.x; i < numel; i += kThreads) {
       const float v = Half2<DT>::lo(xs[i]);
-      q[i] = (uint8_t)e4m3_slow_byte(v, p.s);
+      q[i] = (uint8_t)e4m3_slow_byte(v, s);
     }
   }
 }

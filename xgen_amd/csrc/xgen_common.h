@@ -243,10 +243,10 @@ struct RowQuant {
   bool finite;   // FP8: scale finite (fast division valid)
 };
 
-__device__ __forceinline__ RowQuant fp8_row_params(float amax) {
+// The FP8 parameters of a finite scale s >= FLT_MIN (or of a non-finite one:
+// finite = false).
+__device__ __forceinline__ RowQuant fp8_scale_params(float s) {
   RowQuant p;
-  float s = amax / kE4M3Max;
-  s = (s < kFltMin) ? kFltMin : s;  // clamp_min keeps NaN
   p.s = canonical_nan(s);
   p.finite = __builtin_isfinite(s);
   // r = RN(1/s) is a positive normal for a finite s >= FLT_MIN; the residual
@@ -260,6 +260,12 @@ __device__ __forceinline__ RowQuant fp8_row_params(float amax) {
   p.mul = r;
   p.mul_lo = e * r;
   return p;
+}
+
+__device__ __forceinline__ RowQuant fp8_row_params(float amax) {
+  float s = amax / kE4M3Max;
+  s = (s < kFltMin) ? kFltMin : s;  // clamp_min keeps NaN
+  return fp8_scale_params(s);
 }
 
 __device__ __forceinline__ RowQuant i8_row_params(float amax) {
