@@ -7,7 +7,7 @@
 //              LDS reads and multiplied by v_mfma_f32_32x32x16_bf16: exact
 //              products summed in fp32, the accumulation _scaled_mm's
 //              use_fast_accum=False asks for (h3_fp8.py:63-66), at twice the
-//              matrix-core time of the FP8 instructions
+//              matrix-core time of the FP8 instructions, plus the conversions
 //   INT8     : v_mfma_i32_32x32x32_i8      (int8 x int8 -> exact int32)
 //              replaces torch_npu.npu_quant_matmul at x_base/x_base/operator/matmul.py:63-64
 //
@@ -19,13 +19,12 @@
 //
 // out[m, n] = act(cvt(acc[m, n] * (sa[m] * sw[n]) + bias[n])),  acc = sum_k a[m,k] w[n,k]
 //
-// Tiling (FP8 and INT8): a 256x256 output tile per workgroup of 4 waves, one
-// per SIMD, each owning a 128x128 block (4x4 MFMA fragments, accumulators in
+// Tiling (every kind): a 256x256 output tile per workgroup of 4 waves, one per
+// SIMD, each owning a 128x128 block (4x4 MFMA fragments, accumulators in
 // AGPRs).  K advances in pairs of 64-byte sub-stages: bounds-checked buffer
 // loads on the LDS-DMA path (no VGPR staging; rows past M/N and the K tail
 // read as zero) move 128 bytes of K per row into a ring of two 64 KB pair
-// slots, one pair ahead, one barrier per pair.  The FP8-exact kind runs on an
-// 8-wave kernel (2 per SIMD, 128x64 each, 64-byte stages in a 4-slot ring).
+// slots, one pair ahead, one barrier per pair.
 //
 // The MFMA's A operand is the weight tile and its B operand the activation
 // tile, so each lane's accumulator column is one token and its 4 consecutive
@@ -34,7 +33,7 @@
 //
 // Workgroup -> tile mapping: the dispatcher places consecutive workgroup ids
 // on the 8 XCDs round-robin; ids are remapped so each XCD owns a contiguous
-// range of tiles, walked in groups of 4 or 8 tile-rows, so concurrently running
+// range of tiles, walked in groups of 8 tile-rows, so concurrently running
 // tiles on one XCD share activation rows and weight columns in its L2.
 #include "xgen_common.h"
 
@@ -43,49 +42,8 @@ namespace xgen {
 namespace {
 
 constexpr int BK = 64;  // K bytes per pipeline stage
-// instruction classes of __builtin_amdgcn_sched_group_barrier
-constexpr int kMfma = 0x008, kVmemRead = 0x020, kDsRead = 0x100;
-
-// Tiling of one kernel instance: a BM x BN output tile per workgroup of
-// WM x WN waves, a ring of STAGES LDS slots, WGS workgroups resident per CU.
-template <int BM_, int BN_, int WM_, int WN_, int STAGES_, int WGS_>
-struct Tiling {
-  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, kStages = STAGES_, kWgsPerCu = WGS_;
-  static constexpr int kWaves = WM * WN, kThreads = 64 * kWaves;
-  static constexpr int FM = BM / WM / 32;  // activation (token) fragments per wave
-  static constexpr int FN = BN / WN / 32;  // weight (feature) fragments per wave
-  static constexpr int kTileA = BM * BK, kTileW = BN * BK;  // operand tiles of one stage
-  static constexpr int kStageBytes = kTileA + kTileW;
-  // DMA: wave w fills rows [w * kRows*, (w + 1) * kRows*) of both tiles, 16 rows (1 KB) per load
-  static constexpr int kRowsA = BM / kWaves, kRowsW = BN / kWaves;
-  static constexpr int kLoadsA = kRowsA / 16, kLoadsW = kRowsW / 16;
-  static constexpr int kLoadsPerStage = kLoadsA + kLoadsW;  // per thread
-  // One parameter set: [sa f32 x BM][sw f32 x BN][bias f32 x BN].  The bias
-  // arrives as stored (bf16 / f16 / f32) at the start of its row and is
-  // converted to f32 in place in the epilogue.
-  static constexpr int kParamBytes = 4 * (BM + 2 * BN);
-  // A tile's parameters are loaded with its first stage, issued kStages stages
-  // ahead, and read in its epilogue; the set is reloaded kParamSets tiles later.
-  // With KT stages per tile that reload is issued after the epilogue when
-  // (kParamSets - 1) * KT >= kStages, for every KT >= 1.
-  static constexpr int kParamSets = kStages + 1;
-  static constexpr int kLdsBytes = kStages * kStageBytes + kParamSets * kParamBytes;
-  static_assert(kRowsA % 16 == 0 && kRowsW % 16 == 0, "DMA rows");
-  static_assert(kWaves >= 3, "the parameter loads use waves 0, 1 and 2");
-  static_assert(BM * 4 <= 1024 && BN * 4 <= 1024, "one DMA load per parameter row");
-  // load q of a stage is a weight load if ((q + 1) * kLoadsW) / L > (q * kLoadsW) / L:
-  // the two operands' loads interleave in proportion
-  static constexpr __device__ bool load_is_w(int q) {
-    return ((q + 1) * kLoadsW) / kLoadsPerStage > (q * kLoadsW) / kLoadsPerStage;
-  }
-  static constexpr __device__ int load_index(int q) {
-    return load_is_w(q) ? (q * kLoadsW) / kLoadsPerStage : q - (q * kLoadsW) / kLoadsPerStage;
-  }
-};
-
-// Production tiling: 256 x 256 tiles, 8 waves (2 per SIMD) of 128 x 64 each,
-// a 4-deep ring (148 KB of LDS), one workgroup per CU.
-typedef Tiling<256, 256, 2, 4, 4, 1> TileMain;
+// Output tiles of 256 x 256, one persistent workgroup per CU.
+constexpr int kTileM = 256, kTileN = 256;
 
 struct GemmArgs {
   const uint8_t *a;
@@ -117,18 +75,12 @@ struct GemmArgs {
   uint32_t residual_bytes, gate_bytes;  // (M - 1) * ld_residual * 2 + N * 2, (gate_rows - 1) * gate_stride * 2 + N * 2
 };
 
-// LDS layout of one operand tile of one stage: rows of 64 bytes (4 chunks
-// of 16 bytes).  Chunk c of row r is stored at chunk position c ^ ((r >> 2) & 3).
-// gfx950's LDS has 64 banks (256 bytes per cycle): the 16 lanes one 128-bit
-// access serves (rows r..r+15, one logical chunk) then hit 16 distinct 16-byte
-// bank groups.
-__device__ __forceinline__ int swz(int row, int chunk) {
-  return row * BK + ((chunk ^ ((row >> 2) & 3)) << 4);
-}
-
 // Operand kinds of the kernel template.
 enum Kind { kInt8 = 0, kFp8 = 1, kFp8Exact = 2 };
 
+// Operand traits per kind: accumulator and fragment types (one fragment = 32
+// rows of one 64-byte K step, as the fragment reads deliver them), MFMA steps per
+// 64-byte K step, 16-byte LDS reads per fragment, accumulator to float.
 template <int KIND>
 struct Mfma;
 
@@ -138,33 +90,17 @@ struct Mfma<kFp8> {
   typedef i32x8 frag_t;
   static constexpr int kSteps = BK / 64;  // 32x32x64: one step per stage
   static constexpr int kReads = 2;        // ds_read_b128 per fragment
-  static __device__ __forceinline__ frag_t load(const uint8_t *tile, int row, int ks, int lane) {
-    const int c0 = ks * 4 + (lane >> 5) * 2;
-    const u32x4 lo = *reinterpret_cast<const u32x4 *>(tile + swz(row, c0));
-    const u32x4 hi = *reinterpret_cast<const u32x4 *>(tile + swz(row, c0 + 1));
-    return frag_t{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-  }
-  static __device__ __forceinline__ acc_t mma(const frag_t &w, const frag_t &x, const acc_t &c) {
-    // cbsz = blgp = 0: both operands e4m3; zero scale operands: unscaled MFMA.
-    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w, x, c, 0, 0, 0, 0, 0, 0);
-  }
   static __device__ __forceinline__ float to_f32(float v) { return v; }
-  static constexpr int kMfmaPerMma = 1;
 };
 
-// e4m3fn bytes of one fragment (32 per lane, the FP8 kind's LDS reads) as four
-// 32x32x16 bf16 MFMAs: step s takes bytes 8s..8s+7 of each lane's 32, from both
-// operands alike, so every product pairs the same K index of the two.  The
-// conversion is exact (bf16 holds every e4m3fn value, subnormals included).
+// The exact kind reads the FP8 kind's fragments and multiplies them as bf16.
+// The conversion is exact (bf16 holds every e4m3fn value, subnormals included).
 template <>
 struct Mfma<kFp8Exact> {
   typedef f32x16 acc_t;
   typedef i32x8 frag_t;
   static constexpr int kSteps = 1;
   static constexpr int kReads = 2;
-  static __device__ __forceinline__ frag_t load(const uint8_t *tile, int row, int ks, int lane) {
-    return Mfma<kFp8>::load(tile, row, ks, lane);
-  }
   static __device__ __forceinline__ bf16x8 widen(int lo, int hi) {
     const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false);
     const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true);
@@ -172,20 +108,7 @@ struct Mfma<kFp8Exact> {
     const bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true);
     return bf16x8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
   }
-  // Each call converts its own copies: shared across the calls of a stage the
-  // converted weight fragments would stay live (32 more registers) and spill.
-  static __device__ __forceinline__ acc_t mma(const frag_t &w, const frag_t &x, const acc_t &c) {
-    acc_t r = c;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      int w0 = w[2 * s], w1 = w[2 * s + 1];
-      asm volatile("" : "+v"(w0), "+v"(w1));
-      r = __builtin_amdgcn_mfma_f32_32x32x16_bf16(widen(w0, w1), widen(x[2 * s], x[2 * s + 1]), r, 0, 0, 0);
-    }
-    return r;
-  }
   static __device__ __forceinline__ float to_f32(float v) { return v; }
-  static constexpr int kMfmaPerMma = 4;
 };
 
 template <>
@@ -194,16 +117,7 @@ struct Mfma<kInt8> {
   typedef i32x4 frag_t;
   static constexpr int kSteps = BK / 32;  // 32x32x32: two steps per stage
   static constexpr int kReads = 1;        // ds_read_b128 per fragment
-  static __device__ __forceinline__ frag_t load(const uint8_t *tile, int row, int ks, int lane) {
-    const int c = ks * 2 + (lane >> 5);
-    const u32x4 v = *reinterpret_cast<const u32x4 *>(tile + swz(row, c));
-    return frag_t{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
-  }
-  static __device__ __forceinline__ acc_t mma(const frag_t &w, const frag_t &x, const acc_t &c) {
-    return __builtin_amdgcn_mfma_i32_32x32x32_i8(w, x, c, 0, 0, 0);
-  }
   static __device__ __forceinline__ float to_f32(int v) { return (float)v; }
-  static constexpr int kMfmaPerMma = 1;
 };
 
 // One 16-byte-per-lane buffer load on the LDS-DMA path: lane l's 16 bytes land
@@ -255,13 +169,6 @@ __device__ __forceinline__ uint32_t pack_out(float a, float b) {
   else return pack_f16x2(a, b);
 }
 
-// Bias element n of a bf16 / f16 / f32 row, as float.
-__device__ __forceinline__ float bias_at(const uint8_t *bias, int dtype, int n) {
-  if (dtype == XGEN_DTYPE_F32) return reinterpret_cast<const float *>(bias)[n];
-  const uint16_t h = reinterpret_cast<const uint16_t *>(bias)[n];
-  return dtype == XGEN_DTYPE_BF16 ? Half2<XGEN_DTYPE_BF16>::lo(h) : Half2<XGEN_DTYPE_F16>::lo(h);
-}
-
 // Output tile -> (m0, n0): tiles are walked in groups of group_m tile-rows.
 template <int BM, int BN>
 __device__ __forceinline__ void tile_origin(int pid, int tiles_m, int tiles_n, int group_m, int &m0, int &n0) {
@@ -274,391 +181,26 @@ __device__ __forceinline__ void tile_origin(int pid, int tiles_m, int tiles_n, i
   n0 = (in_group / gm) * BN;
 }
 
-// Persistent kernel: C::kWgsPerCu workgroups per CU.  The tiles of XCD x
-// (workgroups x, x+8, ... run there) are the contiguous range [x*per_xcd,
-// (x+1)*per_xcd), dealt round-robin to that XCD's workgroups, so the tiles
-// running at once on one XCD are neighbours in its L2.  The stage sequence of
-// all of a workgroup's tiles is one stream: the DMA ring runs across tile
-// boundaries, so a tile's epilogue overlaps the loads of the next tile's first
-// stages.
-//
-// Epilogue.  gfx9 has a single in-order vector-memory counter, so a global
-// load in the epilogue would also wait for the DMA still in flight.  The
-// per-token scales, per-channel scales and bias of a tile therefore arrive in
-// LDS by the same DMA path, with the tile's first stage (kParamSets buffers,
-// indexed by tile), and are read with LDS loads.  Outputs are transposed
-// through the ring slot just consumed (free until the next barrier) so every
-// store writes full row segments.
-//
-// GATED: the bf16 output y feeds out = bf16(residual + bf16(y * gate[indices[m % seq]])).
-template <int KIND, int ACT, int OUT_DT, bool ACC_OUT, class C, bool GATED = false>
-__global__ __attribute__((amdgpu_flat_work_group_size(C::kThreads, C::kThreads),
-                          amdgpu_waves_per_eu(C::kWaves * C::kWgsPerCu / 4, C::kWaves * C::kWgsPerCu / 4)))
-void gemm_w8a8_kernel(GemmArgs p) {
-  typedef Mfma<KIND> T;
-  constexpr int BM = C::BM, BN = C::BN, WM = C::WM, WN = C::WN, kStages = C::kStages;
-  constexpr int kWaves = C::kWaves, FM = C::FM, FN = C::FN;
-  constexpr int kLoadsPerStage = C::kLoadsPerStage;
-  constexpr int kStageBytes = C::kStageBytes, kParamBytes = C::kParamBytes;
-  // epilogue transpose: one 32-row block of the wave's outputs, kRowBytes per row
-  constexpr int kRowBytes = FN * 32 * 2;
-  constexpr int kRowsPerLine = 256 / kRowBytes;      // rows sharing one 256-byte line of banks
-  constexpr int kChunks8 = kRowBytes / 8;            // 8-byte chunks per row
-  constexpr int kLanesPerRow = kRowBytes / 16;       // 16-byte chunks per row
-  constexpr int kRowsPerRead = 64 / kLanesPerRow;    // rows per 16-byte-per-lane read
-  static_assert((kRowBytes == 128 || kRowBytes == 256) && kWaves * 32 * kRowBytes <= kStageBytes,
-                "epilogue transpose layout");
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[C::kLdsBytes];
-
-  // --- this workgroup's tiles ------------------------------------------------
-  const int ntiles = p.tiles_m * p.tiles_n;
-  const int xcd = blockIdx.x & 7, local = blockIdx.x >> 3, wgs_per_xcd = gridDim.x >> 3;
-  const int t_first = xcd * p.per_xcd + local;
-  const int t_end = min((xcd + 1) * p.per_xcd, ntiles);
-  const int n_my = t_first < t_end ? (t_end - t_first + wgs_per_xcd - 1) / wgs_per_xcd : 0;
-  const int KT = (p.K + BK - 1) / BK;
-  const int G = n_my * KT;  // stages of all my tiles
-  if (G == 0) return;
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave % WM, wn = wave / WM;
-
-  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint8_t *>(p.a), (short)0, (int)p.a_bytes, kBufferFlags);
-  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint8_t *>(p.w), (short)0, (int)p.w_bytes, kBufferFlags);
-  const int bias_elem = p.bias_dtype == XGEN_DTYPE_F32 ? 4 : 2;
-  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float *>(p.sa), (short)0, p.M * 4, kBufferFlags);
-  const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float *>(p.sw), (short)0, p.N * 4, kBufferFlags);
-  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<void *>(p.bias), (short)0, p.bias ? p.N * bias_elem : 0, kBufferFlags);
-  // per-tensor scales (stride 0): one uniform value each
-  const float sa0 = p.sa_stride ? 0.0f : p.sa[0];
-  const float sw0 = p.sw_stride ? 0.0f : p.sw[0];
-
-  // --- global -> LDS DMA ------------------------------------------------------
-  // A 16-byte DMA load writes LDS at (wave base + lane * 16), so one wave-load
-  // fills 1 KB = 16 rows x 64 bytes.  Lane l lands on row base + (l >> 2),
-  // physical chunk l & 3, i.e. logical chunk (l & 3) ^ ((row >> 2) & 3) =
-  // (l & 3) ^ ((l >> 4) & 3), fetched from global.
-  const int dma_chunk = (lane & 3) ^ ((lane >> 4) & 3);
-  // Byte offsets of this lane's first A and W rows in my current tile; load l
-  // adds l * 16 rows.  Rows past M (N) need no test: their offsets lie past the
-  // end of the buffer resource (the host checks they fit in 32 bits), where
-  // the buffer loads read zeros.
-  uint32_t offa = 0, offw = 0;
-  int dma_m0 = 0, dma_n0 = 0;
-  auto set_dma_tile = [&](int i) {
-    tile_origin<BM, BN>(t_first + i * wgs_per_xcd, p.tiles_m, p.tiles_n, p.group_m, dma_m0, dma_n0);
-    offa = (uint32_t)(dma_m0 + wave * C::kRowsA + (lane >> 2)) * (uint32_t)p.lda + dma_chunk * 16;
-    offw = (uint32_t)(dma_n0 + wave * C::kRowsW + (lane >> 2)) * (uint32_t)p.ldw + dma_chunk * 16;
-  };
-  // The load stream: the next stage to load is issue_g (slot issue_g %
-  // kStages), stage issue_kt of my tile issue_i.  Past my last stage the
-  // stream goes on with stages whose loads are all out of range: they write
-  // zeros into slots nothing reads, which keeps the stream free of branches.
-  int issue_g = 0, issue_kt = 0, issue_i = 0;
-  auto issue_params = [&]() {  // a tile's epilogue parameters ride with its first stage
-    if (issue_kt != 0 || issue_g >= G) return;
-    uint8_t *prm = smem + kStages * kStageBytes + (issue_i % C::kParamSets) * kParamBytes;
-    // lanes past a row's bytes stay idle (their 16 bytes would land in the next row)
-    if (wave == 0 && p.sa_stride && lane * 16 < BM * 4)
-      dma_load16(rsa, prm, (uint32_t)dma_m0 * 4 + lane * 16);
-    if (wave == 1 && p.sw_stride && lane * 16 < BN * 4)
-      dma_load16(rsw, prm + BM * 4, (uint32_t)dma_n0 * 4 + lane * 16);
-    if (wave == 2 && p.bias && lane * 16 < BN * bias_elem)
-      dma_load16(rb, prm + (BM + BN) * 4, (uint32_t)(dma_n0 * bias_elem) + lane * 16);
-  };
-  // operand load q (0 .. kLoadsPerStage-1) of stage issue_g
-  struct Issue {
-    uint8_t *base;
-    uint32_t oa, ow;  // this stage's offsets of load 0, or out of range
-  };
-  auto issue_setup = [&]() {
-    const int k0 = issue_kt * BK;
-    // K tail and the stages past my last: out of range -> zeros
-    const bool kin = issue_g < G && k0 + dma_chunk * 16 < p.K;
-    uint32_t oa = kin ? offa + k0 : kOutOfRange, ow = kin ? offw + k0 : kOutOfRange;
-    // opaque to the optimizer, so the offsets of loads 1.. are formed per stage
-    // (one add each) rather than hoisted out of the loop into registers
-    asm volatile("" : "+v"(oa), "+v"(ow));
-    return Issue{smem + (issue_g % kStages) * kStageBytes, oa, ow};
-  };
-  // (kOutOfRange + l * 16 * ld stays out of range: the host keeps (M + 512) * lda below 2^32.)
-  auto issue_load = [&](const Issue &is, int q) {
-    const int l = C::load_index(q);
-    if (C::load_is_w(q))
-      dma_load16(rw, is.base + C::kTileA + (wave * C::kRowsW + l * 16) * BK, is.ow + (uint32_t)(l * 16 * p.ldw));
-    else
-      dma_load16(ra, is.base + (wave * C::kRowsA + l * 16) * BK, is.oa + (uint32_t)(l * 16 * p.lda));
-  };
-  auto issue_advance = [&]() {
-    ++issue_g;
-    if (++issue_kt == KT) {
-      issue_kt = 0;
-      if (++issue_i < n_my) set_dma_tile(issue_i);
-    }
-  };
-  auto issue_next = [&]() {  // a whole stage at once (prologue)
-    issue_params();
-    const Issue is = issue_setup();
-#pragma unroll
-    for (int q = 0; q < kLoadsPerStage; ++q) issue_load(is, q);
-    issue_advance();
-  };
-
-  typedef typename T::frag_t frag_t;
-  const int row_x = wm * (BM / WM) + (lane & 31);
-  const int row_w = wn * (BN / WN) + (lane & 31);
-  auto slot_of = [&](int stage) { return smem + (stage % kStages) * kStageBytes; };
-  // this thread's loads of stage h (and of the parameter row issued with it)
-  // are done once at most the loads of the stages issued after it remain
-  // outstanding (the parameter loads only make the count conservative)
-  auto wait_stage = [&](int h) {
-    const int later = issue_g - 1 - h;
-    if (later >= 2) wait_vmcnt<2 * kLoadsPerStage>();
-    else if (later == 1) wait_vmcnt<kLoadsPerStage>();
-    else wait_vmcnt<0>();
-  };
-
-  typename T::acc_t acc[FN][FM];
-#pragma unroll
-  for (int i = 0; i < FN; ++i)
-#pragma unroll
-    for (int j = 0; j < FM; ++j) acc[i][j] = typename T::acc_t{};
-
-  int tile_i = 0, kt = 0;
-  // Operand fragments in registers: xf = activation fragments of the stage
-  // being multiplied; wf[c] = weight fragments of it, wf[c ^ 1] = those of the
-  // next stage.  Each activation fragment is refilled with the next stage's
-  // as soon as its last MFMA has been issued, so the LDS reads of stage g+1
-  // overlap the MFMAs of stage g within 64 fragment registers.
-  frag_t xf[T::kSteps][FM], wf[2][T::kSteps][FN];
-
-  // One stage.  The barrier at the top publishes every wave's DMA of stage
-  // g+1 and retires every wave's reads of slot g % kStages, which then takes
-  // the DMA of stage g + kStages.  (Past the last stage the reads of "stage
-  // g+1" fetch stale LDS that nothing uses.)
-  auto stage = [&](int g, int c) {
-    wait_stage(g + 1);
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): my reads of slot g are done
-    lds_barrier();
-    issue_params();
-    const Issue is = issue_setup();
-    const uint8_t *nx = slot_of(g + 1), *nw = nx + C::kTileA;
-#pragma unroll
-    for (int ks = 0; ks < T::kSteps; ++ks)
-#pragma unroll
-      for (int f = 0; f < FN; ++f) wf[c ^ 1][ks][f] = T::load(nw, row_w + f * 32, ks, lane);
-    // The operand loads of stage g + kStages are spread over the MFMAs: issued
-    // together, the workgroup's loads queue up in the address unit, and a wave
-    // whose load waits there cannot issue its MFMAs either.  Slot s (one
-    // activation fragment's MFMAs) issues loads [first(s), first(s + 1)).
-    constexpr int kSlots = T::kSteps * FM;
-    auto first = [](int s) { return (s * kLoadsPerStage + kSlots - 1) / kSlots; };
-#pragma unroll
-    for (int ks = 0; ks < T::kSteps; ++ks)
-#pragma unroll
-      for (int j = 0; j < FM; ++j) {
-#pragma unroll
-        for (int i = 0; i < FN; ++i) acc[i][j] = T::mma(wf[c][ks][i], xf[ks][j], acc[i][j]);
-        xf[ks][j] = T::load(nx, row_x + j * 32, ks, lane);
-        const int slot = ks * FM + j;
-#pragma unroll
-        for (int q = first(slot); q < first(slot + 1); ++q) issue_load(is, q);
-      }
-    // Keep that order in the schedule: the weight reads, then per activation
-    // fragment its MFMAs, its refill and its share of the loads.  (Left alone
-    // the scheduler issues most MFMAs first and the reads of the next stage
-    // too late.)
-    __builtin_amdgcn_sched_group_barrier(kDsRead, T::kReads * T::kSteps * FN, 0);
-#pragma unroll
-    for (int k = 0; k < kSlots; ++k) {
-      __builtin_amdgcn_sched_group_barrier(kMfma, FN * T::kMfmaPerMma, 0);
-      __builtin_amdgcn_sched_group_barrier(kDsRead, T::kReads, 0);
-#pragma unroll
-      for (int q = first(k); q < first(k + 1); ++q) __builtin_amdgcn_sched_group_barrier(kVmemRead, 1, 0);
-    }
-    issue_advance();
-    if (++kt < KT) return;
-
-    // --- epilogue of my tile tile_i -------------------------------------------
-    // acc[i][j] element e: feature n = n0 + wn*(BN/WN) + i*32 + (e/4)*8 + (lane/32)*4 + e%4,
-    //                      token   m = m0 + wm*(BM/WM) + j*32 + lane%32.
-    int m0, n0;
-    tile_origin<BM, BN>(t_first + tile_i * wgs_per_xcd, p.tiles_m, p.tiles_n, p.group_m, m0, n0);
-    // The lane index, opaque to the optimizer: the epilogue's LDS addresses are
-    // formed here, not hoisted out of the stage loop into registers it needs.
-    int el = lane;
-    asm volatile("" : "+v"(el));
-    uint8_t *prm = smem + kStages * kStageBytes + (tile_i % C::kParamSets) * kParamBytes;
-    float *psa = reinterpret_cast<float *>(prm);
-    float *psw = reinterpret_cast<float *>(prm + BM * 4);
-    float *pbf = reinterpret_cast<float *>(prm + (BM + BN) * 4);
-    // The bias as stored, read before the barrier that precedes its in-place
-    // conversion to f32 (the parameter DMA completed stages ago).
-    float bias_v[(BN + C::kThreads - 1) / C::kThreads];
-#pragma unroll
-    for (int u = 0; u * C::kThreads < BN; ++u) {
-      const int t = tid + u * C::kThreads;
-      bias_v[u] = p.bias && t < BN ? bias_at(reinterpret_cast<const uint8_t *>(pbf), p.bias_dtype, t) : 0.0f;
-    }
-    // The transpose area: this wave's 32 rows of slot (g+1) % kStages, whose
-    // fragments every wave must have read first.  Its next DMA is issued after
-    // the barrier of stage g+1.
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-    lds_barrier();
-    // Parameters as float rows: per-tensor scales broadcast, bias converted
-    // (zeros without one), so the loops below read them without branches.
-#pragma unroll
-    for (int u = 0; u * C::kThreads < BM; ++u) {
-      const int t = tid + u * C::kThreads;
-      if (!p.sa_stride && t < BM) psa[t] = sa0;
-    }
-#pragma unroll
-    for (int u = 0; u * C::kThreads < BN; ++u) {
-      const int t = tid + u * C::kThreads;
-      if (t < BN) {
-        if (!p.sw_stride) psw[t] = sw0;
-        pbf[t] = bias_v[u];
-      }
-    }
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    lds_barrier();
-    uint8_t *xb = smem + ((g + 1) % kStages) * kStageBytes + wave * 32 * kRowBytes;
-#pragma unroll
-    for (int j = 0; j < FM; ++j) {
-      const int ml = wm * (BM / WM) + j * 32 + (el & 31);
-      const float sam = psa[ml];
-      const int wrow = el & 31;
-#pragma unroll
-      for (int i = 0; i < FN; ++i)
-#pragma unroll
-        for (int gq = 0; gq < 4; ++gq) {
-          const int nl = wn * (BN / WN) + i * 32 + gq * 8 + (el >> 5) * 4;
-          const f32x4 sw4 = *reinterpret_cast<const f32x4 *>(psw + nl);
-          const f32x4 b4 = *reinterpret_cast<const f32x4 *>(pbf + nl);
-          const float swv[4] = {sw4.x, sw4.y, sw4.z, sw4.w}, bv[4] = {b4.x, b4.y, b4.z, b4.w};
-          float y[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float a = T::to_f32(acc[i][j][gq * 4 + e]);
-            y[e] = __builtin_fmaf(a, sam * swv[e], bv[e]);
-            if constexpr (ACT == XGEN_ACT_GELU_TANH) y[e] = gelu_tanh(round_out<OUT_DT>(y[e]));
-          }
-          // row wrow, 8-byte chunk c8 (4 outputs) of the wave's row, XOR-swizzled
-          // by the row's index among the rows of its bank line: conflict-free
-          // 64-bit writes
-          const int c8 = i * 8 + gq * 2 + (el >> 5);
-          *reinterpret_cast<u32x2 *>(xb + wrow * kRowBytes + ((c8 ^ ((wrow / kRowsPerLine) & (kChunks8 - 1))) << 3)) =
-              u32x2{pack_out<OUT_DT>(y[0], y[1]), pack_out<OUT_DT>(y[2], y[3])};
-          if constexpr (ACC_OUT) {
-            const int m = m0 + ml, n = n0 + nl;
-            if (m < p.M && n < p.N) {
-              if constexpr (KIND != kInt8) {
-                const f32x4 v = {acc[i][j][gq * 4 + 0], acc[i][j][gq * 4 + 1], acc[i][j][gq * 4 + 2],
-                                 acc[i][j][gq * 4 + 3]};
-                *reinterpret_cast<f32x4 *>(static_cast<float *>(p.acc_out) + (int64_t)m * p.N + n) = v;
-              } else {
-                const i32x4 v = {acc[i][j][gq * 4 + 0], acc[i][j][gq * 4 + 1], acc[i][j][gq * 4 + 2],
-                                 acc[i][j][gq * 4 + 3]};
-                *reinterpret_cast<i32x4 *>(static_cast<int32_t *>(p.acc_out) + (int64_t)m * p.N + n) = v;
-              }
-            }
-          }
-        }
-      // read back kRowsPerRead whole rows per instruction, 16 bytes per lane, and
-      // store them as full row segments (LDS operations of a wave complete in order)
-#pragma unroll
-      for (int q = 0; q < 32 / kRowsPerRead; ++q) {
-        const int row = q * kRowsPerRead + el / kLanesPerRow, c16 = el % kLanesPerRow;
-        const int sw4 = (row / kRowsPerLine) & (kChunks8 - 1);
-        u32x4 v = *reinterpret_cast<const u32x4 *>(xb + row * kRowBytes + ((c16 ^ (sw4 >> 1)) << 4));
-        if (sw4 & 1) v = u32x4{v.z, v.w, v.x, v.y};
-        const int m = m0 + wm * (BM / WM) + j * 32 + row;
-        const int n = n0 + wn * (BN / WN) + c16 * 8;
-        if (m < p.M && n < p.N) {
-          if constexpr (GATED) {
-            const int64_t gi = p.indices[(uint32_t)m % p.seq];
-            if (gi >= 0 && gi < p.gate_rows) {
-              const u32x4 r = *reinterpret_cast<const u32x4 *>(p.residual + ((int64_t)m * p.ld_residual + n) * 2);
-              const u32x4 t = *reinterpret_cast<const u32x4 *>(p.gate + (gi * p.gate_stride + n) * 2);
-              v = gate_residual8(r, v, t);
-            } else {
-              v = u32x4{0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};  // index outside the table: NaN
-            }
-          }
-          *reinterpret_cast<u32x4 *>(static_cast<uint16_t *>(p.out) + (int64_t)m * p.ldo + n) = v;
-        }
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < FN; ++i)
-#pragma unroll
-      for (int j = 0; j < FM; ++j) acc[i][j] = typename T::acc_t{};
-    kt = 0;
-    ++tile_i;
-  };
-
-  set_dma_tile(0);
-#pragma unroll
-  for (int s = 0; s < kStages - 1; ++s) issue_next();
-  wait_stage(0);
-  lds_barrier();
-  issue_next();
-  {
-    const uint8_t *sx = slot_of(0), *sw = sx + C::kTileA;
-#pragma unroll
-    for (int ks = 0; ks < T::kSteps; ++ks) {
-#pragma unroll
-      for (int f = 0; f < FN; ++f) wf[0][ks][f] = T::load(sw, row_w + f * 32, ks, lane);
-#pragma unroll
-      for (int f = 0; f < FM; ++f) xf[ks][f] = T::load(sx, row_x + f * 32, ks, lane);
-    }
-  }
-  // two stages per trip so the weight-fragment buffers alternate without copies
-  for (int g = 0; g < G; g += 2) {
-    stage(g, 0);
-    if (g + 1 < G) stage(g + 1, 1);
-  }
-  // the loads of the stages past my last may still be writing LDS
-  wait_vmcnt<0>();
-}
-
-// C::kWgsPerCu persistent workgroups per CU (a multiple of the 8 XCDs), never
-// more than the tiles need
-template <class C>
+// One persistent workgroup per CU (a multiple of the 8 XCDs), never more than
+// the tiles need.  The tiles of XCD x (workgroups x, x+8, ... run there) are the
+// contiguous range [x*per_xcd, (x+1)*per_xcd), dealt round-robin to that XCD's
+// workgroups, so the tiles running at once on one XCD are neighbours in its L2.
 dim3 gemm_grid(const GemmArgs &a) {
   const int ntiles = a.tiles_m * a.tiles_n;
-  int wgs = device_cu_count() * C::kWgsPerCu / 8 * 8;
+  int wgs = device_cu_count() / 8 * 8;
   const int need = ((ntiles + 7) / 8) * 8;
   if (wgs > need) wgs = need;
   if (wgs < 8) wgs = 8;
   return dim3((unsigned)wgs);
 }
 
-template <int KIND, int ACT, int OUT_DT, class C>
-void launch_gemm(const GemmArgs &a, bool acc_out, hipStream_t stream) {
-  const dim3 grid = gemm_grid<C>(a), block(C::kThreads);
-  if (acc_out) gemm_w8a8_kernel<KIND, ACT, OUT_DT, true, C><<<grid, block, 0, stream>>>(a);
-  else gemm_w8a8_kernel<KIND, ACT, OUT_DT, false, C><<<grid, block, 0, stream>>>(a);
-}
-
-template <int KIND, class C>
-void launch_gemm_gated(const GemmArgs &a, hipStream_t stream) {
-  gemm_w8a8_kernel<KIND, XGEN_ACT_NONE, XGEN_DTYPE_BF16, false, C, true>
-      <<<gemm_grid<C>(a), dim3(C::kThreads), 0, stream>>>(a);
-}
-
 // ---------------------------------------------------------------------------
-// FP8 / INT8 kernel with one wave per SIMD.  Four waves (2 x 2) share a
-// 256 x 256 output tile; each wave owns a 128 x 128 block, 4 x 4 MFMA
-// fragments whose 256 accumulators live in AGPRs, and issues 16 MFMAs (FP8;
-// 32 for INT8) per 64-byte K stage from its own instruction stream, so the
-// stage's barrier syncs four waves and the LDS read traffic is 1 KB per
-// MFMA (two waves per SIMD at 128 x 64 read 1.5 KB).
+// The kernel: one wave per SIMD.  Four waves (2 x 2) share a 256 x 256 output
+// tile; each wave owns a 128 x 128 block, 4 x 4 MFMA fragments whose 256
+// accumulators live in AGPRs, and issues 16 MFMAs (FP8; 32 for INT8, 64 bf16
+// ones for the exact kind) per 64-byte K stage from its own instruction stream,
+// so the stage's barrier syncs four waves and the LDS read traffic is 1 KB per
+// 64 K of a 32 x 32 block (two waves per SIMD at 128 x 64 read 1.5 KB).
 // ---------------------------------------------------------------------------
 namespace w4 {
 constexpr int kWaves = 4, kThreads = 256;
@@ -724,6 +266,40 @@ struct MfmaA<kInt8> {
   static __device__ __forceinline__ void mma0(i32x16 &c, const i32x4 &w, const i32x4 &x) {
     asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, 0" : "=a"(c) : "v"(w), "v"(x));
   }
+};
+// The exact kind: e4m3fn fragments in the FP8 kind's layout, widened to bf16
+// (exact for every code) and multiplied by four 32x32x16 bf16 MFMAs, step s on
+// bytes 8s..8s+7 of each lane's 32 from both operands, so every product pairs
+// the same K index.  The activation fragment is widened once per block row
+// (widen_x) and reused by its blocks; the weight fragment per call.
+template <>
+struct MfmaA<kFp8Exact> {
+  struct xw_t {
+    bf16x8 s[4];
+  };
+  static __device__ __forceinline__ xw_t widen_x(const i32x8 &x) {
+    xw_t r;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) r.s[k] = Mfma<kFp8Exact>::widen(x[2 * k], x[2 * k + 1]);
+    return r;
+  }
+  template <bool ZERO>
+  static __device__ __forceinline__ void run(f32x16 &c, const i32x8 &w, const xw_t &xb) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const bf16x8 wb = Mfma<kFp8Exact>::widen(w[2 * k], w[2 * k + 1]);
+      // the operands were just written by VALU conversions: 2 wait states before
+      // an MFMA reads them (the compiler cannot see the MFMA inside the assembly)
+      if (ZERO && k == 0)
+        asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=a"(c) : "v"(wb), "v"(xb.s[k]));
+      else
+        asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(wb), "v"(xb.s[k]));
+    }
+  }
+  static __device__ __forceinline__ void mma(f32x16 &c, const i32x8 &w, const xw_t &xb) { run<false>(c, w, xb); }
+  static __device__ __forceinline__ void mma0(f32x16 &c, const i32x8 &w, const xw_t &xb) { run<true>(c, w, xb); }
+  static __device__ __forceinline__ void mma(f32x16 &c, const i32x8 &w, const i32x8 &x) { run<false>(c, w, widen_x(x)); }
+  static __device__ __forceinline__ void mma0(f32x16 &c, const i32x8 &w, const i32x8 &x) { run<true>(c, w, widen_x(x)); }
 };
 // 24 wait states after the last MFMAs before any accumulator is read by VALU
 // (16-pass MFMAs need 18 on gfx950).  Every accumulator is an operand, so no
@@ -1098,11 +674,18 @@ void gemm_w4_kernel(GemmArgs p) {
     // The MFMAs are volatile asm statements, so the loads written between them
     // stay in this order: per MFMA, its share of the next stage's fragment
     // reads (weights first) and of the DMA loads.
+    [[maybe_unused]] typename std::conditional<KIND == kFp8Exact, MfmaA<kFp8Exact>::xw_t, int>::type xw{};
 #pragma unroll
     for (int s = 0; s < kMfmas; ++s) {
       const int ks = s / (FM * FN), j = (s / FN) % FM, i = s % FN;
-      if (fresh && ks == 0) MfmaA<KIND>::mma0(acc[i][j], wf[cb][ks][i], xf[cb][ks][j]);
-      else MfmaA<KIND>::mma(acc[i][j], wf[cb][ks][i], xf[cb][ks][j]);
+      if constexpr (KIND == kFp8Exact) {
+        if (i == 0) xw = MfmaA<KIND>::widen_x(xf[cb][ks][j]);
+        if (fresh && ks == 0) MfmaA<KIND>::mma0(acc[i][j], wf[cb][ks][i], xw);
+        else MfmaA<KIND>::mma(acc[i][j], wf[cb][ks][i], xw);
+      } else {
+        if (fresh && ks == 0) MfmaA<KIND>::mma0(acc[i][j], wf[cb][ks][i], xf[cb][ks][j]);
+        else MfmaA<KIND>::mma(acc[i][j], wf[cb][ks][i], xf[cb][ks][j]);
+      }
       if constexpr (read) {
 #pragma unroll
         for (int r = spread_first(s, kReads / T::kReads, kMfmas); r < spread_first(s + 1, kReads / T::kReads, kMfmas); ++r) {
@@ -1210,7 +793,7 @@ void gemm_w4_kernel(GemmArgs p) {
 
 template <int KIND, int ACT, int OUT_DT>
 void launch_gemm_w4(const GemmArgs &a, bool acc_out, hipStream_t stream) {
-  const dim3 grid = gemm_grid<TileMain>(a), block(w4::kThreads);
+  const dim3 grid = gemm_grid(a), block(w4::kThreads);
   if (acc_out) gemm_w4_kernel<KIND, ACT, OUT_DT, true, false><<<grid, block, 0, stream>>>(a);
   else gemm_w4_kernel<KIND, ACT, OUT_DT, false, false><<<grid, block, 0, stream>>>(a);
 }
@@ -1218,7 +801,7 @@ void launch_gemm_w4(const GemmArgs &a, bool acc_out, hipStream_t stream) {
 template <int KIND>
 void launch_gemm_w4_gated(const GemmArgs &a, hipStream_t stream) {
   gemm_w4_kernel<KIND, XGEN_ACT_NONE, XGEN_DTYPE_BF16, false, true>
-      <<<gemm_grid<TileMain>(a), dim3(w4::kThreads), 0, stream>>>(a);
+      <<<gemm_grid(a), dim3(w4::kThreads), 0, stream>>>(a);
 }
 
 struct GateParams {  // the gated residual epilogue's inputs (null residual: plain GEMM)
@@ -1296,16 +879,13 @@ int gemm_entry(const char *fn, const void *a, int64_t lda, const void *w, int64_
   g.out = out;
   g.ldo = ldo;
   g.acc_out = acc_out;
-  typedef TileMain C;
-  g.tiles_m = (int)((M + C::BM - 1) / C::BM);
-  g.tiles_n = (int)((N + C::BN - 1) / C::BN);
+  g.tiles_m = (int)((M + kTileM - 1) / kTileM);
+  g.tiles_n = (int)((N + kTileN - 1) / kTileN);
   g.per_xcd = (g.tiles_m * g.tiles_n + 7) / 8;
-  // The 32 tiles one XCD runs at once span group_m tile-rows.  One wave per
-  // SIMD (FP8, INT8), measured at M=15,624: 8 rows beat 4 for QKV and FFN up by
-  // ~1% and tie for FFN down; 2 are 4-7% slower, 16 no better.  The 8-wave
-  // kernel (FP8-exact): 4 rows beat 8 for outputs of 24-63 tile-columns (QKV
-  // 0.9%, FFN up 2.8%), 8 beat 4 for FFN down's 12 (1.7%).
-  g.group_m = KIND != kFp8Exact || !(g.tiles_n >= 24 && g.tiles_n < 64) ? 8 : 4;
+  // The 32 tiles one XCD runs at once span group_m tile-rows; measured at
+  // M=15,624: 8 rows beat 4 for QKV and FFN up by ~1% and tie for FFN down; 2
+  // are 4-7% slower, 16 no better.
+  g.group_m = 8;
   g.a_bytes = (uint32_t)a_bytes;
   g.w_bytes = (uint32_t)w_bytes;
   g.residual = static_cast<const uint8_t *>(gp.residual);
@@ -1326,27 +906,14 @@ int gemm_entry(const char *fn, const void *a, int64_t lda, const void *w, int64_
     return fail(XGEN_ERR_UNSUPPORTED, "%s: output rows too long for 32-bit offsets", fn);
   g.out_bytes = (uint32_t)out_bytes;
   const bool with_acc = acc_out != nullptr;
-  if constexpr (KIND != kFp8Exact) {
-    // FP8 and INT8: the one-wave-per-SIMD kernel
-    if (gated) {
-      launch_gemm_w4_gated<KIND>(g, stream);
-    } else if (activation == XGEN_ACT_NONE) {
-      if (out_dtype == XGEN_DTYPE_BF16) launch_gemm_w4<KIND, XGEN_ACT_NONE, XGEN_DTYPE_BF16>(g, with_acc, stream);
-      else launch_gemm_w4<KIND, XGEN_ACT_NONE, XGEN_DTYPE_F16>(g, with_acc, stream);
-    } else {
-      if (out_dtype == XGEN_DTYPE_BF16) launch_gemm_w4<KIND, XGEN_ACT_GELU_TANH, XGEN_DTYPE_BF16>(g, with_acc, stream);
-      else launch_gemm_w4<KIND, XGEN_ACT_GELU_TANH, XGEN_DTYPE_F16>(g, with_acc, stream);
-    }
-    return launch_status(fn);
-  }
   if (gated) {
-    launch_gemm_gated<KIND, C>(g, stream);
+    launch_gemm_w4_gated<KIND>(g, stream);
   } else if (activation == XGEN_ACT_NONE) {
-    if (out_dtype == XGEN_DTYPE_BF16) launch_gemm<KIND, XGEN_ACT_NONE, XGEN_DTYPE_BF16, C>(g, with_acc, stream);
-    else launch_gemm<KIND, XGEN_ACT_NONE, XGEN_DTYPE_F16, C>(g, with_acc, stream);
+    if (out_dtype == XGEN_DTYPE_BF16) launch_gemm_w4<KIND, XGEN_ACT_NONE, XGEN_DTYPE_BF16>(g, with_acc, stream);
+    else launch_gemm_w4<KIND, XGEN_ACT_NONE, XGEN_DTYPE_F16>(g, with_acc, stream);
   } else {
-    if (out_dtype == XGEN_DTYPE_BF16) launch_gemm<KIND, XGEN_ACT_GELU_TANH, XGEN_DTYPE_BF16, C>(g, with_acc, stream);
-    else launch_gemm<KIND, XGEN_ACT_GELU_TANH, XGEN_DTYPE_F16, C>(g, with_acc, stream);
+    if (out_dtype == XGEN_DTYPE_BF16) launch_gemm_w4<KIND, XGEN_ACT_GELU_TANH, XGEN_DTYPE_BF16>(g, with_acc, stream);
+    else launch_gemm_w4<KIND, XGEN_ACT_GELU_TANH, XGEN_DTYPE_F16>(g, with_acc, stream);
   }
   return launch_status(fn);
 }
