@@ -907,7 +907,8 @@ int gemm_entry(const char *fn, const void *a, int64_t lda, const void *w, int64_
   g.out_bytes = (uint32_t)out_bytes;
   const bool with_acc = acc_out != nullptr;
   if (gated) {
-    launch_gemm_w4_gated<KIND>(g, stream);
+    // (the gated entry takes the FP8 and INT8 kinds only: no exact-kind instance)
+    if constexpr (KIND != kFp8Exact) launch_gemm_w4_gated<KIND>(g, stream);
   } else if (activation == XGEN_ACT_NONE) {
     if (out_dtype == XGEN_DTYPE_BF16) launch_gemm_w4<KIND, XGEN_ACT_NONE, XGEN_DTYPE_BF16>(g, with_acc, stream);
     else launch_gemm_w4<KIND, XGEN_ACT_NONE, XGEN_DTYPE_F16>(g, with_acc, stream);
