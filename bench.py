@@ -562,7 +562,7 @@ def main():
                    "M": M, "K": K, "N": Nf, "weight_scaling": "per-channel", "activation_scaling": "per-token"},
         "roofline": {"bound": "mfma", "achieved": gemm_tflops, "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
                      "frac": gemm_tflops / PEAK_FP8_TFLOPS, "traffic": QKV_GEMM_TRAFFIC_BYTES,
-                     "kernel": "gemm_w8a8_kernel<fp8> (QKV)", "flop_per_launch": flop},
+                     "kernel": "gemm_w4_kernel<fp8> (QKV)", "flop_per_launch": flop},
         "quant": {"gbs": quant_gbs, "frac_of_hbm": quant_gbs / PEAK_HBM_GBS},
         "kernels": kernels,
         "cpu_baseline": cpu,

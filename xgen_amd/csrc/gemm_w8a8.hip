@@ -341,7 +341,7 @@ void gemm_w4_kernel(GemmArgs p) {
   constexpr int kReads = T::kReads * KS * (FM + FN);   // ds_read_b128 per stage per wave
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kLdsBytes];
 
-  // --- this workgroup's tiles (as gemm_w8a8_kernel) ---------------------------
+  // --- this workgroup's tiles: a contiguous range per XCD, strided by workgroup ---
   const int ntiles = p.tiles_m * p.tiles_n;
   const int xcd = blockIdx.x & 7, local = blockIdx.x >> 3, wgs_per_xcd = gridDim.x >> 3;
   const int t_first = xcd * p.per_xcd + local;
@@ -375,8 +375,7 @@ void gemm_w4_kernel(GemmArgs p) {
   const __amdgpu_buffer_rsrc_t rgate = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t *>(p.gate), (short)0, GATED ? (int)p.gate_bytes : 0, kBufferFlags);
 
-  // --- global -> LDS DMA (layout as gemm_w8a8_kernel: chunk c of row r at
-  // c ^ ((r >> 2) & 3); wave w fills rows [64 w, 64 w + 64) of both tiles) ---
+  // --- global -> LDS DMA (wave w fills rows [64 w, 64 w + 64) of both tiles) ---
   // lane l fills row (l >> 3) of an 8-row load, physical chunk l & 7: logical
   // chunk (l & 7) ^ ((row >> 1) & 7), i.e. ^ (l >> 4) in even loads, ^ (4 | l >> 4) in odd
   const int ch_e = (lane & 7) ^ (lane >> 4), ch_o = (lane & 7) ^ (4 | (lane >> 4));
