@@ -20,7 +20,9 @@ Function -> reference -> how it is pinned (tests/test_oracle_*.py):
   abs_peak            h3_abs_peak.py:14-25   max is order-free; NaN propagates.
   layer/rms norm      hunyuan.py:359 (nn.LayerNorm, eps 1e-6), f2bc_kernel.asc:68-81
         float64 statistics; == torch.nn.functional.layer_norm within 1 bf16 ulp;
-        invariants (zero mean, unit variance of the fp64 result).
+        invariants (zero mean, unit variance of the fp64 result); RMSNorm bit-exact
+        against torch.nn.functional.rms_norm run in float64 (widths, eps, weight
+        dtypes, rows where eps dominates), scale invariance, unit mean square.
   modulate            h3_indexed_affine.py:22-28 / hunyuan.py:393
         eager bf16 torch expression == numpy restatement with explicit RNE
         rounding after each op, bit for bit.
