@@ -213,7 +213,7 @@ def median_runs(fn, min_runs=5, budget_s=3.0, max_runs=500):
 
 
 def cpu_baseline(x_qkv, qw_qkv, sw_qkv, b_qkv):
-    """The reported CPU baseline (BASELINE.md plan): the oracle's quantize-dequantize W8A8 linear
+    """The reported CPU baseline: the oracle's quantize-dequantize W8A8 linear
     on the host, all allowed threads.  C1 (x [256, 1024], W [1024, 1024], seed 0) in its FP8 and
     INT8 forms, then a bounded row sample of the QKV workload as a second figure."""
     import torch
