@@ -35,6 +35,7 @@
 // on the 8 XCDs round-robin; ids are remapped so each XCD owns a contiguous
 // range of tiles, walked in groups of 8 tile-rows, so concurrently running
 // tiles on one XCD share activation rows and weight columns in its L2.
+#include "fastdiv.h"
 #include "xgen_common.h"
 
 namespace xgen {
@@ -71,7 +72,7 @@ struct GemmArgs {
   int64_t gate_stride;  // elements
   int64_t gate_rows;
   const int64_t *indices;
-  uint32_t seq;
+  uint32_t seq, seq_magic, seq_shift;  // m % seq = m - ((mulhi(m, magic) + m) >> shift) * seq
   uint32_t residual_bytes, gate_bytes;  // (M - 1) * ld_residual * 2 + N * 2, (gate_rows - 1) * gate_stride * 2 + N * 2
 };
 
@@ -374,6 +375,10 @@ void gemm_w4_kernel(GemmArgs p) {
       const_cast<uint8_t *>(p.residual), (short)0, GATED ? (int)p.residual_bytes : 0, kBufferFlags);
   const __amdgpu_buffer_rsrc_t rgate = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t *>(p.gate), (short)0, GATED ? (int)p.gate_bytes : 0, kBufferFlags);
+  // the AdaLN indices, read through a buffer (counted by vmcnt only: a flat load
+  // would also hold every LDS wait of the epilogue until memory answers); seq < M < 2^28
+  const __amdgpu_buffer_rsrc_t rind = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int64_t *>(p.indices), (short)0, GATED ? (int)(p.seq * 8) : 0, kBufferFlags);
 
   // --- global -> LDS DMA (wave w fills rows [64 w, 64 w + 64) of both tiles) ---
   // lane l fills row (l >> 3) of an 8-row load, physical chunk l & 7: logical
@@ -481,12 +486,15 @@ void gemm_w4_kernel(GemmArgs p) {
     int pm = 0;          // the pending rows' first token (GATED)
     // GATED: each step reads the AdaLN indices of its 4 token rows (mrow + 8 q) before
     // its values are computed, and after its read-back issues the loads of its
-    // residual pieces, which its stores use during the next step; pgrow is the
-    // pending rows' gate-table row, kOutOfRange where the index lies outside it
+    // residual pieces, which its stores use during the next step.  The FP8 instance
+    // loads its gate pieces there too; the INT8 one reads them at the store (loading
+    // them ahead is 3% faster for FP8, and slower for INT8, whose registers then spill)
+    constexpr bool kGateAhead = KIND == kFp8;
     u32x2 gidx[4];
-    uint32_t pgrow[4];
-    u32x4 pres[4];
-    int pn = 0;  // this lane's first pending column
+    uint32_t pbad = 0;  // bit q: the pending row q's index lies outside the table
+    uint32_t pgrow[4];  // (gate read at the store) the pending rows' gate-table rows
+    u32x4 pres[4], pgate[4];
+    [[maybe_unused]] int pn = 0;  // this lane's first pending column (gate read at the store)
     // rows past M need no check: their offsets lie past the output's last byte, where the
     // buffer drops stores (the host keeps (M + 256) * ldo * 2 below 2^32)
     auto store_pending = [&]() {
@@ -494,13 +502,13 @@ void gemm_w4_kernel(GemmArgs p) {
       for (int q = 0; q < 4; ++q) {
         u32x4 v = prow[q];
         if constexpr (GATED) {
-          // (the gate rows are small and cache-resident: read here)
-          const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(
-              rgate, pcol && pgrow[q] != kOutOfRange ? (pgrow[q] * (uint32_t)p.gate_stride + (uint32_t)pn) * 2
-                                                      : kOutOfRange, 0, 0);
+          if constexpr (!kGateAhead)  // (the gate rows are small and cache-resident)
+            pgate[q] = __builtin_amdgcn_raw_buffer_load_b128(
+                rgate, pcol && !((pbad >> q) & 1u) ? (pgrow[q] * (uint32_t)p.gate_stride + (uint32_t)pn) * 2
+                                                   : kOutOfRange, 0, 0);
           if (pcol && pm + q * 8 < p.M)
-            v = pgrow[q] != kOutOfRange ? gate_residual8(pres[q], v, t)
-                                        : u32x4{0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};  // index outside the table: NaN
+            v = (pbad >> q) & 1u ? u32x4{0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u}  // index outside the table: NaN
+                                 : gate_residual8(pres[q], v, pgate[q]);
         }
         // non-temporal: the output streams past the caches the operands are re-read from
         // (measured: FFN down 4.7%, FFN up 2% faster; QKV unchanged)
@@ -568,7 +576,8 @@ void gemm_w4_kernel(GemmArgs p) {
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             const uint32_t m = (uint32_t)(m0 + wm * kWaveRows + j * 32 + rr + 8 * q);
-            gidx[q] = *reinterpret_cast<const u32x2 *>(p.indices + m % p.seq);
+            const uint32_t mq = (__umulhi(m, p.seq_magic) + m) >> p.seq_shift;
+            gidx[q] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rind, (m - mq * p.seq) * 8, 0, 0));
           }
         }
 #pragma unroll
@@ -623,13 +632,20 @@ void gemm_w4_kernel(GemmArgs p) {
         pn = ncol;
         if constexpr (GATED) {
           // (out-of-range rows and columns read zeros, and their stores are dropped)
+          pbad = 0;
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             const uint32_t m = (uint32_t)(mrow + 8 * q);
             // an int64 index in [0, gate_rows): high word 0, low word below gate_rows (< 2^31)
-            pgrow[q] = gidx[q].y == 0 && gidx[q].x < (uint32_t)p.gate_rows ? gidx[q].x : kOutOfRange;
+            const bool ok = gidx[q].y == 0 && gidx[q].x < (uint32_t)p.gate_rows;
+            pbad |= ok ? 0u : 1u << q;
             pres[q] = __builtin_amdgcn_raw_buffer_load_b128(
                 rres, pcol ? (m * (uint32_t)p.ld_residual + (uint32_t)ncol) * 2 : kOutOfRange, 0, 0);
+            if constexpr (kGateAhead)
+              pgate[q] = __builtin_amdgcn_raw_buffer_load_b128(
+                  rgate, pcol && ok ? (gidx[q].x * (uint32_t)p.gate_stride + (uint32_t)ncol) * 2 : kOutOfRange, 0, 0);
+            else
+              pgrow[q] = gidx[q].x;
           }
         }
       }
@@ -894,6 +910,11 @@ int gemm_entry(const char *fn, const void *a, int64_t lda, const void *w, int64_
   g.gate_rows = gp.gate_rows;
   g.indices = gp.indices;
   g.seq = (uint32_t)gp.seq;
+  if (gated) {
+    const FastDiv fd = make_fastdiv((uint32_t)gp.seq);
+    g.seq_magic = fd.m;
+    g.seq_shift = fd.l;
+  }
   g.residual_bytes = gated ? (uint32_t)(((M - 1) * gp.ld_residual + N) * 2) : 0;
   g.gate_bytes = gated ? (uint32_t)(((gp.gate_rows - 1) * gp.gate_stride + N) * 2) : 0;
   g.kt4 = (int)(((K + BK - 1) / BK + 3) / 4 * 4);
