@@ -115,3 +115,32 @@ def test_full_size_out_projection(cuda):
     m = H3FP8Linear(w, b, weight_scaling="channel", activation_scaling="token")
     fused = m.forward_gate_residual(x[None], residual, gate, idx)
     assert torch.equal(u16(fused), u16(gate_residual(residual, m(x[None]), gate, idx)))
+
+
+@pytest.mark.parametrize("kind", ["fp8", "int8"])
+def test_fused_epilogue_bad_indices(cuda, kind):
+    """Indices outside the gate table (negative, = T, a high word set) poison their rows in the
+    fused epilogue exactly as in the standalone op (NaN rows, bit for bit); other rows unchanged."""
+    B, S, K, Nf, T = 3, 100, 256, 96, 5
+    g = torch.Generator().manual_seed(17)
+    x, _ = workloads.activations(B * S, K, g)
+    w = (torch.randn((Nf, K), generator=g) * 0.02).to(torch.bfloat16)
+    b = (torch.randn((Nf,), generator=g) * 0.01).to(torch.bfloat16)
+    residual = torch.randn((B, S, Nf), generator=g).to(torch.bfloat16)
+    gate = (torch.randn((T, Nf), generator=g) * 0.5).to(torch.bfloat16)
+    idx = torch.randint(T, (S,), generator=g)
+    bad = [3, 40, 41, 99]
+    idx[3], idx[40], idx[41], idx[99] = -1, T, 1 << 40, -(1 << 40)
+    dt = torch.float8_e4m3fn if kind == "fp8" else torch.int8
+    qa, sa = xops.quantize_rows(x.to(cuda), dt)
+    qw, sw = xops.quantize_rows(w.to(cuda), dt)
+    fused = xops.scaled_mm_gate_residual(qa, qw, sa, sw, b.to(cuda), residual.reshape(-1, Nf).to(cuda),
+                                         gate.to(cuda), idx.to(cuda))
+    y, _ = xops.scaled_mm(qa, qw, sa, sw, b.to(cuda), torch.bfloat16, N.ACT_NONE, False)
+    twostep = xops.gate_residual(residual.to(cuda), y.reshape(B, S, Nf), gate.to(cuda), idx.to(cuda))
+    assert torch.equal(u16(fused), u16(twostep.reshape(-1, Nf)))
+    rows_bad = torch.zeros(S, dtype=torch.bool)
+    rows_bad[bad] = True
+    nan_rows = torch.isnan(fused.float().cpu()).reshape(B, S, Nf).all(dim=2)
+    assert torch.equal(nan_rows, rows_bad.expand(B, S))
+    assert not torch.isnan(fused.float().cpu()).reshape(B, S, Nf)[:, ~rows_bad].any()
