@@ -910,6 +910,7 @@ int gemm_entry(const char *fn, const void *a, int64_t lda, const void *w, int64_
   g.gate_rows = gp.gate_rows;
   g.indices = gp.indices;
   g.seq = (uint32_t)gp.seq;
+  g.seq_magic = g.seq_shift = 0;  // (read by the gated kernels only)
   if (gated) {
     const FastDiv fd = make_fastdiv((uint32_t)gp.seq);
     g.seq_magic = fd.m;
