@@ -121,20 +121,25 @@ def test_int8_gemm_accumulators_bit_exact(cuda, M, K, Nf):
     assert_within_rounding(out, ref, exact.abs().double(), sa, sw, bias)
 
 
-@pytest.mark.parametrize("kind", ["fp8", "int8"])
-@pytest.mark.parametrize("bias_dtype", [None, torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("kind", ["fp8", "fp8_exact", "int8"])
+@pytest.mark.parametrize("bias_dtype", [None, torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
 def test_epilogue_variants(cuda, kind, bias_dtype, out_dtype):
+    """Every epilogue branch: bias absent or of each dtype, bf16 / f16 output, per-token and
+    per-tensor activation scales against per-channel and per-tensor weight scales (stride 0 or 1
+    each), with and without GELU-tanh, for the three kinds."""
     M, K, Nf = 200, 512, 320
-    qa, sa, qw, sw, bias = quantized_operands(M, K, Nf, cuda, kind, seed=11)
+    exact = kind == "fp8_exact"
+    qa, sa, qw, sw, bias = quantized_operands(M, K, Nf, cuda, "int8" if kind == "int8" else "fp8", seed=11)
     bias = None if bias_dtype is None else bias.to(bias_dtype)
-    # per-tensor scales too (stride 0)
-    for sa_, sw_ in ((sa, sw), (sa[:1].clone(), sw[:1].clone())):
-        out, _ = xops.scaled_mm(qa, qw, sa_, sw_, bias, out_dtype, N.ACT_NONE, False)
-        fn = R.w8a8_linear_fp8 if kind == "fp8" else R.w8a8_linear_int8
-        ref = fn(qa.cpu(), sa_.cpu(), qw.cpu(), sw_.cpu(), None if bias is None else bias.cpu(), out_dtype)
-        assert out.dtype == out_dtype
-        check_close(out, ref)
+    fn = R.w8a8_linear_int8 if kind == "int8" else R.w8a8_linear_fp8
+    for sa_, sw_ in ((sa, sw), (sa[:1].clone(), sw[:1].clone()), (sa, sw[:1].clone()), (sa[:1].clone(), sw)):
+        for act, act_name in ((N.ACT_NONE, None), (N.ACT_GELU_TANH, "gelu_tanh")):
+            out, _ = xops.scaled_mm(qa, qw, sa_, sw_, bias, out_dtype, act, False, exact)
+            ref = fn(qa.cpu(), sa_.cpu(), qw.cpu(), sw_.cpu(), None if bias is None else bias.cpu(), out_dtype,
+                     act_name)
+            assert out.dtype == out_dtype
+            check_close(out, ref)
 
 
 @pytest.mark.parametrize("kind", ["fp8", "int8"])
