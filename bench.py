@@ -10,7 +10,8 @@ Inputs are resident in HBM; activations rotate over 4 buffers (384 MB) so the
 
 Also timed (HIP events on the launch stream, same process): the GEMM alone
 (roofline), the per-token quantizer alone, the fused LayerNorm + AdaLN
-modulate + FP8 quant front end, the FFN up (+GELU) / down GEMMs and the INT8
+modulate + FP8 quant front end, the FFN up (with and without the GELU-tanh
+epilogue) / down GEMMs, the FFN-down requant with and without the GELU, the INT8
 QKV and FFN-up GEMMs, the QKV GEMM with exact accumulation, and the reference's
 default per-tensor H3FP8Linear.  The CPU baseline is the oracle's
 quantize-dequantize linear on config C1 (FP8 and INT8) plus a bounded row
@@ -377,10 +378,14 @@ def main():
         qu, su = xops.quantize_rows(wu, fp8)
         qd, sd = xops.quantize_rows(wd, fp8)
         h, _ = xops.scaled_mm(qa0, qu, sa0, su, bu, torch.bfloat16, N.ACT_GELU_TANH, False)
+        hp, _ = xops.scaled_mm(qa0, qu, sa0, su, bu, torch.bfloat16, N.ACT_NONE, False)
         qh, sh = xops.quantize_rows(h, fp8)
         f_up = 2.0 * M * qu.shape[0] * K
         ms_up = timed(lambda: xops.scaled_mm(qa0, qu, sa0, su, bu, torch.bfloat16, N.ACT_GELU_TANH, False),
                       args.steps, args.warmup)
+        ms_up_plain = timed(lambda: xops.scaled_mm(qa0, qu, sa0, su, bu, torch.bfloat16, N.ACT_NONE, False),
+                            args.steps, args.warmup)
+        ms_rq_gelu = timed(lambda: xops.quantize_rows(hp, fp8, N.ACT_GELU_TANH), args.steps, args.warmup)
         ms_dn = timed(lambda: xops.scaled_mm(qh, qd, sh, sd, bd, torch.bfloat16, N.ACT_NONE, False),
                       args.steps, args.warmup)
         ms_rq = timed(lambda: xops.quantize_rows(h, fp8), args.steps, args.warmup)
@@ -390,7 +395,14 @@ def main():
                                         "frac_of_peak": f_up / (ms_dn * 1e-3) / 1e12 / PEAK_FP8_TFLOPS}
         rq_bytes = M * 4 * K * 3 + 4 * M
         kernels["requant_fp8_12288"] = {"ms": ms_rq, "gbs": rq_bytes / (ms_rq * 1e-3) / 1e9}
-        del wu, wd, qu, qd, h, qh
+        # the GELU-tanh between the FFN GEMMs: in the up-projection's epilogue, or in the
+        # down-projection's input quantization (same bytes and scales into the down GEMM)
+        kernels["gemm_fp8_ffn_up"] = {"ms": ms_up_plain, "tflops": f_up / (ms_up_plain * 1e-3) / 1e12,
+                                      "frac_of_peak": f_up / (ms_up_plain * 1e-3) / 1e12 / PEAK_FP8_TFLOPS}
+        kernels["requant_gelu_fp8_12288"] = {"ms": ms_rq_gelu, "gbs": rq_bytes / (ms_rq_gelu * 1e-3) / 1e9}
+        kernels["ffn_pair_fp8"] = {"gelu_in_up_epilogue_ms": ms_up + ms_rq + ms_dn,
+                                   "gelu_in_requant_ms": ms_up_plain + ms_rq_gelu + ms_dn}
+        del wu, wd, qu, qd, h, hp, qh
     if want("int8"):
         qai, sai = xops.quantize_rows(xs[0], torch.int8)
         qwi, swi = xops.quantize_rows(w, torch.int8)
@@ -499,7 +511,7 @@ def main():
                                      "frac_of_hbm": dec_bytes / (ms_dec * 1e-3) / 1e9 / PEAK_HBM_GBS,
                                      "bytes": dec_bytes}
 
-    # ---- C5 chain at a 10 s clip's share (M=31,248): front end -> QKV -> out -> up(+GELU) -> down
+    # ---- C5 chain at a 10 s clip's share (M=31,248): front end -> QKV -> out -> up -> GELU requant -> down
     if want("c5"):
         from xgen_amd.operator.dit_chain import DiTLinearChain
         M5 = W.M_10S
@@ -512,7 +524,7 @@ def main():
         chain_flop = 2.0 * M5 * K * (3 * K + K + 4 * K + 4 * K)
         qkv5, o5, h5, _ = chain(x5, sc5, sh5, idx5)
         qa5, sa5 = xops.quantize_rows(o5.reshape(M5, K), fp8)
-        qh5, sh5_ = xops.quantize_rows(h5.reshape(M5, 4 * K), fp8)
+        qh5, sh5_ = chain.ff_down.quantize_input(h5.reshape(M5, 4 * K))
         qv5, sv5 = xops.quantize_rows(qkv5.reshape(M5, 3 * K)[:, 2 * K:], fp8)
         stages = {"front_end": timed(lambda: xops.norm_affine_quant(x5, None, sc5, sh5, idx5, 1e-6, N.NORM_LAYER,
                                                                     fp8, False), args.steps, args.warmup)}
@@ -522,9 +534,9 @@ def main():
                                     args.steps, args.warmup)
         stages["out"] = timed(lambda: chain.out.forward_quantized(qv5, sv5), args.steps, args.warmup)
         stages["requant_o"] = timed(lambda: xops.quantize_rows(o5.reshape(M5, K), fp8), args.steps, args.warmup)
-        stages["ffn_up_gelu"] = timed(lambda: chain.ff_up.forward_quantized(qa5, sa5), args.steps, args.warmup)
-        stages["requant_h"] = timed(lambda: xops.quantize_rows(h5.reshape(M5, 4 * K), fp8), args.steps,
-                                    args.warmup)
+        stages["ffn_up"] = timed(lambda: chain.ff_up.forward_quantized(qa5, sa5), args.steps, args.warmup)
+        stages["requant_h_gelu"] = timed(lambda: chain.ff_down.quantize_input(h5.reshape(M5, 4 * K)), args.steps,
+                                         args.warmup)
         stages["ffn_down"] = timed(lambda: chain.ff_down.forward_quantized(qh5, sh5_), args.steps, args.warmup)
         kernels["c5_chain_m31248"] = {"ms": ms_chain, "gemm_flop": chain_flop,
                                       "tflops": chain_flop / (ms_chain * 1e-3) / 1e12,

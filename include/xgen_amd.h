@@ -89,6 +89,19 @@ int xgen_quantize_rows(int in_dtype, const void *x, int64_t rows, int64_t cols, 
                        int out_dtype, void *q, int64_t ldq, float *scale, hipStream_t stream);
 
 /*
+ * xgen_quantize_rows of dtype(gelu_tanh(x)) (dtype = in_dtype) in the same single
+ * pass: the FFN's GELU-tanh and the down-projection's per-token input quantization
+ * (diffusers FeedForward "gelu-approximate" between the two linears,
+ * x_diffusers/x_diffusers/framework/transformer/hunyuan.py:358; the reference
+ * materializes the GELU output and its next linear quantizes it).  The GELU is the
+ * one the GEMM epilogue applies with XGEN_ACT_GELU_TANH, so an up-projection
+ * without it followed by this gives the bytes and scales of the up-projection
+ * with it followed by xgen_quantize_rows.  Arguments as xgen_quantize_rows.
+ */
+int xgen_quantize_rows_gelu(int in_dtype, const void *x, int64_t rows, int64_t cols, int64_t ldx,
+                            int out_dtype, void *q, int64_t ldq, float *scale, hipStream_t stream);
+
+/*
  * NaN-propagating max |x| over a contiguous BF16/F16 tensor of numel elements
  * (activation_abs_peak, x_base/x_base/operator/h3_abs_peak.py:21-25).
  * peak: one float32 on the device.  workspace: device memory of at least

@@ -1,5 +1,5 @@
-"""GPU parity of the C5 chain (fused front end -> QKV -> out-proj -> FFN up with
-GELU-tanh -> per-token requant -> FFN down) through DiTLinearChain.
+"""GPU parity of the C5 chain (fused front end -> QKV -> out-proj -> FFN up ->
+GELU-tanh + per-token requant -> FFN down) through DiTLinearChain.
 
 Each stage is checked against the oracle applied to the kernel's own input of
 that stage: quantized bytes and scales bit-exact, bf16 outputs within rel-L2
@@ -26,6 +26,7 @@ import torch
 
 import oracle.ref as R
 import xgen_amd  # noqa: F401
+from xgen_amd import _native as N
 from xgen_amd import workloads
 from xgen_amd.operator.dit_chain import DiTLinearChain
 
@@ -37,7 +38,7 @@ MODEL_REL_MAX, MODEL_COS_MIN = 5e-3, 0.99999
 NAMES = ("qkv", "out", "ffn_up", "ffn_down")
 
 
-def chain_inputs(B, S, d, T, seed, dev, accumulation):
+def chain_inputs(B, S, d, T, seed, dev, accumulation, gelu="requant"):
     g = workloads.generator(seed)
     x, _ = workloads.activations(B * S, d, g)
     shift, scale = workloads.adaln_tables(T, d, g)
@@ -47,16 +48,18 @@ def chain_inputs(B, S, d, T, seed, dev, accumulation):
         w = (torch.randn((N, K), generator=g) * 0.02).to(torch.bfloat16)
         b = (torch.randn((N,), generator=g) * 0.01).to(torch.bfloat16)
         weights[name] = (w, b)
-    chain = DiTLinearChain(*[t.to(dev) for name in NAMES for t in weights[name]], accumulation=accumulation)
+    chain = DiTLinearChain(*[t.to(dev) for name in NAMES for t in weights[name]], accumulation=accumulation,
+                           gelu=gelu)
     return x.reshape(B, S, d), scale, shift, idx, weights, chain
 
 
-def check_stage(lin, inp, out, rows=None, act=None):
-    """out = lin(inp) per the oracle, given the kernel's own bf16 input (rows: optional sample)."""
+def check_stage(lin, inp, out, rows=None, act=None, gelu=None):
+    """out = lin(inp) per the oracle, given the kernel's own bf16 input (rows: optional sample);
+    gelu: the GPU's GELU (the kernel_gelu fixture) where lin quantizes gelu_tanh of its input."""
     if rows is not None:
         inp, out = inp[rows], out[rows]
-    qa, sa = xops.quantize_rows(inp.contiguous(), FP8)
-    q2, s2 = R.quantize_rows_fp8(inp.cpu())
+    qa, sa = xops.quantize_rows(inp.contiguous(), FP8, N.ACT_GELU_TANH if gelu else N.ACT_NONE)
+    q2, s2 = R.quantize_rows_fp8(gelu(inp) if gelu else inp.cpu())
     assert torch.equal(qa.cpu().view(torch.uint8), q2.view(torch.uint8))
     assert torch.equal(sa.cpu().view(torch.int32), s2.view(torch.int32))
     acc = R.fp8_mfma_accumulate if lin.accumulation == "mfma" else None
@@ -86,7 +89,7 @@ def check_end_to_end(got, x, scale, shift, idx, weights, accumulation, front):
 
 @pytest.mark.parametrize("accumulation", ["exact", "mfma"])
 @pytest.mark.parametrize("B,S,d", [(2, 150, 256), (1, 333, 512)])
-def test_chain_matches_oracle(cuda, B, S, d, accumulation):
+def test_chain_matches_oracle(cuda, kernel_gelu, B, S, d, accumulation):
     x, scale, shift, idx, weights, chain = chain_inputs(B, S, d, 20, seed=S + d, dev=cuda, accumulation=accumulation)
     qkv, o, h, y = chain(x.to(cuda), scale.to(cuda), shift.to(cuda), idx.to(cuda))
     M = B * S
@@ -100,13 +103,31 @@ def test_chain_matches_oracle(cuda, B, S, d, accumulation):
                                 chain.qkv.bias.cpu(), accumulate=acc)
     assert R.rel_l2(qkv, ref_qkv) <= 1e-3 and R.cosine(qkv, ref_qkv) >= 0.9999
     check_stage(chain.out, qkv[:, 2 * d:], o)
-    check_stage(chain.ff_up, o, h, act="gelu_tanh")
-    check_stage(chain.ff_down, h, y)
-    check_end_to_end((qkv, o, h, y), x, scale, shift, idx, weights, accumulation, (fq.cpu(), fs.cpu()))
+    check_stage(chain.ff_up, o, h)
+    check_stage(chain.ff_down, h, y, gelu=kernel_gelu)
+    # the oracle composite's hidden is after the GELU
+    check_end_to_end((qkv, o, kernel_gelu(h), y), x, scale, shift, idx, weights, accumulation,
+                     (fq.cpu(), fs.cpu()))
+
+
+def test_gelu_placements_agree(cuda, kernel_gelu):
+    """gelu='requant' (GELU in ff_down's quantizer, the default) and gelu='epilogue' (GELU in
+    ff_up's GEMM epilogue) give the same QKV, out-projection and FFN output bit for bit; the
+    epilogue form's hidden is the GPU's GELU of the requant form's."""
+    outs = {}
+    for gelu in ("requant", "epilogue"):
+        x, scale, shift, idx, _, chain = chain_inputs(1, 333, 512, 20, seed=7, dev=cuda, accumulation="mfma",
+                                                      gelu=gelu)
+        outs[gelu] = chain(x.to(cuda), scale.to(cuda), shift.to(cuda), idx.to(cuda))
+    (qkv1, o1, h1, y1), (qkv2, o2, h2, y2) = outs["requant"], outs["epilogue"]
+    for a, b in ((qkv1, qkv2), (o1, o2), (y1, y2)):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert torch.equal(kernel_gelu(h1).view(torch.int16), h2.cpu().view(torch.int16))
+    assert not torch.equal(h1.view(torch.int16), h2.view(torch.int16))
 
 
 @pytest.mark.parametrize("accumulation", ["exact", "mfma"])
-def test_chain_full_size_c5_sampled_rows(cuda, accumulation):
+def test_chain_full_size_c5_sampled_rows(cuda, kernel_gelu, accumulation):
     """C5 at M = 31,248 tokens (10 s clip, SP8 share), d = 3,072: the whole chain on the GPU,
     48 seeded rows (first and last included) checked stage by stage and end to end."""
     M, d = workloads.M_10S, workloads.D_MODEL
@@ -122,9 +143,11 @@ def test_chain_full_size_c5_sampled_rows(cuda, accumulation):
     rc = rows.to(cuda)
     fq, fs = xops.norm_affine_quant(x[rc][None], None, scale, shift, idx[rc], 1e-6, 0, FP8, False)[:2]
     check_stage(chain.out, qkv[:, 2 * d:], o, rc)
-    check_stage(chain.ff_up, o, h, rc, act="gelu_tanh")
-    check_stage(chain.ff_down, h, y, rc)
+    check_stage(chain.ff_up, o, h, rc)
+    check_stage(chain.ff_down, h, y, rc, gelu=kernel_gelu)
     weights = {k: (w.cpu(), b.cpu()) for k, (w, b) in wb.items()}
-    dist = check_end_to_end([t[rc].cpu() for t in (qkv, o, h, y)], x[rc][None].cpu(), scale.cpu(), shift.cpu(),
+    got = [t[rc].cpu() for t in (qkv, o, h, y)]
+    got[2] = kernel_gelu(got[2])
+    dist = check_end_to_end(got, x[rc][None].cpu(), scale.cpu(), shift.cpu(),
                             idx[rc].cpu(), weights, accumulation, (fq.cpu(), fs.cpu()))
     print(f"C5 end to end ({accumulation}):", {n: f"rel {r:.2e} cos {c:.7f}" for n, (r, c) in dist.items()})

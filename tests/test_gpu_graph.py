@@ -67,7 +67,7 @@ def test_c2_step_replays(cuda):
 
 @pytest.mark.parametrize("accumulation", ["mfma", "exact"])
 def test_chain_replays(cuda, accumulation):
-    """The C5 chain's kernels (front end, QKV, requant, out-projection, FFN up + GELU, requant, FFN
+    """The C5 chain's kernels (front end, QKV, requant, out-projection, FFN up, GELU requant, FFN
     down) at S = 700, d = 512 in one graph."""
     B, S, d, T = 1, 700, 512, 20
     g = workloads.generator(32, cuda)

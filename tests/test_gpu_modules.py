@@ -192,3 +192,26 @@ def test_ffn_pair_gelu_requant(cuda, kind):
     qh2, sh2 = quant(h.cpu())
     assert torch.equal(qh_gpu.cpu().view(torch.uint8), qh2.view(torch.uint8))
     assert torch.equal(sh_gpu.cpu(), sh2)
+
+
+def test_ffn_pair_gelu_in_down_requant(cuda):
+    """H3FP8Linear(input_activation='gelu_tanh') applies the GELU in its input quantization: the
+    down projection of the plain up output equals the down projection of the GELU-epilogue up
+    output, bit for bit."""
+    g = workloads.generator(4)
+    M, d = 300, 512
+    x, _ = workloads.activations(M, d, g)
+    wu = (torch.randn(4 * d, d, generator=g) * 0.02).to(torch.bfloat16)
+    bu = (torch.randn(4 * d, generator=g) * 0.01).to(torch.bfloat16)
+    wd = (torch.randn(d, 4 * d, generator=g) * 0.02).to(torch.bfloat16)
+    bd = (torch.randn(d, generator=g) * 0.01).to(torch.bfloat16)
+    opts = dict(weight_scaling="channel", activation_scaling="token")
+    up_gelu = H3FP8Linear(wu, bu, activation="gelu_tanh", **opts).cuda()
+    up = H3FP8Linear(wu, bu, **opts).cuda()
+    down = H3FP8Linear(wd, bd, **opts).cuda()
+    down_gelu = H3FP8Linear(wd, bd, input_activation="gelu_tanh", **opts).cuda()
+    xc = x.cuda()[None]
+    y1 = down(up_gelu(xc))
+    y2 = down_gelu(up(xc))
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+    assert "input_activation=gelu_tanh" in repr(down_gelu)

@@ -5,6 +5,7 @@ import torch
 
 import oracle.ref as R
 import xgen_amd  # noqa: F401
+from xgen_amd import _native as N
 from xgen_amd import workloads
 from xgen_amd.operator.h3_abs_peak import activation_abs_peak
 from xgen_amd.operator.h3_fp8_quant import quantize_activation
@@ -175,3 +176,71 @@ def test_full_size_token_quant_c2(cuda):
     qi, si = xops.quantize_rows(x, torch.int8)
     qi_ref, si_ref = R.quantize_rows_c(x.cpu(), "int8")
     assert_same_quant(qi, si, qi_ref, si_ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_kernel_gelu_within_ulp_of_torch(kernel_gelu, dtype):
+    """The GELU-tanh shared by the GEMM epilogue and the GELU requant, on every 16-bit value:
+    within 1 ulp of torch's GELU(approximate='tanh') above -3 (absolute 1e-3 at and below -3,
+    where torch's float32 tanh form cancels), exact (x/2) for |x| < 2^-60, +0 -> +0, -0 -> -0,
+    +inf -> +inf, NaN wherever torch gives NaN."""
+    x = torch.arange(1 << 16, dtype=torch.int32).to(torch.int16).view(dtype)
+    got = kernel_gelu(x)
+    ref = torch.nn.functional.gelu(x.float(), approximate="tanh").to(dtype)
+    fin = torch.isfinite(x)
+    assert torch.equal(torch.isnan(got[~fin]), torch.isnan(ref[~fin]))
+    assert got[x == float("inf")].item() == float("inf")
+    body = fin & (x.float() > -3)
+    assert R.bf16_ulp_diff(got[body], ref[body]).max() <= 1
+    tail = fin & (x.float() <= -3)
+    assert (got[tail].float() - ref[tail].float()).abs().max() <= 1e-3
+    tiny = fin & (x.float().abs() < 2.0 ** -60)
+    assert torch.equal(got[tiny].view(torch.int16), (x[tiny].float() * 0.5).to(dtype).view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("K", [13, 1000, 2048, 3072, 4096, 6144, 8192, 12288, 16384, 20000])
+@pytest.mark.parametrize("out", ["fp8", "int8"])
+def test_gelu_row_quantizers_match_oracle(cuda, kernel_gelu, dtype, K, out):
+    """quantize_rows(x, ., ACT_GELU_TANH) quantizes dtype(gelu_tanh(x)): bytes and scales bit-exact
+    against the oracle's row quantizer of the GPU's GELU of x, for every launch form (2 to 32
+    values per lane, 1 to 4 waves per row, the generic kernel for odd and wide rows) and the edge
+    rows (zeros, -0, tiny, inf, NaN, outlier channels)."""
+    x = rows_with_edges(67, K, dtype, seed=K + 1)
+    q, s = xops.quantize_rows(x.to(cuda), torch.float8_e4m3fn if out == "fp8" else torch.int8, N.ACT_GELU_TANH)
+    q_ref, s_ref = R.quantize_rows_c(kernel_gelu(x), out)
+    assert_same_quant(q, s, q_ref, s_ref)
+
+
+@pytest.mark.parametrize("kind", ["fp8", "int8"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_gelu_requant_equals_epilogue_then_requant(cuda, kind, dtype):
+    """The FFN's two placements of the GELU give the down-projection the same input: quantizing
+    the up GEMM's plain output with the GELU requant equals quantizing its GELU-epilogue output,
+    bit for bit, on row widths of every launch form (strided views of one [M, 16,400] output)."""
+    dt = torch.float8_e4m3fn if kind == "fp8" else torch.int8
+    g = workloads.generator(41, cuda)
+    M, K, Nf = 200, 256, 16400
+    qa, sa = xops.quantize_rows(torch.randn((M, K), generator=g, device=cuda).to(torch.bfloat16), dt)
+    qw, sw = xops.quantize_rows((torch.randn((Nf, K), generator=g, device=cuda) * 0.05).to(torch.bfloat16), dt)
+    bias = (torch.randn((Nf,), generator=g, device=cuda) * 0.1).to(dtype)
+    pre, _ = xops.scaled_mm(qa, qw, sa, sw, bias, dtype, N.ACT_NONE, False)
+    post, _ = xops.scaled_mm(qa, qw, sa, sw, bias, dtype, N.ACT_GELU_TANH, False)
+    for width in (1000, 2048, 3072, 4096, 6144, 8192, 12288, 16384, 16400, 1003):
+        q1, s1 = xops.quantize_rows(pre[:, :width], dt, N.ACT_GELU_TANH)
+        q2, s2 = xops.quantize_rows(post[:, :width], dt)
+        assert torch.equal(q1.view(torch.uint8), q2.view(torch.uint8)), width
+        assert torch.equal(s1.view(torch.int32), s2.view(torch.int32)), width
+
+
+def test_full_size_gelu_requant_k12288(cuda, kernel_gelu):
+    """The GELU requant at C3 size (M=15,624, K=12,288; the non-temporal-load form): bytes and
+    scales of every row against the oracle's quantizer of the GPU's GELU, FP8 and INT8."""
+    g = torch.Generator(device=cuda).manual_seed(13)
+    h = torch.randn((workloads.M_5S, 4 * workloads.D_MODEL), generator=g, device=cuda).to(torch.bfloat16)
+    h[9] *= 50
+    gh = kernel_gelu(h)
+    for out, dt in (("fp8", torch.float8_e4m3fn), ("int8", torch.int8)):
+        q, s = xops.quantize_rows(h, dt, N.ACT_GELU_TANH)
+        q_ref, s_ref = R.quantize_rows_c(gh, out)
+        assert_same_quant(q, s, q_ref, s_ref)

@@ -7,6 +7,7 @@ from torch import nn
 
 import xgen_amd  # noqa: F401  (registers torch.ops.xgen_amd)
 from xgen_amd import config
+from xgen_amd.operator.dit_chain import DiTLinearChain
 from xgen_amd.operator.h3_fp8 import H3FP8Linear
 from xgen_amd.operator.nq2 import norm_affine_quant
 
@@ -21,6 +22,18 @@ def test_projection_rejects_unaligned_dimensions():
     # x_base/tests/test_h3_cuda_precision_ops.py:14-16
     with pytest.raises(ValueError, match='divisible by 16'):
         H3FP8Linear(torch.randn(17, 32))
+
+
+def test_input_activation_contract():
+    with pytest.raises(ValueError, match="activation_scaling='token'"):
+        H3FP8Linear(torch.randn(32, 32), input_activation="gelu_tanh")
+    with pytest.raises(ValueError, match="unsupported input_activation"):
+        H3FP8Linear(torch.randn(32, 32), activation_scaling="token", input_activation="relu")
+    w = torch.zeros(32, 64, dtype=torch.float8_e4m3fn)
+    with pytest.raises(ValueError, match="activation_scaling='token'"):
+        H3FP8Linear.from_packed(w, torch.ones(()), input_activation="gelu_tanh")
+    with pytest.raises(ValueError, match="gelu must be"):
+        DiTLinearChain(*([torch.zeros(16, 16)] * 8), gelu="both")
 
 
 def test_from_packed_contract():

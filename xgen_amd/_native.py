@@ -45,6 +45,7 @@ SIGNATURES = {
     "xgen_status_string": (ctypes.c_char_p, [_c_int]),
     "xgen_last_error": (ctypes.c_char_p, []),
     "xgen_quantize_rows": (_c_int, [_c_int, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_ptr, _c_i64, _c_ptr, _c_ptr]),
+    "xgen_quantize_rows_gelu": (_c_int, [_c_int, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_ptr, _c_i64, _c_ptr, _c_ptr]),
     "xgen_abs_peak_workspace_bytes": (_c_size, [_c_i64]),
     "xgen_abs_peak": (_c_int, [_c_int, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_size, _c_ptr]),
     "xgen_fp8_tensor_scale": (_c_int, [_c_int, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_size, _c_ptr]),

@@ -149,20 +149,18 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-// GELU with the tanh approximation, via tanh(z) = 2*sigmoid(2z) - 1:
-// 0.5*x*(1 + tanh(z)) = x / (1 + exp(-2z)),  z = sqrt(2/pi) * (x + 0.044715 x^3).
-__device__ __forceinline__ float gelu_tanh(float x) {
-  // -2 z log2(e) = x (c0 + c1 x^2): the exponent of exp(-2z) in base 2
-  constexpr float kC0 = (float)(-2.0 * 1.4426950408889634 * 0.7978845608028654);
-  constexpr float kC1 = (float)(-2.0 * 1.4426950408889634 * 0.7978845608028654 * 0.044715);
-  const float t = __builtin_amdgcn_exp2f(x * __builtin_fmaf(kC1, x * x, kC0));
-  return x * __builtin_amdgcn_rcpf(1.0f + t);
-}
-
+// v rounded to the output dtype, as the stored output is rounded.  For f16 the
+// empty asm keeps v an f32 value: the fma producing it would otherwise be
+// selected with the f16 rounding as one v_fma_mixlo_f16 (one rounding of the
+// exact a*b+c, where the store rounds the f32 result).
 template <int OUT_DT>
 __device__ __forceinline__ float round_out(float v) {
-  if constexpr (OUT_DT == XGEN_DTYPE_BF16) return round_bf16(v);
-  else return (float)(_Float16)v;
+  if constexpr (OUT_DT == XGEN_DTYPE_BF16) {
+    return round_bf16(v);
+  } else {
+    asm volatile("" : "+v"(v));
+    return (float)(_Float16)v;
+  }
 }
 template <int OUT_DT>
 __device__ __forceinline__ uint32_t pack_out(float a, float b) {

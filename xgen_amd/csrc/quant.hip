@@ -3,6 +3,10 @@
 //  * xgen_quantize_rows  — per-row FP8 e4m3fn (the arithmetic of
 //    x_base/x_base/operator/h3_fp8.py:9-12 applied per row) or per-row INT8
 //    (npu_dynamic_quant as restated in npu_fusion/f2bc/op_kernel/f2bc_kernel.asc:89-107).
+//  * xgen_quantize_rows_gelu — the same of dtype(gelu_tanh(x)): the FFN's GELU
+//    (x_diffusers/x_diffusers/framework/transformer/hunyuan.py:358, diffusers
+//    FeedForward "gelu-approximate") and the down-projection's input quantization
+//    in one pass over the hidden activation.
 //  * xgen_abs_peak / xgen_fp8_tensor_scale / xgen_fp8_pack — the per-tensor
 //    activation quantizer of x_base/x_base/operator/h3_fp8_quant.py:9-25 and
 //    h3_abs_peak.py:14-25.
@@ -22,6 +26,31 @@ namespace {
 
 constexpr int kThreads = 256;  // 4 waves per workgroup
 
+// dtype(gelu_tanh(x)) of the 8 values of a chunk, in place (a chunk of zeros
+// stays zeros: gelu_tanh(0) = 0)
+template <int DT>
+__device__ __forceinline__ u32x4 gelu_chunk(const u32x4 &c) {
+  const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float lo = gelu_tanh(Half2<DT>::lo(w[i])), hi = gelu_tanh(Half2<DT>::hi(w[i]));
+    o[i] = DT == XGEN_DTYPE_BF16 ? pack_bf16x2(lo, hi) : pack_f16x2(lo, hi);
+  }
+  return u32x4{o[0], o[1], o[2], o[3]};
+}
+
+// the 16-bit pattern of dtype(gelu_tanh(x)) for a 16-bit input pattern.  The
+// empty asm keeps the product an f32 value: without it the f16 rounding of
+// x * r (x an f16 widened to f32) is selected as v_fma_mixlo_f16 x, r, +0,
+// which turns a -0 product (x = -0, or x far below 0 where r = 0) into +0.
+template <int DT>
+__device__ __forceinline__ uint32_t gelu_bits(uint32_t b) {
+  float g = gelu_tanh(Half2<DT>::lo(b));
+  asm volatile("" : "+v"(g));
+  return (DT == XGEN_DTYPE_BF16 ? pack_bf16x2(g, 0.0f) : pack_f16x2(g, 0.0f)) & 0xffffu;
+}
+
 // WPR waves per row, CH chunks of 8 elements per lane: one row covers up to
 // 512 * WPR * CH elements.  Requires cols % 8 == 0 and 16-byte aligned rows.
 //
@@ -36,8 +65,9 @@ constexpr int kThreads = 256;  // 4 waves per workgroup
 // repeated; the compiler's wait counts then name exactly the loads a step
 // needs.  The wave index is made wave-uniform, so row addresses are
 // scalar-unit work.  NT: the input is read non-temporally (calls larger than
-// the last-level cache).
-template <int DT, int OUT, int WPR, int CH, bool NT>
+// the last-level cache).  ACT: XGEN_ACT_GELU_TANH quantizes dtype(gelu_tanh(x)),
+// applied to the row in registers.
+template <int DT, int OUT, int WPR, int CH, bool NT, int ACT>
 __global__ __launch_bounds__(kThreads) void quant_rows_vec_kernel(
     const uint8_t *__restrict__ x, int64_t rows, int cols, int64_t ldx_bytes,
     uint8_t *__restrict__ q, int64_t ldq, float *__restrict__ scale) {
@@ -69,6 +99,10 @@ __global__ __launch_bounds__(kThreads) void quant_rows_vec_kernel(
     __builtin_amdgcn_sched_barrier(0);
     load_row(base + step + row_in_block, cn);
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (ACT == XGEN_ACT_GELU_TANH) {
+#pragma unroll
+      for (int j = 0; j < CH; ++j) c[j] = gelu_chunk<DT>(c[j]);
+    }
     u16x2 m = {0, 0};
 #pragma unroll
     for (int j = 0; j < CH; ++j) m = absmax_chunk<DT>(c[j], m);
@@ -105,7 +139,7 @@ __global__ __launch_bounds__(kThreads) void quant_rows_vec_kernel(
 }
 
 // Any width / alignment: one workgroup per row, two passes over global memory.
-template <int DT, int OUT>
+template <int DT, int OUT, int ACT>
 __global__ __launch_bounds__(kThreads) void quant_rows_generic_kernel(
     const uint16_t *__restrict__ x, int64_t rows, int64_t cols, int64_t ldx,
     uint8_t *__restrict__ q, int64_t ldq, float *__restrict__ scale) {
@@ -113,7 +147,7 @@ __global__ __launch_bounds__(kThreads) void quant_rows_generic_kernel(
   const uint16_t *xr = x + row * ldx;
   uint32_t mb = 0;
   for (int64_t c = threadIdx.x; c < cols; c += kThreads) {
-    uint32_t b = xr[c] & 0x7fffu;
+    uint32_t b = (ACT == XGEN_ACT_GELU_TANH ? gelu_bits<DT>(xr[c]) : xr[c]) & 0x7fffu;
     mb = mb > b ? mb : b;
   }
   mb = wave_max_u32(mb);
@@ -127,7 +161,7 @@ __global__ __launch_bounds__(kThreads) void quant_rows_generic_kernel(
   const RowQuant p = (OUT == XGEN_DTYPE_E4M3) ? fp8_row_params(amax) : i8_row_params(amax);
   uint8_t *qr = q + row * ldq;
   for (int64_t c = threadIdx.x; c < cols; c += kThreads) {
-    const uint32_t w = xr[c];
+    const uint32_t w = ACT == XGEN_ACT_GELU_TANH ? gelu_bits<DT>(xr[c]) : xr[c];
     const float v = Half2<DT>::lo(w);
     uint32_t b;
     if constexpr (OUT == XGEN_DTYPE_E4M3) {
@@ -141,29 +175,29 @@ __global__ __launch_bounds__(kThreads) void quant_rows_generic_kernel(
   if (threadIdx.x == 0) scale[row] = p.s;
 }
 
-template <int DT, int OUT, int WPR, int CH, bool NT>
+template <int DT, int OUT, int WPR, int CH, bool NT, int ACT>
 void launch_vec_policy(const void *x, int64_t rows, int64_t cols, int64_t ldx, void *q, int64_t ldq,
                        float *scale, hipStream_t stream) {
   constexpr int kRowsPerBlock = 4 / WPR;
   // as many workgroups as are resident at once (a streaming grid must not queue)
-  static const int per_cu = resident_blocks_per_cu(quant_rows_vec_kernel<DT, OUT, WPR, CH, NT>, kThreads);
+  static const int per_cu = resident_blocks_per_cu(quant_rows_vec_kernel<DT, OUT, WPR, CH, NT, ACT>, kThreads);
   const int64_t need = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
   const int64_t cap = (int64_t)device_cu_count() * per_cu;
   const int64_t blocks = need < cap ? need : cap;
-  quant_rows_vec_kernel<DT, OUT, WPR, CH, NT><<<dim3((unsigned)blocks), dim3(kThreads), 0, stream>>>(
+  quant_rows_vec_kernel<DT, OUT, WPR, CH, NT, ACT><<<dim3((unsigned)blocks), dim3(kThreads), 0, stream>>>(
       static_cast<const uint8_t *>(x), rows, (int)cols, ldx * 2, static_cast<uint8_t *>(q), ldq, scale);
 }
 
-template <int DT, int OUT, int WPR, int CH>
+template <int DT, int OUT, int ACT, int WPR, int CH>
 void launch_vec(const void *x, int64_t rows, int64_t cols, int64_t ldx, void *q, int64_t ldq,
                 float *scale, hipStream_t stream) {
   if (rows * cols * 3 > kLastLevelCacheBytes)  // 2 bytes read + 1 written per element
-    launch_vec_policy<DT, OUT, WPR, CH, true>(x, rows, cols, ldx, q, ldq, scale, stream);
+    launch_vec_policy<DT, OUT, WPR, CH, true, ACT>(x, rows, cols, ldx, q, ldq, scale, stream);
   else
-    launch_vec_policy<DT, OUT, WPR, CH, false>(x, rows, cols, ldx, q, ldq, scale, stream);
+    launch_vec_policy<DT, OUT, WPR, CH, false, ACT>(x, rows, cols, ldx, q, ldq, scale, stream);
 }
 
-template <int DT, int OUT>
+template <int DT, int OUT, int ACT>
 int quantize_rows_typed(const void *x, int64_t rows, int64_t cols, int64_t ldx, void *q,
                         int64_t ldq, float *scale, hipStream_t stream) {
   const bool vec = (cols % 8 == 0) && (ldx % 8 == 0) && (ldq % 8 == 0) && aligned16(x) &&
@@ -172,26 +206,26 @@ int quantize_rows_typed(const void *x, int64_t rows, int64_t cols, int64_t ldx, 
   // (32 values) per lane where 4 waves suffice (register budget of the
   // streaming kernel, which holds the current and the next row).
   if (vec && cols <= 512 * 2) {
-    launch_vec<DT, OUT, 1, 2>(x, rows, cols, ldx, q, ldq, scale, stream);
+    launch_vec<DT, OUT, ACT, 1, 2>(x, rows, cols, ldx, q, ldq, scale, stream);
   } else if (vec && cols <= 512 * 4) {
-    launch_vec<DT, OUT, 1, 4>(x, rows, cols, ldx, q, ldq, scale, stream);
+    launch_vec<DT, OUT, ACT, 1, 4>(x, rows, cols, ldx, q, ldq, scale, stream);
   } else if (vec && cols <= 1024 * 3) {
-    launch_vec<DT, OUT, 2, 3>(x, rows, cols, ldx, q, ldq, scale, stream);
+    launch_vec<DT, OUT, ACT, 2, 3>(x, rows, cols, ldx, q, ldq, scale, stream);
   } else if (vec && cols <= 1024 * 4) {
-    launch_vec<DT, OUT, 2, 4>(x, rows, cols, ldx, q, ldq, scale, stream);
+    launch_vec<DT, OUT, ACT, 2, 4>(x, rows, cols, ldx, q, ldq, scale, stream);
   } else if (vec && cols <= 2048 * 3) {
-    launch_vec<DT, OUT, 4, 3>(x, rows, cols, ldx, q, ldq, scale, stream);
+    launch_vec<DT, OUT, ACT, 4, 3>(x, rows, cols, ldx, q, ldq, scale, stream);
   } else if (vec && cols <= 2048 * 4) {
-    launch_vec<DT, OUT, 4, 4>(x, rows, cols, ldx, q, ldq, scale, stream);
+    launch_vec<DT, OUT, ACT, 4, 4>(x, rows, cols, ldx, q, ldq, scale, stream);
   } else if (vec && cols <= 2048 * 6) {
-    launch_vec<DT, OUT, 4, 6>(x, rows, cols, ldx, q, ldq, scale, stream);
+    launch_vec<DT, OUT, ACT, 4, 6>(x, rows, cols, ldx, q, ldq, scale, stream);
   } else if (vec && cols <= 2048 * 8) {
-    launch_vec<DT, OUT, 4, 8>(x, rows, cols, ldx, q, ldq, scale, stream);
+    launch_vec<DT, OUT, ACT, 4, 8>(x, rows, cols, ldx, q, ldq, scale, stream);
   } else {
-    quant_rows_generic_kernel<DT, OUT><<<dim3((unsigned)rows), dim3(kThreads), 0, stream>>>(
+    quant_rows_generic_kernel<DT, OUT, ACT><<<dim3((unsigned)rows), dim3(kThreads), 0, stream>>>(
         static_cast<const uint16_t *>(x), rows, cols, ldx, static_cast<uint8_t *>(q), ldq, scale);
   }
-  return launch_status("xgen_quantize_rows");
+  return XGEN_OK;
 }
 
 // ---------------------------------------------------------------------------
@@ -351,10 +385,11 @@ int check_peak_args(const char *fn, int in_dtype, const void *x, int64_t numel, 
 
 using namespace xgen;
 
-extern "C" int xgen_quantize_rows(int in_dtype, const void *x, int64_t rows, int64_t cols,
-                                  int64_t ldx, int out_dtype, void *q, int64_t ldq, float *scale,
-                                  hipStream_t stream) {
-  const char *fn = "xgen_quantize_rows";
+namespace xgen {
+namespace {
+template <int ACT>
+int quantize_rows_entry(const char *fn, int in_dtype, const void *x, int64_t rows, int64_t cols, int64_t ldx,
+                        int out_dtype, void *q, int64_t ldq, float *scale, hipStream_t stream) {
   if (!is_input_dtype(in_dtype)) return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: input dtype must be BF16 or F16", fn);
   if (!is_quant_dtype(out_dtype)) return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: output dtype must be E4M3 or I8", fn);
   if (rows < 0 || cols <= 0 || ldx < cols || ldq < cols)
@@ -364,13 +399,33 @@ extern "C" int xgen_quantize_rows(int in_dtype, const void *x, int64_t rows, int
   if (rows == 0) return ok();
   if (!x || !q || !scale) return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
   if (in_dtype == XGEN_DTYPE_BF16) {
-    return out_dtype == XGEN_DTYPE_E4M3
-               ? quantize_rows_typed<XGEN_DTYPE_BF16, XGEN_DTYPE_E4M3>(x, rows, cols, ldx, q, ldq, scale, stream)
-               : quantize_rows_typed<XGEN_DTYPE_BF16, XGEN_DTYPE_I8>(x, rows, cols, ldx, q, ldq, scale, stream);
+    if (out_dtype == XGEN_DTYPE_E4M3)
+      quantize_rows_typed<XGEN_DTYPE_BF16, XGEN_DTYPE_E4M3, ACT>(x, rows, cols, ldx, q, ldq, scale, stream);
+    else
+      quantize_rows_typed<XGEN_DTYPE_BF16, XGEN_DTYPE_I8, ACT>(x, rows, cols, ldx, q, ldq, scale, stream);
+  } else {
+    if (out_dtype == XGEN_DTYPE_E4M3)
+      quantize_rows_typed<XGEN_DTYPE_F16, XGEN_DTYPE_E4M3, ACT>(x, rows, cols, ldx, q, ldq, scale, stream);
+    else
+      quantize_rows_typed<XGEN_DTYPE_F16, XGEN_DTYPE_I8, ACT>(x, rows, cols, ldx, q, ldq, scale, stream);
   }
-  return out_dtype == XGEN_DTYPE_E4M3
-             ? quantize_rows_typed<XGEN_DTYPE_F16, XGEN_DTYPE_E4M3>(x, rows, cols, ldx, q, ldq, scale, stream)
-             : quantize_rows_typed<XGEN_DTYPE_F16, XGEN_DTYPE_I8>(x, rows, cols, ldx, q, ldq, scale, stream);
+  return launch_status(fn);
+}
+}  // namespace
+}  // namespace xgen
+
+extern "C" int xgen_quantize_rows(int in_dtype, const void *x, int64_t rows, int64_t cols,
+                                  int64_t ldx, int out_dtype, void *q, int64_t ldq, float *scale,
+                                  hipStream_t stream) {
+  return quantize_rows_entry<XGEN_ACT_NONE>("xgen_quantize_rows", in_dtype, x, rows, cols, ldx, out_dtype, q, ldq,
+                                            scale, stream);
+}
+
+extern "C" int xgen_quantize_rows_gelu(int in_dtype, const void *x, int64_t rows, int64_t cols,
+                                       int64_t ldx, int out_dtype, void *q, int64_t ldq, float *scale,
+                                       hipStream_t stream) {
+  return quantize_rows_entry<XGEN_ACT_GELU_TANH>("xgen_quantize_rows_gelu", in_dtype, x, rows, cols, ldx, out_dtype,
+                                                 q, ldq, scale, stream);
 }
 
 extern "C" size_t xgen_abs_peak_workspace_bytes(int64_t numel) {

@@ -116,6 +116,18 @@ __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
   f32x2 v = {lo, hi};
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
 }
+
+// GELU with the tanh approximation (the GEMM epilogue's and the requant's: one definition, so
+// both give the same bits), via tanh(z) = 2*sigmoid(2z) - 1:
+// 0.5*x*(1 + tanh(z)) = x / (1 + exp(-2z)),  z = sqrt(2/pi) * (x + 0.044715 x^3).
+__device__ __forceinline__ float gelu_tanh(float x) {
+  // -2 z log2(e) = x (c0 + c1 x^2): the exponent of exp(-2z) in base 2
+  constexpr float kC0 = (float)(-2.0 * 1.4426950408889634 * 0.7978845608028654);
+  constexpr float kC1 = (float)(-2.0 * 1.4426950408889634 * 0.7978845608028654 * 0.044715);
+  const float t = __builtin_amdgcn_exp2f(x * __builtin_fmaf(kC1, x * x, kC0));
+  return x * __builtin_amdgcn_rcpf(1.0f + t);
+}
+
 // fp32 rounded to bf16 precision (RNE), returned as fp32: one
 // v_cvt_pk_bf16_f32 with the value in the high half and +0 in the low half, so
 // the word is the rounded value's fp32 bit pattern.

@@ -12,8 +12,14 @@ every later projection quantizes its own input per token:
     qkv  = QKV(q, s)                                     # [M, 3d]
     a    = attention(qkv)                                # caller's (default: the V third)
     o    = out_proj(a)                                   # [M, d]
-    h    = ff_up(o)  with the GELU-tanh epilogue         # [M, 4d]
-    y    = ff_down(h)                                    # [M, d]
+    h    = ff_up(o)                                      # [M, 4d], before the GELU
+    y    = ff_down(h)  GELU-tanh inside its input quantization  # [M, d]
+
+The GELU-tanh (hunyuan.py:358) runs in ff_down's per-token quantizer: the
+quantizer applies the same function to the same bf16 pre-activation, and rounds
+to bf16, as ff_up's GEMM epilogue would, so y is bit for bit the y of
+``gelu="epilogue"`` (GELU in ff_up's epilogue, h after the GELU), while the
+GEMM's epilogue stays the plain one.
 
 ``accumulation`` ("mfma" or "exact") is passed to the four linears.  Each
 per-token requantization can turn a last-bit difference of its bf16 input
@@ -37,17 +43,21 @@ from .nq2 import norm_affine_quant
 
 
 class DiTLinearChain(nn.Module):
-    """QKV, out-projection, FFN up (GELU-tanh) and FFN down as W8A8 FP8
+    """QKV, out-projection, FFN up and FFN down (GELU-tanh between them) as W8A8 FP8
     linears with per-channel weight and per-token activation scales."""
 
     def __init__(self, w_qkv, b_qkv, w_out, b_out, w_up, b_up, w_down, b_down, *, eps: float = 1e-6,
-                 accumulation: str = "mfma"):
+                 accumulation: str = "mfma", gelu: str = "requant"):
         super().__init__()
+        if gelu not in ("requant", "epilogue"):
+            raise ValueError("gelu must be 'requant' (in ff_down's quantizer) or 'epilogue' (in ff_up's GEMM)")
+        self.gelu = gelu
         opts = dict(weight_scaling="channel", activation_scaling="token", accumulation=accumulation)
         self.qkv = H3FP8Linear(w_qkv, b_qkv, **opts)
         self.out = H3FP8Linear(w_out, b_out, **opts)
-        self.ff_up = H3FP8Linear(w_up, b_up, activation="gelu_tanh", **opts)
-        self.ff_down = H3FP8Linear(w_down, b_down, **opts)
+        in_requant = gelu == "requant"
+        self.ff_up = H3FP8Linear(w_up, b_up, activation=None if in_requant else "gelu_tanh", **opts)
+        self.ff_down = H3FP8Linear(w_down, b_down, input_activation="gelu_tanh" if in_requant else None, **opts)
         self.eps = float(eps)
         d = self.qkv.in_features
         if self.qkv.out_features != 3 * d or self.out.in_features != d or self.ff_up.in_features != d \
@@ -56,8 +66,8 @@ class DiTLinearChain(nn.Module):
 
     def forward(self, x, scale_table, shift_table, indices, attention=None):
         """x bf16 [B, S, d]; scale/shift tables bf16 [T, d]; indices int64 [S].
-        Returns (qkv [B,S,3d], out-proj [B,S,d], FFN hidden after GELU [B,S,4d],
-        FFN output [B,S,d]), all bf16."""
+        Returns (qkv [B,S,3d], out-proj [B,S,d], FFN hidden [B,S,4d] (before the GELU with
+        gelu="requant", after it with gelu="epilogue"), FFN output [B,S,d]), all bf16."""
         if x.dim() != 3:
             raise ValueError("DiTLinearChain expects x of shape [B, S, d]")
         B, S, d = x.shape

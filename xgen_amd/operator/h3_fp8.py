@@ -64,11 +64,19 @@ def quantize_per_channel(value: torch.Tensor):
     return _on(value.device, *quantize_activation_rows(_device_weight(value)))
 
 
+def _check_input_activation(input_activation, activation_scaling):
+    if input_activation not in (None, "gelu_tanh"):
+        raise ValueError(f"unsupported input_activation {input_activation!r}")
+    if input_activation is not None and activation_scaling != "token":
+        raise ValueError("input_activation needs activation_scaling='token'")
+
+
 class H3FP8Linear(nn.Module):
     """Keep FP8 weights; quantize activations to E4M3 and run the FP8 MFMA GEMM."""
 
     def __init__(self, weight, bias=None, *, weight_scaling: str = "tensor",
-                 activation_scaling: str = "tensor", activation: str | None = None, accumulation: str = "mfma"):
+                 activation_scaling: str = "tensor", activation: str | None = None, accumulation: str = "mfma",
+                 input_activation: str | None = None):
         super().__init__()
         if weight.ndim != 2 or weight.shape[0] % 16 or weight.shape[1] % 16:
             raise ValueError("H3 FP8 requires projection dimensions divisible by 16")
@@ -78,6 +86,7 @@ class H3FP8Linear(nn.Module):
             raise ValueError(f"unsupported activation {activation!r}")
         if accumulation not in _ACCUMULATIONS:
             raise ValueError(f"accumulation must be one of {_ACCUMULATIONS}")
+        _check_input_activation(input_activation, activation_scaling)
         self.out_features, self.in_features = weight.shape
         packed, scale = (quantize_per_tensor(weight) if weight_scaling == "tensor"
                          else quantize_per_channel(weight))
@@ -87,12 +96,13 @@ class H3FP8Linear(nn.Module):
         self.register_buffer('bias', bias.detach().clone() if bias is not None else None)
         self.activation_scaling = activation_scaling
         self.activation = activation
+        self.input_activation = input_activation
         self.accumulation = accumulation
         self.calls = 0
 
     @classmethod
     def from_packed(cls, weight, scale, bias=None, *, activation_scaling: str = "tensor",
-                    activation: str | None = None, accumulation: str = "mfma"):
+                    activation: str | None = None, accumulation: str = "mfma", input_activation: str | None = None):
         """Reuse already quantized bytes and their original scale(s) without requantization."""
         if weight.dtype != torch.float8_e4m3fn or weight.ndim != 2 or any(n % 16 for n in weight.shape):
             raise ValueError('Packed H3 FP8 projection requires an aligned E4M3 matrix')
@@ -101,6 +111,7 @@ class H3FP8Linear(nn.Module):
         if activation_scaling not in ("tensor", "token") or activation not in _ACTIVATIONS \
                 or accumulation not in _ACCUMULATIONS:
             raise ValueError("bad activation_scaling / activation / accumulation")
+        _check_input_activation(input_activation, activation_scaling)
         result = cls.__new__(cls)
         nn.Module.__init__(result)
         result.out_features, result.in_features = weight.shape
@@ -109,6 +120,7 @@ class H3FP8Linear(nn.Module):
         result.register_buffer('bias', bias.detach().clone() if bias is not None else None)
         result.activation_scaling = activation_scaling
         result.activation = activation
+        result.input_activation = input_activation
         result.accumulation = accumulation
         result.calls = 0
         return result
@@ -117,8 +129,13 @@ class H3FP8Linear(nn.Module):
         return self._local_forward(x, self.bias)
 
     def quantize_input(self, matrix):
-        """(e4m3fn [M,K], float32 scale [1] or [M]) for a [M,K] activation."""
+        """(e4m3fn [M,K], float32 scale [1] or [M]) for a [M,K] activation; with
+        input_activation='gelu_tanh' the rows quantized are dtype(gelu_tanh(matrix)), computed in the
+        quantizer's pass (the bytes and scales of the previous linear's GELU epilogue followed by
+        this quantization, hunyuan.py:358)."""
         if self.activation_scaling == "token":
+            if getattr(self, 'input_activation', None) is not None:
+                return xops.quantize_rows(matrix, torch.float8_e4m3fn, _ACTIVATIONS[self.input_activation])
             return quantize_activation_rows(matrix)
         group = getattr(self, 'activation_group', None)
         packed, scale = quantize_activation(matrix, group=group)
@@ -167,4 +184,5 @@ class H3FP8Linear(nn.Module):
     def extra_repr(self):
         return (f"in_features={self.in_features}, out_features={self.out_features}, "
                 f"weight_scale={tuple(self.weight_scale.shape)}, activation_scaling={self.activation_scaling}, "
-                f"activation={self.activation}, accumulation={self.accumulation}")
+                f"activation={self.activation}, input_activation={getattr(self, 'input_activation', None)}, "
+                f"accumulation={self.accumulation}")

@@ -18,7 +18,7 @@ NAMESPACE = "xgen_amd"
 _LIB = None
 
 SCHEMAS = {
-    "quantize_rows": "quantize_rows(Tensor x, ScalarType out_dtype) -> (Tensor, Tensor)",
+    "quantize_rows": "quantize_rows(Tensor x, ScalarType out_dtype, int activation=0) -> (Tensor, Tensor)",
     "abs_peak": "abs_peak(Tensor x) -> Tensor",
     "fp8_tensor_scale": "fp8_tensor_scale(Tensor x) -> Tensor",
     "fp8_pack": "fp8_pack(Tensor x, Tensor scale) -> Tensor",
@@ -52,8 +52,9 @@ def _rows_view(x: torch.Tensor) -> torch.Tensor:
 
 
 # --------------------------------------------------------------------------- meta
-def _quantize_rows_meta(x, out_dtype):
+def _quantize_rows_meta(x, out_dtype, activation=0):
     _require(x.dtype in (torch.bfloat16, torch.float16), "quantize_rows: BF16/F16 input required")
+    _require(activation in (N.ACT_NONE, N.ACT_GELU_TANH), "quantize_rows: activation must be none or gelu_tanh")
     _require(out_dtype in (torch.float8_e4m3fn, torch.int8), "quantize_rows: out_dtype must be float8_e4m3fn or int8")
     _require(x.dim() >= 1 and x.shape[-1] > 0, "quantize_rows: input needs a non-empty last dimension")
     rows = x.numel() // x.shape[-1]
@@ -184,16 +185,17 @@ def _on_gpu(*ts):
             _require(t.device == dev, "xgen_amd operators require all tensors on the same device")
 
 
-def _quantize_rows_gpu(x, out_dtype):
+def _quantize_rows_gpu(x, out_dtype, activation=0):
+    """Per-row quantization of x, or (activation = ACT_GELU_TANH) of dtype(gelu_tanh(x)) in the same pass."""
     _on_gpu(x)
-    q, scale = _quantize_rows_meta(x, out_dtype)
+    q, scale = _quantize_rows_meta(x, out_dtype, activation)
     if x.numel() == 0:
         return q, scale
     m = _rows_view(x)
-    L = N.lib()
-    st = L.xgen_quantize_rows(N.dtype_code(x.dtype), m.data_ptr(), m.shape[0], m.shape[1], m.stride(0),
+    fn = "xgen_quantize_rows_gelu" if activation == N.ACT_GELU_TANH else "xgen_quantize_rows"
+    st = getattr(N.lib(), fn)(N.dtype_code(x.dtype), m.data_ptr(), m.shape[0], m.shape[1], m.stride(0),
                               N.dtype_code(out_dtype), q.data_ptr(), m.shape[1], scale.data_ptr(), N.stream_of(x))
-    N.check(st, "xgen_quantize_rows")
+    N.check(st, fn)
     return q, scale
 
 
