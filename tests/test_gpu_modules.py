@@ -194,24 +194,39 @@ def test_ffn_pair_gelu_requant(cuda, kind):
     assert torch.equal(sh_gpu.cpu(), sh2)
 
 
-def test_ffn_pair_gelu_in_down_requant(cuda):
-    """H3FP8Linear(input_activation='gelu_tanh') applies the GELU in its input quantization: the
-    down projection of the plain up output equals the down projection of the GELU-epilogue up
-    output, bit for bit."""
+@pytest.mark.parametrize("kind", ["fp8", "int8"])
+def test_ffn_pair_gelu_in_down_requant(cuda, kind):
+    """input_activation='gelu_tanh' (H3FP8Linear, WeightQuantLinearModule) applies the GELU in the
+    module's input quantization: the down projection of the plain up output equals the down
+    projection of the GELU-epilogue up output, bit for bit, also with the gated residual fused."""
+    from xgen_amd import _native as N
     g = workloads.generator(4)
-    M, d = 300, 512
+    M, d, T = 300, 512, 5
     x, _ = workloads.activations(M, d, g)
     wu = (torch.randn(4 * d, d, generator=g) * 0.02).to(torch.bfloat16)
     bu = (torch.randn(4 * d, generator=g) * 0.01).to(torch.bfloat16)
     wd = (torch.randn(d, 4 * d, generator=g) * 0.02).to(torch.bfloat16)
     bd = (torch.randn(d, generator=g) * 0.01).to(torch.bfloat16)
-    opts = dict(weight_scaling="channel", activation_scaling="token")
-    up_gelu = H3FP8Linear(wu, bu, activation="gelu_tanh", **opts).cuda()
-    up = H3FP8Linear(wu, bu, **opts).cuda()
-    down = H3FP8Linear(wd, bd, **opts).cuda()
-    down_gelu = H3FP8Linear(wd, bd, input_activation="gelu_tanh", **opts).cuda()
     xc = x.cuda()[None]
-    y1 = down(up_gelu(xc))
-    y2 = down_gelu(up(xc))
-    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
-    assert "input_activation=gelu_tanh" in repr(down_gelu)
+    if kind == "fp8":
+        opts = dict(weight_scaling="channel", activation_scaling="token")
+        h_gelu = H3FP8Linear(wu, bu, activation="gelu_tanh", **opts).cuda()(xc)
+        h = H3FP8Linear(wu, bu, **opts).cuda()(xc)
+        down = H3FP8Linear(wd, bd, **opts).cuda()
+        down_gelu = H3FP8Linear(wd, bd, input_activation="gelu_tanh", **opts).cuda()
+        assert "input_activation=gelu_tanh" in repr(down_gelu)
+    else:
+        up = WeightQuantLinearModule(wu, bu).cuda()
+        qx, sx = xops.quantize_rows(xc[0], torch.int8)
+        h_gelu = xops.scaled_mm(qx, up.weight, sx, up.antiquant_scale, up.bias, torch.bfloat16, N.ACT_GELU_TANH,
+                                False)[0][None]
+        h = up(xc)
+        down = WeightQuantLinearModule(wd, bd).cuda()
+        down_gelu = WeightQuantLinearModule(wd, bd, input_activation="gelu_tanh").cuda()
+    assert torch.equal(down(h_gelu).view(torch.int16), down_gelu(h).view(torch.int16))
+    res = torch.randn((1, M, d), generator=g).to(torch.bfloat16).cuda()
+    gate = (torch.randn((T, d), generator=g) * 0.1).to(torch.bfloat16).cuda()
+    idx = torch.randint(T, (M,), generator=g).cuda()
+    r1 = down.forward_gate_residual(h_gelu, res, gate, idx)
+    r2 = down_gelu.forward_gate_residual(h, res, gate, idx)
+    assert torch.equal(r1.view(torch.int16), r2.view(torch.int16))

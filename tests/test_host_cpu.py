@@ -9,6 +9,7 @@ import xgen_amd  # noqa: F401  (registers torch.ops.xgen_amd)
 from xgen_amd import config
 from xgen_amd.operator.dit_chain import DiTLinearChain
 from xgen_amd.operator.h3_fp8 import H3FP8Linear
+from xgen_amd.operator.matmul import WeightQuantLinearModule
 from xgen_amd.operator.nq2 import norm_affine_quant
 
 xops = torch.ops.xgen_amd
@@ -32,6 +33,8 @@ def test_input_activation_contract():
     w = torch.zeros(32, 64, dtype=torch.float8_e4m3fn)
     with pytest.raises(ValueError, match="activation_scaling='token'"):
         H3FP8Linear.from_packed(w, torch.ones(()), input_activation="gelu_tanh")
+    with pytest.raises(ValueError, match="unsupported input_activation"):
+        WeightQuantLinearModule(torch.zeros(32, 32), None, input_activation="silu")
     with pytest.raises(ValueError, match="gelu must be"):
         DiTLinearChain(*([torch.zeros(16, 16)] * 8), gelu="both")
 

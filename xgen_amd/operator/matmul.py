@@ -8,6 +8,10 @@ Mirrors x_base/x_base/operator/matmul.py:
       int32 accumulation; dequant acc * pertoken_scale * antiquant_scale + bias
   * enable_weight_quant_linear(model, quant_config, dtype)     matmul.py:141-202
 
+Extension: ``input_activation="gelu_tanh"`` quantizes int8(gelu_tanh(x)) per row in the
+quantizer's pass (the FFN-down input of a GELU FeedForward, hunyuan.py:358): the bytes and
+scales of the up projection's GELU epilogue followed by the plain quantization.
+
 The quantizer is the one the reference restates for the NPU path
 (npu_fusion/f2bc/op_kernel/f2bc_kernel.asc:89-107): scale = amax * fl(1/127),
 q = rint_half_even(x * fl(127/amax)); a zero row gives zeros and scale 0.
@@ -33,8 +37,11 @@ class WeightQuantLinearModule(nn.Module):
     (matmul.py:39-48: quantize on the accelerator, copy to CPU to lower its peak memory); the
     model is moved to its device afterwards."""
 
-    def __init__(self, weight, bias, name=None):
+    def __init__(self, weight, bias, name=None, *, input_activation=None):
         super().__init__()
+        if input_activation not in (None, "gelu_tanh"):
+            raise ValueError(f"unsupported input_activation {input_activation!r}")
+        self.input_activation = input_activation
         w = weight.detach()
         if w.ndim != 2:
             raise ValueError("WeightQuantLinearModule requires a 2-D weight")
@@ -64,9 +71,16 @@ class WeightQuantLinearModule(nn.Module):
         if x.dtype == torch.float32:
             x = x.to(torch.bfloat16)
             ori_dtype = torch.bfloat16
-        x_int8, pertoken_scale = dynamic_quant(x)
+        x_int8, pertoken_scale = self.quantize_input(x)
         out = quant_matmul_raw(x_int8, pertoken_scale, self, ori_dtype)
         return out.reshape(*ori_shape[:-1], -1)
+
+    def quantize_input(self, matrix):
+        """(int8 [M,K], float32 [M]) for a bf16/fp16 [M,K] activation; of gelu_tanh(matrix) with
+        input_activation='gelu_tanh'."""
+        if getattr(self, 'input_activation', None) == "gelu_tanh":
+            return xops.quantize_rows(matrix, torch.int8, N.ACT_GELU_TANH)
+        return dynamic_quant(matrix)
 
     def forward_gate_residual(self, x, residual, gate_table, indices):
         """`residual + bf16(gate_table[indices] * self(x))` with the gated residual in the INT8 GEMM's
@@ -77,7 +91,7 @@ class WeightQuantLinearModule(nn.Module):
         m = x.reshape(-1, x.shape[-1])
         if m.dtype == torch.float32:
             m = m.to(torch.bfloat16)
-        q, s = dynamic_quant(m)
+        q, s = self.quantize_input(m)
         out = xops.scaled_mm_gate_residual(q, self.weight, s.reshape(-1), self.antiquant_scale.reshape(-1), self.bias,
                                            residual.reshape(-1, residual.shape[-1]), gate_table, indices)
         return out.reshape(residual.shape)
