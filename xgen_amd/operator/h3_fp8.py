@@ -143,7 +143,8 @@ class H3FP8Linear(nn.Module):
 
     def forward_quantized(self, packed, scale, out_dtype=torch.bfloat16, activation=None):
         """GEMM on an already quantized activation (shared-QKV pattern,
-        x_diffusers/x_diffusers/framework/transformer/h3_npu_fusion.py:103-119)."""
+        x_diffusers/x_diffusers/framework/transformer/h3_npu_fusion.py:103-119).  input_activation
+        does not apply here: it acts where this module quantizes its own input (quantize_input)."""
         act = _ACTIVATIONS[activation if activation is not None else self.activation]
         out, _ = xops.scaled_mm(packed, self.weight, scale, self.weight_scale.reshape(-1), self.bias,
                                 out_dtype, act, False, self.accumulation == "exact")
