@@ -408,16 +408,18 @@ def dit_chain_fp8(x, scale_tab, shift_tab, indices, weights, eps=1e-6, accumulat
     out-projection on the V third (attention stand-in), FFN up with GELU-tanh (A12) and FFN down,
     each later projection quantizing its own bf16 input per token.  `weights` maps
     qkv/out/ffn_up/ffn_down to (bf16 W [N,K], bf16 bias [N]); weights are quantized per channel.
-    Returns (qkv, out, hidden, y) as bf16 [B*S, N].  accumulate: as in w8a8_linear_fp8; front: an
-    already quantized front-end output (q, token scale) to start from instead of x."""
+    Returns (qkv, out, hidden, y) as bf16 [B*S, N].  accumulate: as in w8a8_linear_fp8, for every
+    projection, or a dict {qkv/out/ffn_up/ffn_down: accumulate}; front: an already quantized
+    front-end output (q, token scale) to start from instead of x."""
     q, s = front if front is not None else norm_affine_quant(x, None, scale_tab, shift_tab, indices, eps,
                                                              "layer", "fp8")[:2]
     packed = {k: quantize_rows_fp8(w) + (b.detach().cpu(),) for k, (w, b) in weights.items()}
     d = x.shape[-1]
+    per_stage = accumulate if isinstance(accumulate, dict) else dict.fromkeys(packed, accumulate)
 
     def lin(qa, sa, name, act=None):
         qw, sw, b = packed[name]
-        return w8a8_linear_fp8(qa, sa, qw, sw, b, torch.bfloat16, act, accumulate)
+        return w8a8_linear_fp8(qa, sa, qw, sw, b, torch.bfloat16, act, per_stage[name])
 
     qkv = lin(q, s, "qkv")
     o = lin(*quantize_rows_fp8(qkv[:, 2 * d:].contiguous()), "out")

@@ -87,7 +87,7 @@ def test_fused_epilogue_equals_gemm_then_op(cuda, kind, B, S, K, Nf):
     assert R.rel_l2(fused, ref) <= 1e-3 and R.cosine(fused, ref) >= 0.9999
 
 
-@pytest.mark.parametrize("kind", ["fp8", "int8"])
+@pytest.mark.parametrize("kind", ["fp8", "fp8_mfma", "int8"])
 def test_module_forward_gate_residual(cuda, kind):
     g = torch.Generator().manual_seed(3)
     B, S, K, Nf = 2, 64, 512, 256
@@ -97,14 +97,17 @@ def test_module_forward_gate_residual(cuda, kind):
     residual = torch.randn((B, S, Nf), generator=g).to(torch.bfloat16).to(cuda)
     gate = (torch.randn((3, Nf), generator=g) * 0.5).to(torch.bfloat16).to(cuda)
     idx = torch.randint(3, (S,), generator=g).to(cuda)
-    m = (H3FP8Linear(w, b, weight_scaling="channel", activation_scaling="token") if kind == "fp8"
-         else WeightQuantLinearModule(w, b)).to(cuda)
+    acc = "mfma" if kind == "fp8_mfma" else "exact"
+    m = (H3FP8Linear(w, b, weight_scaling="channel", activation_scaling="token", accumulation=acc)
+         if kind.startswith("fp8") else WeightQuantLinearModule(w, b)).to(cuda)
     fused = m.forward_gate_residual(x, residual, gate, idx)
     assert torch.equal(u16(fused), u16(gate_residual(residual, m(x), gate, idx)))
 
 
-def test_full_size_out_projection(cuda):
-    """Out-projection [3072 x 3072] at M = 15,624 with the gated residual fused: bit-exact against GEMM-then-op."""
+@pytest.mark.parametrize("accumulation", ["mfma", "exact"])
+def test_full_size_out_projection(cuda, accumulation):
+    """Out-projection [3072 x 3072] at M = 15,624 with the gated residual (fused into the FP8 MFMA
+    kind's epilogue; after the GEMM for the exact kind): bit-exact against GEMM-then-op."""
     M, d = workloads.M_5S, workloads.D_MODEL
     g = workloads.generator(0, cuda)
     x, _ = workloads.activations(M, d, g, cuda)
@@ -112,7 +115,7 @@ def test_full_size_out_projection(cuda):
     residual = torch.randn((1, M, d), generator=g, device=cuda).to(torch.bfloat16)
     gate = (torch.randn((20, d), generator=g, device=cuda) * 0.1).to(torch.bfloat16)
     idx = torch.randint(20, (M,), generator=g, device=cuda)
-    m = H3FP8Linear(w, b, weight_scaling="channel", activation_scaling="token")
+    m = H3FP8Linear(w, b, weight_scaling="channel", activation_scaling="token", accumulation=accumulation)
     fused = m.forward_gate_residual(x[None], residual, gate, idx)
     assert torch.equal(u16(fused), u16(gate_residual(residual, m(x[None]), gate, idx)))
 

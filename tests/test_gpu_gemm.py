@@ -248,3 +248,23 @@ def test_repeated_launches_are_bit_identical(cuda, kind):
         torch.cuda.synchronize()
         for a in accs[1:]:
             assert torch.equal(a.view(torch.int32), accs[0].view(torch.int32))
+
+
+def test_torch_scaled_mm_on_this_gpu_sums_like_the_fp8_mfma(cuda):
+    """What the reference's own call computes here: torch._scaled_mm(..., use_fast_accum=False)
+    (h3_fp8.py:63-66, hipBLASLt on this GPU) against the FP8 MFMA kind's accumulators and the exact
+    sum.  Recorded evidence for the accumulation choice, not parity: the reference's arithmetic is
+    the exact sum (fp8_accumulate_exact), which the default exact kind computes."""
+    qa, sa, qw, sw, _ = quantized_operands(512, 3072, 1024, cuda, "fp8", seed=21)
+    one = torch.ones((), device=cuda)
+    try:
+        ref_call = torch._scaled_mm(qa, qw.t(), scale_a=one, scale_b=one, out_dtype=torch.float32,
+                                    use_fast_accum=False)
+    except (RuntimeError, NotImplementedError) as error:  # not every build has the FP8 GEMM
+        pytest.skip(f"torch._scaled_mm unavailable: {error}")
+    _, acc = xops.scaled_mm(qa, qw, one.reshape(1), one.reshape(1), None, torch.bfloat16, N.ACT_NONE, True)
+    exact = R.fp8_accumulate_exact(qa, qw)
+    to_mfma, to_exact = R.rel_l2(ref_call, acc), R.rel_l2(ref_call, exact)
+    print(f"torch._scaled_mm(use_fast_accum=False): rel-L2 {to_mfma:.2e} from the FP8 MFMA kind, "
+          f"{to_exact:.2e} from the exact sum; MFMA kind from exact {R.rel_l2(acc, exact):.2e}")
+    assert to_mfma < 0.1 * to_exact

@@ -65,7 +65,7 @@ def test_c2_step_replays(cuda):
         torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("accumulation", ["mfma", "exact"])
+@pytest.mark.parametrize("accumulation", [None, "mfma", "exact"])
 def test_chain_replays(cuda, accumulation):
     """The C5 chain's kernels (front end, QKV, requant, out-projection, FFN up, GELU requant, FFN
     down) at S = 700, d = 512 in one graph."""

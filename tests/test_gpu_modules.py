@@ -72,6 +72,28 @@ def test_token_channel_module_c1(cuda, dtype):
     assert R.rel_l2(out, R.cpu_fake_quant_linear_fp8(inp.x, qw, sw, inp.bias)) <= 1e-2
 
 
+def test_default_accumulation_is_exact(cuda):
+    """H3FP8Linear sums exactly by default, as the reference's use_fast_accum=False asks
+    (h3_fp8.py:63-66): its output equals the exact kind's bit for bit and sits at the exactly
+    summed oracle's rounding; accumulation='mfma' is the FP8 MFMA's sum."""
+    inp = workloads.linear_inputs(200, 1024, 512, seed=9)
+    opts = dict(weight_scaling="channel", activation_scaling="token")
+    default = H3FP8Linear(inp.weight, inp.bias, **opts).cuda()
+    fast = H3FP8Linear(inp.weight, inp.bias, accumulation="mfma", **opts).cuda()
+    assert default.accumulation == "exact" and H3FP8Linear.from_packed(default.weight, default.weight_scale).accumulation == "exact"
+    x = inp.x.cuda()
+    qa, sa = R.quantize_rows_fp8(inp.x)
+    qw, sw = default.weight.cpu(), default.weight_scale.cpu()
+    exact = R.w8a8_linear_fp8(qa, sa, qw, sw, inp.bias)
+    y = default(x)
+    assert R.bf16_ulp_diff(y, exact).max() <= 1 and R.rel_l2(y, exact) < 1e-4
+    q, s = xops.quantize_rows(x, torch.float8_e4m3fn)
+    y2, _ = xops.scaled_mm(q, default.weight, s, default.weight_scale, default.bias, torch.bfloat16, 0, False, True)
+    assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
+    model = R.w8a8_linear_fp8(qa, sa, qw, sw, inp.bias, accumulate=R.fp8_mfma_accumulate)
+    assert R.rel_l2(fast(x), model) < 1e-4
+
+
 def test_from_packed_reuses_bytes(cuda):
     inp = workloads.linear_inputs(64, 256, 128, seed=2)
     a = H3FP8Linear(inp.weight, inp.bias).cuda()
@@ -123,17 +145,20 @@ def test_swapper_replaces_selected_linears(cuda):
     assert y.shape == (5, 64) and torch.isfinite(y).all()
 
 
-@pytest.mark.parametrize("kind", ["fp8", "int8"])
+@pytest.mark.parametrize("kind", ["fp8", "fp8_mfma", "int8"])
 def test_shared_qkv_quant_matmul(cuda, kind):
-    """One activation quantization shared by Q, K, V (h3_npu_fusion.py:103-119)."""
+    """One activation quantization shared by Q, K, V (h3_npu_fusion.py:103-119); fp8: the default
+    (exact) accumulation, fp8_mfma: the FP8 MFMA sum."""
+    acc_kind = "mfma" if kind == "fp8_mfma" else "exact"
+    kind = "fp8" if kind.startswith("fp8") else kind
     g = workloads.generator(7)
     x, _ = workloads.activations(130, 512, g)
     layers = []
     for _ in range(3):
         w = (torch.randn(256, 512, generator=g) * 0.02).to(torch.bfloat16)
         b = (torch.randn(256, generator=g) * 0.01).to(torch.bfloat16)
-        layers.append((H3FP8Linear(w, b, weight_scaling="channel", activation_scaling="token") if kind == "fp8"
-                       else WeightQuantLinearModule(w, b)).cuda())
+        layers.append((H3FP8Linear(w, b, weight_scaling="channel", activation_scaling="token",
+                                   accumulation=acc_kind) if kind == "fp8" else WeightQuantLinearModule(w, b)).cuda())
     assert all(quant_linear(m, 512, torch.device("cuda", 0)) for m in layers)
     xs = x.reshape(1, 130, 512).cuda()
     q, s = xops.quantize_rows(xs.reshape(-1, 512), torch.float8_e4m3fn if kind == "fp8" else torch.int8)
@@ -147,7 +172,7 @@ def test_shared_qkv_quant_matmul(cuda, kind):
         # each projection against the oracle linear on the shared (q, scale)
         if kind == "fp8":
             ref = R.w8a8_linear_fp8(q_ref, s_ref, m.weight.cpu(), m.weight_scale.cpu(), m.bias.cpu(),
-                                    accumulate=R.fp8_mfma_accumulate)
+                                    accumulate=R.fp8_mfma_accumulate if m.accumulation == "mfma" else None)
         else:
             ref = R.w8a8_linear_int8(q_ref, s_ref, m.weight.cpu(), m.antiquant_scale.cpu(), m.bias.cpu())
         rel, cos = R.rel_l2(o.reshape(130, 256), ref), R.cosine(o.reshape(130, 256), ref)

@@ -126,9 +126,11 @@ def test_offset_and_constant_rows(cuda, H):
         assert torch.equal(q1[0].view(torch.uint8), q[r].view(torch.uint8)) and torch.equal(s1[0], s[r])
 
 
-def test_full_size_front_end_c5_share(cuda):
-    """LayerNorm(eps 1e-6) + 20-row AdaLN table + per-token FP8 at M=15,624, d=3,072."""
-    M, H = workloads.M_5S, workloads.D_MODEL
+@pytest.mark.parametrize("M", [workloads.M_5S, workloads.M_10S], ids=["c2_share_m15624", "c5_share_m31248"])
+def test_full_size_front_end(cuda, M):
+    """LayerNorm(eps 1e-6) + 20-row AdaLN table + per-token FP8 at one SP8 rank's share of the 5 s
+    clip (M=15,624) and of the 10 s clip (C5, M=31,248), d=3,072."""
+    H = workloads.D_MODEL
     g = workloads.generator(0, cuda)
     x, _ = workloads.activations(M, H, g, cuda)
     shift, scale = workloads.adaln_tables(20, H, g, cuda)

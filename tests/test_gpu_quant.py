@@ -1,4 +1,6 @@
 """GPU parity of the quantizers: bytes and scales bit-exact against the oracle."""
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -126,6 +128,25 @@ def test_pack_with_caller_scale(cuda):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_pack_infinity_in_chunk_without_nan(cuda, dtype):
+    """+-Inf in 8-value chunks that hold no NaN, at power-of-two scales of the per-tensor
+    kernel's form (1.0 from a peak of 448, and the FLT_MIN floor), where the fast division's
+    low reciprocal part is 0: +Inf -> 448 (0x7e), -Inf -> -448 (0xfe), as _pack's clamp gives
+    (h3_fp8_quant.py:13-14)."""
+    x = torch.tensor([float("inf"), 1, 2, 3, 4, 5, 6, -float("inf"),
+                      -1, float("inf"), 0.5, -0.0, 7, 8, 9, 10], dtype=dtype)
+    for peak in (448.0, 0.0):
+        src = torch.zeros(16, dtype=dtype)
+        src[3] = peak
+        scale = xops.fp8_tensor_scale(src.to(cuda))
+        assert scale.item() in (1.0, torch.finfo(torch.float32).tiny)
+        q = xops.fp8_pack(x.to(cuda), scale)
+        want = R.canonical_nan_e4m3((x.float() / scale.cpu()).clamp(-448, 448).to(torch.float8_e4m3fn))
+        assert torch.equal(u8(q), want.view(torch.uint8)), (u8(q).tolist(), want.view(torch.uint8).tolist())
+        assert u8(q)[0].item() == 0x7E and u8(q)[7].item() == 0xFE
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_pack_every_input_value_at_peak_form_scales(cuda, dtype):
     """fp8_pack's fast division applies to scales of the per-tensor kernel's form,
     max(RN(a / 448), FLT_MIN) for an input value a (what fp8_tensor_scale gives, and a MAX
@@ -192,10 +213,33 @@ def test_kernel_gelu_within_ulp_of_torch(kernel_gelu, dtype):
     assert got[x == float("inf")].item() == float("inf")
     body = fin & (x.float() > -3)
     assert R.bf16_ulp_diff(got[body], ref[body]).max() <= 1
-    tail = fin & (x.float() <= -3)
-    assert (got[tail].float() - ref[tail].float()).abs().max() <= 1e-3
     tiny = fin & (x.float().abs() < 2.0 ** -60)
     assert torch.equal(got[tiny].view(torch.int16), (x[tiny].float() * 0.5).to(dtype).view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_kernel_gelu_tail_within_ulp_of_float64(kernel_gelu, dtype):
+    """The negative tail (x <= -3), where torch's float32 (and, below about -7, float64)
+    0.5x(1 + tanh z) cancels: within 1 ulp of the output dtype of GELU-tanh evaluated in float64
+    as x / (1 + exp(-2z)) (the identity 0.5(1 + tanh z) = 1 / (1 + exp(-2z)); that float64 form is
+    first held to torch's float64 tanh form, 1e-11 relative, above -3 where the latter does not cancel).
+    Exception: the five bf16 inputs in [-10.3125, -10.0625], whose GELU lies below 2^-124 — the
+    kernel's float32 exp2 of 2z·log2(e) overflows there and it returns -0."""
+    x = torch.arange(1 << 16, dtype=torch.int32).to(torch.int16).view(dtype)
+    fin = torch.isfinite(x)
+    xd = x[fin].double()
+    z = math.sqrt(2.0 / math.pi) * (xd + 0.044715 * xd ** 3)
+    exact = xd / (1.0 + torch.exp(-2.0 * z))
+    plain = xd > -3
+    torch_tanh = torch.nn.functional.gelu(xd[plain], approximate="tanh")
+    assert ((exact[plain] - torch_tanh).abs() <= 1e-11 * torch_tanh.abs()).all()
+    got = kernel_gelu(x)[fin]
+    tail = xd <= -3
+    want = exact.to(dtype)
+    under = tail & (exact.abs() < 2.0 ** -124) & (want != 0)
+    assert R.bf16_ulp_diff(got[tail & ~under], want[tail & ~under]).max() <= 1
+    assert torch.equal(got[under].view(torch.int16), torch.full_like(got[under], -0.0).view(torch.int16))
+    assert int(under.sum()) == (5 if dtype == torch.bfloat16 else 0)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])

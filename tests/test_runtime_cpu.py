@@ -5,6 +5,7 @@ Kernels' fallbacks, and the signatures the block calls."""
 import inspect
 import logging
 
+import pytest
 import torch
 from torch import nn
 
@@ -111,3 +112,14 @@ def test_kernels_fall_back_off_device():
         assert k.get(feature, x) is None
     reasons = {f: r for (f, r) in d.fallbacks}
     assert "gfx950" in reasons["swiglu"]
+
+
+def test_quant_linear_refuses_input_activation():
+    """A linear whose own input quantization applies GELU-tanh cannot consume the block's shared
+    plain (q, scale): quant_linear is False (the block then calls the module, and records the
+    fallback) and quant_matmul refuses it instead of silently skipping the GELU."""
+    w = torch.zeros(32, 64, dtype=FP8)
+    gelu_in = H3FP8Linear.from_packed(w, torch.ones(32), activation_scaling="token", input_activation="gelu_tanh")
+    assert not runtime.quant_linear(gelu_in, 64)
+    with pytest.raises(ValueError, match="input_activation"):
+        runtime.quant_matmul(torch.zeros(4, 64, dtype=FP8), torch.ones(4), gelu_in, (4, 64))

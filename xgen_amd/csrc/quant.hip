@@ -304,8 +304,10 @@ __device__ __forceinline__ bool peak_form_scale(float s) {
 // operations, whose e4m3 byte equals IEEE division's for every input value not
 // above the peak a behind the scale (the oracle's exhaustive check over all
 // (x, a) pairs); larger values give quotients above 448 either way, which the
-// clamp maps to 448.  Any other scale, and chunks holding a NaN, use IEEE
-// division (NaN -> 0x7f).
+// clamp maps to 448.  Any other scale, and chunks holding a NaN or an infinity,
+// use IEEE division (NaN -> 0x7f, +-Inf -> +-448): the two-operation form
+// computes fma(x, r, x * r_lo), which is NaN for an infinite x when r_lo = 0
+// (a power-of-two scale such as 1.0 or FLT_MIN).
 template <int DT>
 __global__ __launch_bounds__(kThreads) void fp8_pack_kernel(const uint8_t *__restrict__ x,
                                                             int64_t numel,
@@ -314,7 +316,7 @@ __global__ __launch_bounds__(kThreads) void fp8_pack_kernel(const uint8_t *__res
   const float s = scale[0];
   const bool fast = peak_form_scale<DT>(s);
   const RowQuant p = fp8_scale_params(s);
-  // a 16-bit magnitude above infinity's is a NaN
+  // a 16-bit magnitude at or above infinity's is an infinity or a NaN
   constexpr uint32_t kInfBits = DT == XGEN_DTYPE_BF16 ? 0x7f80u : 0x7c00u;
   const int64_t nchunks = numel >> 3;
   for (int64_t ci = (int64_t)blockIdx.x * kThreads + threadIdx.x; ci < nchunks;
@@ -323,7 +325,7 @@ __global__ __launch_bounds__(kThreads) void fp8_pack_kernel(const uint8_t *__res
     float v[8];
     unpack8<DT>(c, v);
     u32x2 r;
-    if (fast && hmax_u16x2(absmax_chunk<DT>(c, u16x2{0, 0})) <= kInfBits) {
+    if (fast && hmax_u16x2(absmax_chunk<DT>(c, u16x2{0, 0})) < kInfBits) {
       float qv[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) qv[i] = clamp448(div_by_row_scale(v[i], p.mul, p.mul_lo));

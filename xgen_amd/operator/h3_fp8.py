@@ -13,13 +13,15 @@ one scale per token: the W8A8 layout of the DiT linear path.  The GEMM and its
 dequant / bias / optional GELU-tanh epilogue are one HIP kernel; rows need no
 padding to 16 (the reference pads, h3_fp8.py:58-59).
 
-``accumulation`` picks how the K sums are formed.  "mfma" (default) uses
-gfx950's FP8 MFMA, whose sum truncates each product of a group of 8
-consecutive K to a multiple of 2^(E - 13), E the group's largest exponent sum
-(torch._scaled_mm computes the same on this GPU).  "exact" multiplies the same
-e4m3fn bytes exactly on the bf16 MFMA and sums in fp32: the accumulation the
-reference requests with use_fast_accum=False (h3_fp8.py:63-66), at twice the
-matrix-core time.
+``accumulation`` picks how the K sums are formed.  "exact" (default) multiplies
+the e4m3fn bytes exactly on the bf16 MFMA and sums in fp32: the accumulation
+the reference requests with use_fast_accum=False (h3_fp8.py:63-66), at about
+twice the matrix-core time.  "mfma" is the opt-in fast sum, the counterpart of
+use_fast_accum=True: gfx950's FP8 MFMA, whose sum truncates each product of a
+group of 8 consecutive K to a multiple of 2^(E - 13), E the group's largest
+exponent sum.  One linear's bf16 output then sits at rel-L2 ~4e-4 of the
+exactly summed result; a chain of per-token requantizations amplifies that
+(DiTLinearChain picks the kind per projection).
 """
 from __future__ import annotations
 
@@ -72,10 +74,11 @@ def _check_input_activation(input_activation, activation_scaling):
 
 
 class H3FP8Linear(nn.Module):
-    """Keep FP8 weights; quantize activations to E4M3 and run the FP8 MFMA GEMM."""
+    """Keep FP8 weights; quantize activations to E4M3 and run the W8A8 GEMM (exact products summed
+    in fp32 by default, or the FP8 MFMA's sum)."""
 
     def __init__(self, weight, bias=None, *, weight_scaling: str = "tensor",
-                 activation_scaling: str = "tensor", activation: str | None = None, accumulation: str = "mfma",
+                 activation_scaling: str = "tensor", activation: str | None = None, accumulation: str = "exact",
                  input_activation: str | None = None):
         super().__init__()
         if weight.ndim != 2 or weight.shape[0] % 16 or weight.shape[1] % 16:
@@ -102,7 +105,7 @@ class H3FP8Linear(nn.Module):
 
     @classmethod
     def from_packed(cls, weight, scale, bias=None, *, activation_scaling: str = "tensor",
-                    activation: str | None = None, accumulation: str = "mfma", input_activation: str | None = None):
+                    activation: str | None = None, accumulation: str = "exact", input_activation: str | None = None):
         """Reuse already quantized bytes and their original scale(s) without requantization."""
         if weight.dtype != torch.float8_e4m3fn or weight.ndim != 2 or any(n % 16 for n in weight.shape):
             raise ValueError('Packed H3 FP8 projection requires an aligned E4M3 matrix')
@@ -155,16 +158,21 @@ class H3FP8Linear(nn.Module):
         """`residual + bf16(gate_table[indices] * self(x))` with the gated residual in the GEMM's
         epilogue (the out-projection / FFN-down of a DiT block followed by
         x_base/x_base/operator/h3_indexed_affine.py:58-61).  x: bf16/fp16 [B, S, K]; residual bf16
-        [B, S, N]; gate_table bf16 [T, N]; indices int64 [S].  Per-token activation scaling only."""
-        if self.activation_scaling != "token" or _ACTIVATIONS[self.activation] != N.ACT_NONE \
-                or self.accumulation != "mfma":
-            raise ValueError("forward_gate_residual needs activation_scaling='token', no activation and "
-                             "accumulation='mfma'")
+        [B, S, N]; gate_table bf16 [T, N]; indices int64 [S].  Per-token activation scaling only.
+        The FP8 MFMA kind runs it as one kernel; the exact kind as its GEMM followed by the
+        gated residual kernel (the same bytes as a fused form would give)."""
+        if self.activation_scaling != "token" or _ACTIVATIONS[self.activation] != N.ACT_NONE:
+            raise ValueError("forward_gate_residual needs activation_scaling='token' and no activation")
         if x.dim() != 3 or residual.shape != (*x.shape[:-1], self.out_features):
             raise ValueError("forward_gate_residual: x [B,S,K] and residual [B,S,N] required")
         packed, scale = self.quantize_input(x.reshape(-1, x.shape[-1]))
-        out = xops.scaled_mm_gate_residual(packed, self.weight, scale, self.weight_scale.reshape(-1), self.bias,
-                                           residual.reshape(-1, self.out_features), gate_table, indices)
+        if self.accumulation == "exact":
+            branch, _ = xops.scaled_mm(packed, self.weight, scale, self.weight_scale.reshape(-1), self.bias,
+                                       torch.bfloat16, N.ACT_NONE, False, True)
+            out = xops.gate_residual(residual, branch.reshape(residual.shape), gate_table, indices)
+        else:
+            out = xops.scaled_mm_gate_residual(packed, self.weight, scale, self.weight_scale.reshape(-1), self.bias,
+                                               residual.reshape(-1, self.out_features), gate_table, indices)
         self.calls += 1
         return out.reshape(residual.shape)
 

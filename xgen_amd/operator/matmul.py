@@ -7,6 +7,9 @@ Mirrors x_base/x_base/operator/matmul.py:
       fp32 input cast to bf16; per-token int8 quantization; int8 GEMM with exact
       int32 accumulation; dequant acc * pertoken_scale * antiquant_scale + bias
   * enable_weight_quant_linear(model, quant_config, dtype)     matmul.py:141-202
+  * MatmulManager.enable_online_dynamic_quant / matmul_manager  matmul.py:300-348, 423
+      the installer --matmul_quant int8 calls (x_diffusers/x_diffusers/adaptor/load_pipe.py:555-558)
+      and the name x_base/x_base/operator/__init__.py:2 imports
 
 Extension: ``input_activation="gelu_tanh"`` quantizes int8(gelu_tanh(x)) per row in the
 quantizer's pass (the FFN-down input of a GELU FeedForward, hunyuan.py:358): the bytes and
@@ -18,12 +21,17 @@ q = rint_half_even(x * fl(127/amax)); a zero row gives zeros and scale 0.
 """
 from __future__ import annotations
 
+import gc
+import logging
+
 import torch
 from torch import nn
 
 from .. import _native as N
-from ..config import QuantLayerConfig
+from ..config import QuantLayerConfig, detect_config_name, get_config
 from ..ops import xops
+
+LOG = logging.getLogger(__name__)
 
 
 def dynamic_quant(x: torch.Tensor):
@@ -128,3 +136,48 @@ def enable_weight_quant_linear(model: nn.Module, quant_config: QuantLayerConfig,
         else:
             setattr(model, clean_name, quant_module)
     return model
+
+
+def _rank() -> int:
+    dist = torch.distributed
+    return dist.get_rank() if dist.is_available() and dist.is_initialized() else 0
+
+
+class MatmulManager:
+    """The quantization installer object of the reference's pipelines (matmul.py:300-423).
+
+    Only the transformer's W8A8 linears are this path: the VAE installers of the reference
+    (Conv3D through closed NPU operators, the VAE decoder's linears) are not provided and say
+    so when called."""
+
+    def enable_online_dynamic_quant(self, transformer, quant_config: QuantLayerConfig | None = None,
+                                    dtype: str = 'w8a8'):
+        """Swap the selected nn.Linear layers of `transformer` for WeightQuantLinearModule in place
+        and return it.  quant_config None: the model's own rule set, chosen from its class
+        (xgen_amd.config.detect_config_name).  As in the reference, any failure surfaces as
+        ValueError (the cause chained) after being logged."""
+        rank = _rank()
+        try:
+            if quant_config is None:
+                name = detect_config_name(transformer)
+                quant_config = get_config(name)
+                LOG.info("rank %d: quant config %r detected for %s", rank, name, type(transformer).__name__)
+            LOG.info("rank %d: replacing linears by W8A8 modules", rank)
+            model = enable_weight_quant_linear(transformer, quant_config, dtype=dtype)
+            gc.collect()
+            if torch.cuda.is_available():
+                torch.cuda.empty_cache()
+        except Exception as error:
+            LOG.error("W8A8 installation failed: %s", error)
+            raise ValueError("Dynamic weight modify model failed. Please try running the program again.") from error
+        LOG.info("rank %d: W8A8 linears installed", rank)
+        return model
+
+    def enable_vae_conv3d_quant(self, vae):
+        raise NotImplementedError("xgen_amd: VAE Conv3D quantization is outside the W8A8 DiT linear path")
+
+    def enable_vae_linear_quant(self, vae, dtype='int8'):
+        raise NotImplementedError("xgen_amd: VAE linear quantization is outside the W8A8 DiT linear path")
+
+
+matmul_manager = MatmulManager()
