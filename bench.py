@@ -56,7 +56,8 @@ def parse():
     return p.parse_args()
 
 
-PROFILE_KERNELS = ("gemm_fp8_qkv", "gemm_int8_qkv", "gemm_fp8_ffn_up_gelu", "gemm_fp8_ffn_up", "gemm_fp8_ffn_down",
+PROFILE_KERNELS = ("gemm_fp8_qkv", "gemm_fp8_qkv_exact", "gemm_int8_qkv", "gemm_fp8_ffn_up_gelu", "gemm_fp8_ffn_up",
+                   "gemm_fp8_ffn_down",
                    "quant_rows_fp8", "requant_fp8_12288", "requant_gelu_fp8_12288", "front_end_ln_mod_quant_fp8", "gate_residual_op", "swiglu_quant_int8_h3",
                    "wire_encode_h3", "wire_decode_h3", "copy_1gib")
 
@@ -114,15 +115,16 @@ def profile_kernels(names, steps, warmup):
         if name not in PROFILE_KERNELS:
             raise SystemExit(f"unknown kernel {name}; choose from {PROFILE_KERNELS}")
         if name.startswith("gemm"):
-            lin = {"gemm_fp8_qkv": "qkv", "gemm_int8_qkv": "qkv", "gemm_fp8_ffn_up_gelu": "ffn_up",
-                   "gemm_fp8_ffn_up": "ffn_up", "gemm_fp8_ffn_down": "ffn_down"}[name]
+            lin = {"gemm_fp8_qkv": "qkv", "gemm_fp8_qkv_exact": "qkv", "gemm_int8_qkv": "qkv",
+                   "gemm_fp8_ffn_up_gelu": "ffn_up", "gemm_fp8_ffn_up": "ffn_up", "gemm_fp8_ffn_down": "ffn_down"}[name]
             w, b = W.weight(lin, g, dev)
             dt = torch.int8 if "int8" in name else fp8
             a_in = x if lin != "ffn_down" else torch.randn((M, 4 * K), generator=g, device=dev).to(torch.bfloat16)
             qa, sa = xops.quantize_rows(a_in, dt)
             qw, sw = xops.quantize_rows(w, dt)
             act = N.ACT_GELU_TANH if "gelu" in name else N.ACT_NONE
-            fn = lambda: xops.scaled_mm(qa, qw, sa, sw, b, torch.bfloat16, act, False)  # noqa: E731
+            exact = name.endswith("_exact")
+            fn = lambda: xops.scaled_mm(qa, qw, sa, sw, b, torch.bfloat16, act, False, exact)  # noqa: E731
         elif name == "quant_rows_fp8":
             fn = lambda: xops.quantize_rows(nxt(), fp8)  # noqa: E731
         elif name in ("requant_fp8_12288", "requant_gelu_fp8_12288"):  # FFN-down input: [M, 4d] bf16, 576 MB

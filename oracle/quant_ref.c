@@ -23,6 +23,10 @@
  *                            (r_hi = 1/s rounded toward zero, r_lo =
  *                            RN((1 - s*r_hi) * r_hi), q = RN(x*r_hi + RN(x*r_lo)))
  *                            gives the same e4m3 byte as IEEE x / s.
+ *  oracle_check_scale_division  exhaustive check, for every 16-bit amax, that the
+ *                            row scale amax / 448 computed in two operations
+ *                            (amax * r_hi + RN(amax * r_lo) with r_hi, r_lo of 448)
+ *                            is the IEEE quotient bit for bit.
  *  oracle_check_wire_division   the same check for the FP8 wire codec's scale
  *                            s = max(amax / 448, 1e-12) (phaa/fp8_transport.py:52),
  *                            whose kernels always take the fast division.
@@ -186,6 +190,30 @@ int64_t oracle_check_fast_division(int fmt, uint32_t amax_lo, uint32_t amax_hi) 
         if (oracle_e4m3_encode(ref) != oracle_e4m3_encode(got)) ++bad;
       }
     }
+  }
+  return bad;
+}
+
+/* Row scale max(amax / 448, FLT_MIN) as the HIP kernels form it: for amax >=
+ * 2^-90 the quotient in two operations, q = row_div(amax, r_hi, r_lo) with
+ * r_hi, r_lo = row_reciprocal(448) (r_hi = 1/448 rounded toward zero); below
+ * 2^-90 (where amax * r_lo would lose bits to underflow) IEEE division; then
+ * the clamp (NaN stays NaN).  Every 16-bit pattern of format fmt (both signs,
+ * zeros, subnormals, infinities and NaN): count of patterns whose float32 bits
+ * differ from the IEEE form (NaN compares as NaN).  *r_hi_out / *r_lo_out
+ * receive the constants. */
+int64_t oracle_check_scale_division(int fmt, float *r_hi_out, float *r_lo_out) {
+  float r_hi, r_lo;
+  row_reciprocal(448.0f, &r_hi, &r_lo);
+  *r_hi_out = r_hi;
+  *r_lo_out = r_lo;
+  int64_t bad = 0;
+  for (uint32_t ab = 0; ab <= 0xffffu; ++ab) {
+    const float amax = oracle_half_to_f32(fmt, (uint16_t)ab);
+    float ref = amax / 448.0f, got = amax < 0x1p-90f ? amax / 448.0f : row_div(amax, r_hi, r_lo);
+    ref = ref < FLT_MIN ? FLT_MIN : ref;
+    got = got < FLT_MIN ? FLT_MIN : got;
+    if (isnan(ref) ? !isnan(got) : bits_of_f32(ref) != bits_of_f32(got)) ++bad;
   }
   return bad;
 }

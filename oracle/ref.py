@@ -86,6 +86,8 @@ def clib() -> ctypes.CDLL:
         L.oracle_quant_rows_int8.argtypes = L.oracle_quant_rows_fp8.argtypes
         L.oracle_check_fast_division.restype = ctypes.c_int64
         L.oracle_check_fast_division.argtypes = [ctypes.c_int, ctypes.c_uint32, ctypes.c_uint32]
+        L.oracle_check_scale_division.restype = ctypes.c_int64
+        L.oracle_check_scale_division.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
         L.oracle_check_wire_division.restype = ctypes.c_int64
         L.oracle_check_wire_division.argtypes = [ctypes.c_int, ctypes.c_uint32, ctypes.c_uint32]
         L.oracle_fp8_mfma_gemm.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,

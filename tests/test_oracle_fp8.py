@@ -142,3 +142,22 @@ def test_fast_division_exhaustive(fmt, hi):
         bad = sum(pool.map(lambda i: L.oracle_check_fast_division(fmt, int(bounds[i]), int(bounds[i + 1] - 1)),
                            range(8)))
     assert bad == 0
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+def test_row_scale_two_operation_division_exhaustive(fmt):
+    """The kernels' row scale max(amax / 448, FLT_MIN) (fp8_row_scale in xgen_common.h): the
+    quotient as amax * r_hi + RN(amax * r_lo) with the constants of 1/448 (IEEE division below
+    2^-90) equals IEEE division + clamp for every 16-bit amax (bf16 and f16, both signs, zeros,
+    subnormals, infinities, NaN); and the kernel's constants are the oracle's."""
+    import ctypes
+    import re
+    from tests.conftest import ROOT
+    L = R.clib()
+    r_hi, r_lo = ctypes.c_float(), ctypes.c_float()
+    assert L.oracle_check_scale_division(fmt, ctypes.byref(r_hi), ctypes.byref(r_lo)) == 0
+    header = (ROOT / "xgen_amd" / "csrc" / "xgen_common.h").read_text()
+    m = re.search(r"kInv448Hi = (0x[0-9a-fp.+-]+)f, kInv448Lo = (0x[0-9a-fp.+-]+)f", header)
+    assert m and float.fromhex(m.group(1)) == r_hi.value and float.fromhex(m.group(2)) == r_lo.value
+    # the constants are 1/448 split: r_hi rounded toward zero, r_hi + r_lo within 2^-45 relative
+    assert r_hi.value <= 1 / 448 and abs((r_hi.value + r_lo.value) * 448 - 1) < 2.0 ** -45

@@ -234,8 +234,9 @@ __device__ __forceinline__ void norm_rows(const NormArgs &a, RedSlots (&red)[2])
   u32x4 c[CH], cn[CH];
   int64_t g;
   int parity = 0;  // LDS reduction slots of this step
-  // one row (base: the workgroup's first row of this step)
-  auto row_step = [&](int64_t base) {
+  // one row (base: the workgroup's first row of this step) from x chunks c, loading the next
+  // row's into cn (the loop alternates the two buffers: no register copies between rows)
+  auto row_step = [&](int64_t base, u32x4 (&c)[CH], u32x4 (&cn)[CH]) {
     const uint32_t row = clamp_row(base + wave / WPR);
     const bool g_ok = g >= 0 && g < a.table_rows;  // uniform over the wave (one row per wave)
 
@@ -360,15 +361,16 @@ __device__ __forceinline__ void norm_rows(const NormArgs &a, RedSlots (&red)[2])
     const uint32_t amax_bits = row_max_u32<WPR>(__float_as_uint(am) & 0x7fffffffu, wave, lane, red[parity].amax);
 
     // quantize from registers; a row whose index is outside the table is
-    // poisoned (NaN scale; NaN bytes for E4M3, zeros for I8; zero normed row)
-    const float amax = __uint_as_float(amax_bits);
+    // poisoned: its amax is taken as NaN, so the scale is NaN and the row
+    // quantizer's non-finite path writes NaN bytes (E4M3) or zeros (I8); its
+    // normed row is zeros
+    const float amax = g_ok ? __uint_as_float(amax_bits) : __builtin_nanf("");
     const RowQuant p = (OUT == XGEN_DTYPE_E4M3) ? fp8_row_params(amax) : i8_row_params(amax);
-    const u32x2 bad = (OUT == XGEN_DTYPE_E4M3) ? u32x2{0x7f7f7f7fu, 0x7f7f7f7fu} : u32x2{0u, 0u};
     const __amdgpu_buffer_rsrc_t rq = rsrc(a.q + (int64_t)row * a.width, a.width);
     const __amdgpu_buffer_rsrc_t rn = rsrc(NORMED ? a.normed + (int64_t)row * row_bytes : a.q, NORMED ? row_bytes : 0);
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
-      const u32x2 qb = g_ok ? quant8<OUT>(m[j], p) : bad;
+      const u32x2 qb = quant8<OUT>(m[j], p);
       // a chunk past the end: its offset stays past the row's bytes, the stores are dropped
       __builtin_amdgcn_raw_buffer_store_b64(qb, rq, in_off(j) >> 1, 0, 0);
       if constexpr (NORMED) {
@@ -380,9 +382,7 @@ __device__ __forceinline__ void norm_rows(const NormArgs &a, RedSlots (&red)[2])
                                                in_off(j), 0, 0);
       }
     }
-    a.token_scale[row] = g_ok ? p.s : __builtin_nanf("");  // every lane of the row: the same value
-#pragma unroll
-    for (int j = 0; j < CH; ++j) c[j] = cn[j];
+    a.token_scale[row] = p.s;  // every lane of the row: the same value
     g = gn;
     parity ^= 1;
   };
@@ -395,8 +395,12 @@ __device__ __forceinline__ void norm_rows(const NormArgs &a, RedSlots (&red)[2])
   __builtin_amdgcn_sched_barrier(0);
   load_tables(g);
   if (base >= a.rows) return;
-  row_step(base);  // peeled: the loop is then entered with the pending accesses of a step
-  for (base += step; base < a.rows; base += step) row_step(base);
+  row_step(base, c, cn);  // peeled: the loop is then entered with the pending accesses of a step
+  for (base += step; base < a.rows; base += 2 * step) {
+    row_step(base, cn, c);
+    if (base + step >= a.rows) break;
+    row_step(base + step, c, cn);
+  }
 }
 
 template <int NORM, int OUT, int WT, int WPR, int CH>

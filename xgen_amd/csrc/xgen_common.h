@@ -261,24 +261,42 @@ __device__ __forceinline__ RowQuant fp8_scale_params(float s) {
   RowQuant p;
   p.s = canonical_nan(s);
   p.finite = __builtin_isfinite(s);
-  // r = RN(1/s) is a positive normal for a finite s >= FLT_MIN; the residual
-  // 1 - s*r is exact with an FMA; a negative one means r > 1/s: one ulp down.
-  float r = 1.0f / s;
+  // r_hi = 1/s rounded toward zero.  v_rcp_f32 is within one ulp of 1/s (a
+  // positive normal for a finite s >= FLT_MIN) and the residual 1 - s*r of an
+  // FMA is exact: a negative one means r > 1/s (one ulp down); otherwise r goes
+  // one ulp up when that value is still <= 1/s.
+  float r = __builtin_amdgcn_rcpf(s);
   float e = __builtin_fmaf(-s, r, 1.0f);
-  if (p.finite && e < 0.0f) {
+  if (e < 0.0f) {
     r = __uint_as_float(__float_as_uint(r) - 1u);
     e = __builtin_fmaf(-s, r, 1.0f);
+  } else {
+    const float r1 = __uint_as_float(__float_as_uint(r) + 1u);
+    const float e1 = __builtin_fmaf(-s, r1, 1.0f);
+    if (e1 >= 0.0f) r = r1, e = e1;
   }
   p.mul = r;
   p.mul_lo = e * r;
   return p;
 }
 
-__device__ __forceinline__ RowQuant fp8_row_params(float amax) {
-  float s = amax / kE4M3Max;
-  s = (s < kFltMin) ? kFltMin : s;  // clamp_min keeps NaN
-  return fp8_scale_params(s);
+// 1/448 as r_hi + r_lo (r_hi rounded toward zero, r_lo = RN((1 - 448 r_hi) r_hi)),
+// the division by the row scale's constant in div_by_row_scale's form.
+constexpr float kInv448Hi = 0x1.249248p-9f, kInv448Lo = 0x1.249248p-33f;
+
+// max(amax / 448, FLT_MIN) for a 16-bit amax (bf16 or f16 value), the FP8 row
+// scale (h3_fp8.py:11 per row): the quotient in two operations, bit-identical to
+// IEEE division for every 16-bit amax after the clamp (the oracle's exhaustive
+// check); below 2^-90, where amax * r_lo would lose bits to underflow, IEEE
+// division (a branch that is uniform wherever a wave quantizes one row).
+__device__ __forceinline__ float fp8_row_scale(float amax) {
+  float s;
+  if (__builtin_expect(amax < 0x1p-90f, 0)) s = amax / kE4M3Max;
+  else s = div_by_row_scale(amax, kInv448Hi, kInv448Lo);
+  return (s < kFltMin) ? kFltMin : s;  // clamp_min keeps NaN
 }
+
+__device__ __forceinline__ RowQuant fp8_row_params(float amax) { return fp8_scale_params(fp8_row_scale(amax)); }
 
 __device__ __forceinline__ RowQuant i8_row_params(float amax) {
   RowQuant p;
