@@ -8,10 +8,10 @@ no code with xgen_amd (tests/test_oracle_mfma.py).  Runs on an MI355X:
     python tests/golden/make_blas_fixture.py
 
 Contents (e4m3fn codes as uint8, sums as float32):
-  rowq_a [32,3072], rowq_w [96,3072], rowq_acc [32,96]   operands from the per-row FP8
+  rowq_a [16,3072], rowq_w [32,3072], rowq_acc [16,32]   operands from the per-row FP8
       quantizer's arithmetic (N(0,1) activations with a x50 outlier channel, N(0,0.02)
       weights; quantized on the CPU by the oracle)
-  gelu_a [32,12288], gelu_w [48,12288], gelu_acc [32,48]  FFN-down-like operands: the
+  gelu_a [8,12288], gelu_w [16,12288], gelu_acc [8,16]    FFN-down-like operands: the
       quantized GELU-tanh of N(0,1) activations against N(0,0.02) weights, K = 12,288
 """
 from __future__ import annotations
@@ -41,13 +41,13 @@ def blas(qa: torch.Tensor, qw: torch.Tensor) -> np.ndarray:
 
 def main() -> None:
     g = torch.Generator().manual_seed(2026)
-    x = torch.randn((32, 3072), generator=g)
+    x = torch.randn((16, 3072), generator=g)
     x[:, 1234] *= 50
     qa, _ = R.quantize_rows_fp8(x.to(torch.bfloat16))
-    qw, _ = R.quantize_rows_fp8((torch.randn((96, 3072), generator=g) * 0.02).to(torch.bfloat16))
-    h = torch.nn.functional.gelu(torch.randn((32, 12288), generator=g), approximate="tanh")
+    qw, _ = R.quantize_rows_fp8((torch.randn((32, 3072), generator=g) * 0.02).to(torch.bfloat16))
+    h = torch.nn.functional.gelu(torch.randn((8, 12288), generator=g), approximate="tanh")
     qh, _ = R.quantize_rows_fp8(h.to(torch.bfloat16))
-    qd, _ = R.quantize_rows_fp8((torch.randn((48, 12288), generator=g) * 0.02).to(torch.bfloat16))
+    qd, _ = R.quantize_rows_fp8((torch.randn((16, 12288), generator=g) * 0.02).to(torch.bfloat16))
     u8 = lambda t: t.view(torch.uint8).numpy()  # noqa: E731
     np.savez_compressed(HERE / "fp8_blas_gemm.npz",
                         rowq_a=u8(qa), rowq_w=u8(qw), rowq_acc=blas(qa, qw),

@@ -157,17 +157,25 @@ def test_adaln_one_plus_matches_eager_bf16(cuda):
 
 @pytest.mark.parametrize("norm", ["layer", "rms"])
 @pytest.mark.parametrize("out", ["fp8", "int8"])
-@pytest.mark.parametrize("H", [1024, 3072, 5376])
-def test_prepared_one_plus_scale_is_bit_identical(cuda, norm, out, H):
-    """scale_is_one_plus=True with bf16(1 + scale) gives the same bytes, scales and rows as the plain call."""
+@pytest.mark.parametrize("H", [1000, 1024, 3072, 5376, 8192])
+@pytest.mark.parametrize("wdtype", [None, torch.bfloat16, torch.float32])
+def test_prepared_one_plus_scale_is_bit_identical(cuda, norm, out, H, wdtype):
+    """scale_is_one_plus=True with bf16(1 + scale) gives the same bytes, scales and rows as the plain
+    call, with and without a norm weight; an index outside the table poisons its row (NaN scale)
+    in both forms."""
     from xgen_amd.operator.nq2 import adaln_one_plus
     x, scale, shift, idx = inputs(2, 41, H, 7, seed=H, dev=cuda)
+    idx = idx.clone()
+    idx[5] = 7  # outside the table
+    w = None if wdtype is None else (torch.randn(H, generator=torch.Generator().manual_seed(2)) * 0.3 + 1).to(
+        wdtype).to(cuda)
     dt = torch.float8_e4m3fn if out == "fp8" else torch.int8
     eps = 1e-6 if norm == "layer" else 1e-5
-    q0, s0, m0 = norm_affine_quant(x, None, scale, shift, idx, eps=eps, norm=norm, out_dtype=dt, return_normed=True)
+    q0, s0, m0 = norm_affine_quant(x, w, scale, shift, idx, eps=eps, norm=norm, out_dtype=dt, return_normed=True)
     f = adaln_one_plus(scale)
-    q1, s1, m1 = norm_affine_quant(x, None, f, shift, idx, eps=eps, norm=norm, out_dtype=dt, return_normed=True,
+    q1, s1, m1 = norm_affine_quant(x, w, f, shift, idx, eps=eps, norm=norm, out_dtype=dt, return_normed=True,
                                    scale_is_one_plus=True)
     assert torch.equal(q0.view(torch.uint8), q1.view(torch.uint8))
-    assert torch.equal(s0, s1)
+    assert torch.equal(s0.view(torch.int32), s1.view(torch.int32))
     assert torch.equal(m0.view(torch.int16), m1.view(torch.int16))
+    assert torch.isnan(s0[5]) and torch.isnan(s0[41 + 5]) and not torch.isnan(s0[4])
