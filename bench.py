@@ -432,6 +432,21 @@ def main():
             "frac_of_fp8_peak": flop / (ms_ex * 1e-3) / 1e12 / PEAK_FP8_TFLOPS,
             "frac_of_bf16_peak": flop / (ms_ex * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}
 
+    # ---- the reference's own GEMM call on this GPU: torch._scaled_mm (hipBLASLt) on the same QKV
+    # operands, per-tensor scales + bias (h3_fp8.py:63-66) and row-wise scales (this path's semantics)
+    if want("hipblaslt"):
+        ref_mm = {}
+        one = torch.ones((), device=dev)
+        for label, sa_t, sw_t in (("per_tensor", one, one), ("rowwise", sa0.reshape(-1, 1), sw.reshape(1, -1))):
+            try:
+                ms_ref = timed(lambda: torch._scaled_mm(qa0, qw.t(), scale_a=sa_t, scale_b=sw_t, bias=b,
+                                                        out_dtype=torch.bfloat16, use_fast_accum=False),
+                               args.steps, args.warmup)
+                ref_mm[label] = {"ms": ms_ref, "tflops": flop / (ms_ref * 1e-3) / 1e12}
+            except (RuntimeError, NotImplementedError) as error:
+                ref_mm[label] = {"error": str(error)[:200]}
+        kernels["torch_scaled_mm_hipblaslt_qkv"] = ref_mm
+
     # ---- the reference's default H3FP8Linear (per-tensor weight and activation scales) at C2:
     # abs-peak pass -> scale -> pack -> GEMM, the path a maintainer aliasing h3_fp8 gets
     if want("per_tensor"):
