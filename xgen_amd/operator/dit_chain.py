@@ -29,14 +29,14 @@ mapping {"qkv", "out", "ffn_up", "ffn_down"} -> kind.  Each per-token
 requantization can turn a last-bit difference of its bf16 input into a
 different e4m3 rounding (2^-4 relative), so a projection's summation error
 grows with every requantization after it: at C5 the FFN output sits at
-rel-L2 ~2.1e-2 from the exactly summed chain with "mfma" everywhere, ~1e-3
-to 2e-3 with "exact" everywhere.  Attributed stage by stage on the CPU (the
+rel-L2 ~2.2e-2 from the exactly summed chain with "mfma" everywhere, ~2e-3
+with "exact" everywhere.  Attributed stage by stage on the CPU (the
 oracle chain with the MFMA sum model swapped into one stage at a time), the
 error of the first projection dominates: it passes through three
 requantizations.  The default, DEFAULT_ACCUMULATION, is the cheapest mix that
 stays within the path's bar (rel-L2 <= 1e-2, cosine >= 0.9999 at every
 output): the QKV projection exact, the other three on the FP8 MFMA (FFN
-output ~7e-3 modelled).
+output ~7e-3 on MI355X).
 
 Attention is outside this path; without a callable the V third of the QKV
 output stands in for it (the out-projection then sees a real [M, d] bf16
