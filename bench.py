@@ -432,6 +432,22 @@ def main():
             "frac_of_fp8_peak": flop / (ms_ex * 1e-3) / 1e12 / PEAK_FP8_TFLOPS,
             "frac_of_bf16_peak": flop / (ms_ex * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}
 
+    # ---- the same QKV launches on all-zero and all-one e4m3 bytes: the instruction stream is
+    # unchanged, only the data the matrix cores multiply (and with it the power, so the clock) differ
+    if want("operands"):
+        power = {}
+        for label, a_t, w_t in (("zeros", torch.zeros_like(qa0), torch.zeros_like(qw)),
+                                ("ones", torch.ones(qa0.shape, device=dev).to(fp8),
+                                 torch.ones(qw.shape, device=dev).to(fp8))):
+            row = {}
+            for kind, exact in (("fp8_mfma", False), ("exact", True)):
+                ms_o = timed(lambda: xops.scaled_mm(a_t, w_t, sa0, sw, b, torch.bfloat16, N.ACT_NONE, False, exact),
+                             args.steps, args.warmup)
+                row[kind] = {"ms": ms_o, "tflops": flop / (ms_o * 1e-3) / 1e12}
+            power[label] = row
+            del a_t, w_t
+        kernels["gemm_qkv_constant_operands"] = power
+
     # ---- the reference's own GEMM call on this GPU: torch._scaled_mm (hipBLASLt) on the same QKV
     # operands, per-tensor scales + bias (h3_fp8.py:63-66) and row-wise scales (this path's semantics)
     if want("hipblaslt"):
