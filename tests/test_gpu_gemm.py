@@ -268,3 +268,40 @@ def test_torch_scaled_mm_on_this_gpu_sums_like_the_fp8_mfma(cuda):
     print(f"torch._scaled_mm(use_fast_accum=False): rel-L2 {to_mfma:.2e} from the FP8 MFMA kind, "
           f"{to_exact:.2e} from the exact sum; MFMA kind from exact {R.rel_l2(acc, exact):.2e}")
     assert to_mfma < 0.1 * to_exact
+
+
+@pytest.mark.parametrize("kind", ["fp8", "fp8_exact", "int8"])
+def test_operand_views(cuda, kind):
+    """Row-strided operand views (row stride above K, 16-byte aligned: read in place by the kernel)
+    and views the kernel cannot read (a base 1 byte off alignment, a row stride not a multiple of 16:
+    copied by the wrapper) give the bytes of the contiguous operands; so do strided residual and gate
+    rows in the gated form."""
+    M, K, Nf = 300, 320, 272
+    qa, sa, qw, sw, bias = quantized_operands(M, K, Nf, cuda, "int8" if kind == "int8" else "fp8", seed=7)
+    exact = kind == "fp8_exact"
+    ref, _ = xops.scaled_mm(qa, qw, sa, sw, bias, torch.bfloat16, N.ACT_NONE, False, exact)
+
+    def embed(t, cols, first):
+        big = torch.zeros((t.shape[0], cols), dtype=t.dtype, device=cuda)
+        big[:, first:first + t.shape[1]] = t
+        return big[:, first:first + t.shape[1]]
+
+    views = {"row stride K + 64": (embed(qa, K + 64, 32), embed(qw, K + 64, 16)),
+             "unaligned base": (embed(qa, K + 64, 1), embed(qw, K + 64, 3)),
+             "row stride K + 8": (embed(qa, K + 8, 0), embed(qw, K + 8, 8))}
+    for name, (a, w) in views.items():
+        assert a.stride(0) > K and torch.equal(a, qa) and torch.equal(w, qw), name
+        out, _ = xops.scaled_mm(a, w, sa, sw, bias, torch.bfloat16, N.ACT_NONE, False, exact)
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), name
+    if kind == "fp8_exact":
+        return
+    g = torch.Generator().manual_seed(3)
+    residual = torch.randn((M, Nf), generator=g).to(torch.bfloat16).to(cuda)
+    gate = (torch.randn((4, Nf), generator=g) * 0.5).to(torch.bfloat16).to(cuda)
+    idx = torch.randint(4, (M // 3,), generator=g).to(cuda)
+    fused = xops.scaled_mm_gate_residual(qa, qw, sa, sw, bias, residual, gate, idx)
+    for res_v, gate_v in ((embed(residual, Nf + 24, 8), embed(gate, Nf + 40, 16)),
+                          (embed(residual, Nf + 24, 1), embed(gate, Nf + 12, 0))):
+        a, w = views["row stride K + 64"]
+        got = xops.scaled_mm_gate_residual(a, w, sa, sw, bias, res_v, gate_v, idx)
+        assert torch.equal(got.view(torch.int16), fused.view(torch.int16))

@@ -212,3 +212,23 @@ def test_wire_shape_contract():
 
     assert wire_shape(3, 2 * 17 * 3, 128, 2, 0) == (3 * 2 * 17 * 3, 132)
     assert wire_shape(1, 2 * 17 * 3, 128, 2, 4) == (2, 17 * 3 * 132 + 4)
+
+
+def test_gemm_operand_views_are_passed_or_copied():
+    """The GEMM wrappers hand a [rows, cols] view to the kernels as it is when its rows are unit-stride,
+    cover the row, start 16-byte aligned and step by a multiple of the row alignment; anything else
+    is copied into a fresh contiguous tensor (the kernels reject such views)."""
+    from xgen_amd.ops import _kernel_rows
+    big = torch.zeros(8, 96, dtype=torch.int8)
+    assert big.data_ptr() % 16 == 0
+    for view in (big[:, :64], big[:, 16:80], big[2:6, 32:48]):
+        assert _kernel_rows(view, 16) is view
+    unaligned = big[:, 1:65]                               # base 1 byte past a 16-byte boundary
+    column_major = big[:, :64].t().contiguous().t()         # column stride 8
+    odd_rows = big.view(-1)[:160].as_strided((4, 64), (40, 1))  # row stride 40, not a multiple of 16
+    for view in (unaligned, column_major, odd_rows):
+        out = _kernel_rows(view, 16)
+        assert out is not view and out.is_contiguous() and out.data_ptr() % 16 == 0 and torch.equal(out, view)
+    wide = torch.zeros(4, 40, dtype=torch.bfloat16)  # row stride 40 elements: a multiple of 8, not of 16
+    assert _kernel_rows(wide[:, 8:24], 8).data_ptr() == wide[:, 8:24].data_ptr()
+    assert _kernel_rows(wide[:, :16], 16).stride(0) == 16

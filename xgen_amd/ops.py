@@ -43,6 +43,15 @@ def _require(cond: bool, msg: str) -> None:
         raise RuntimeError(msg)
 
 
+def _kernel_rows(t: torch.Tensor, row_align: int) -> torch.Tensor:
+    """t [rows, cols] as the GEMM kernels read it: unit column stride, a row stride that covers the
+    row and is a multiple of row_align elements, a 16-byte aligned base; other views are copied."""
+    if (t.stride(1) == 1 and t.stride(0) >= t.shape[1] and t.stride(0) % row_align == 0
+            and t.data_ptr() % 16 == 0):
+        return t
+    return t.clone(memory_format=torch.contiguous_format)
+
+
 def _rows_view(x: torch.Tensor) -> torch.Tensor:
     """[..., K] -> [M, K] with unit last stride (copies only if needed)."""
     m = x.reshape(-1, x.shape[-1])
@@ -255,8 +264,7 @@ def _mm_gpu(a, w, a_scale, w_scale, bias, out_dtype, activation, return_acc, exa
     Nf = w.shape[0]
     if M == 0:
         return out, acc
-    a = a if a.stride(1) == 1 else a.contiguous()
-    w = w if w.stride(1) == 1 else w.contiguous()
+    a, w = _kernel_rows(a, 16), _kernel_rows(w, 16)
     a_scale = a_scale.contiguous()
     w_scale = w_scale.contiguous()
     bias = None if bias is None else bias.contiguous()
@@ -333,12 +341,10 @@ def _mm_gate_gpu(a, w, a_scale, w_scale, bias, residual, gate_table, indices):
     Nf = w.shape[0]
     if M == 0:
         return out
-    a = a if a.stride(1) == 1 else a.contiguous()
-    w = w if w.stride(1) == 1 else w.contiguous()
+    a, w = _kernel_rows(a, 16), _kernel_rows(w, 16)
     a_scale, w_scale = a_scale.contiguous(), w_scale.contiguous()
     bias = None if bias is None else bias.contiguous()
-    residual = residual if residual.stride(1) == 1 else residual.contiguous()
-    gate_table = gate_table if gate_table.stride(1) == 1 else gate_table.contiguous()
+    residual, gate_table = _kernel_rows(residual, 8), _kernel_rows(gate_table, 8)
     indices = indices.contiguous()
     st = N.lib().xgen_w8a8_gate_residual(
         N.dtype_code(a.dtype), a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0), M, Nf, K, a_scale.data_ptr(),
