@@ -44,12 +44,19 @@ def _require(cond: bool, msg: str) -> None:
 
 
 def _kernel_rows(t: torch.Tensor, row_align: int) -> torch.Tensor:
-    """t [rows, cols] as the GEMM kernels read it: unit column stride, a row stride that covers the
-    row and is a multiple of row_align elements, a 16-byte aligned base; other views are copied."""
-    if (t.stride(1) == 1 and t.stride(0) >= t.shape[1] and t.stride(0) % row_align == 0
+    """t [..., rows, cols] as the kernels read it: unit column stride, every outer stride a multiple
+    of row_align elements, a row stride that covers the row, a 16-byte aligned base; other views
+    are copied (the kernels move rows in 16-byte pieces)."""
+    if (t.stride(-1) == 1 and t.stride(-2) >= t.shape[-1] and all(st % row_align == 0 for st in t.stride()[:-1])
             and t.data_ptr() % 16 == 0):
         return t
     return t.clone(memory_format=torch.contiguous_format)
+
+
+def _aligned_flat(t: torch.Tensor) -> torch.Tensor:
+    """t contiguous with a 16-byte aligned base (copied if not)."""
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
 def _rows_view(x: torch.Tensor) -> torch.Tensor:
@@ -212,7 +219,7 @@ def _peak_common(x, fn):
     _on_gpu(x)
     out = _peak_meta(x)
     _require(x.numel() > 0, f"{fn}: empty input")
-    xc = x.contiguous()
+    xc = _aligned_flat(x)
     L = N.lib()
     ws_bytes = L.xgen_abs_peak_workspace_bytes(xc.numel())
     ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=x.device)
@@ -235,7 +242,7 @@ def _pack_gpu(x, scale):
     q = _pack_meta(x, scale)
     if x.numel() == 0:
         return q
-    xc = x.contiguous()
+    xc = _aligned_flat(x)
     st = N.lib().xgen_fp8_pack(N.dtype_code(x.dtype), xc.data_ptr(), xc.numel(), scale.data_ptr(), q.data_ptr(),
                                N.stream_of(x))
     N.check(st, "xgen_fp8_pack")
@@ -247,6 +254,8 @@ def _norm_gpu(x, weight, scale, shift, indices, eps, norm_kind, out_dtype, retur
     q, s, normed = _norm_meta(x, weight, scale, shift, indices, eps, norm_kind, out_dtype, return_normed)
     if q.numel() == 0:
         return q, s, normed
+    x, scale, shift = _kernel_rows(x, 8), _kernel_rows(scale, 8), _kernel_rows(shift, 8)
+    weight = None if weight is None else _aligned_flat(weight)
     wcode = N.DTYPE_NONE if weight is None else N.dtype_code(weight.dtype)
     st = N.lib().xgen_norm_affine_quant(
         x.data_ptr(), x.shape[0], x.shape[1], x.shape[2], x.stride(0), x.stride(1), norm_kind,
@@ -288,9 +297,7 @@ def _gate_gpu(residual, branch, gate_table, indices):
     out = _gate_meta(residual, branch, gate_table, indices)
     if out.numel() == 0:
         return out
-    residual = residual if residual.stride(2) == 1 else residual.contiguous()
-    branch = branch if branch.stride(2) == 1 else branch.contiguous()
-    gate_table = gate_table if gate_table.stride(1) == 1 else gate_table.contiguous()
+    residual, branch, gate_table = _kernel_rows(residual, 8), _kernel_rows(branch, 8), _kernel_rows(gate_table, 8)
     indices = indices.contiguous()
     B, S, H = residual.shape
     st = N.lib().xgen_gate_residual(
@@ -324,7 +331,7 @@ def _swiglu_gpu(u, gate_first, out_dtype, scale_mode, return_act):
     q, s, act = _swiglu_meta(u, gate_first, out_dtype, scale_mode, return_act)
     if q.numel() == 0:
         return q, s, act
-    u = u if u.stride(2) == 1 else u.contiguous()
+    u = _kernel_rows(u, 8)
     table = silu_table(u.device)
     st = N.lib().xgen_swiglu_quant_lut(
         u.data_ptr(), u.shape[0], u.shape[1], u.shape[2] // 2, u.stride(0), u.stride(1), int(bool(gate_first)),
