@@ -12,8 +12,11 @@ Also timed (HIP events on the launch stream, same process): the GEMM alone
 (roofline), the per-token quantizer alone, the fused LayerNorm + AdaLN
 modulate + FP8 quant front end, the FFN up (with and without the GELU-tanh
 epilogue) / down GEMMs, the FFN-down requant with and without the GELU, the INT8
-QKV and FFN-up GEMMs, the QKV GEMM with exact accumulation, and the reference's
-default per-tensor H3FP8Linear.  The CPU baseline is the oracle's
+QKV and FFN-up GEMMs, the QKV GEMM with exact accumulation, the same QKV launch
+on all-zero and all-one operands (the clock follows the data), hipBLASLt's
+torch._scaled_mm on the QKV operands, the reference's default per-tensor
+H3FP8Linear, the path's neighbours (gated residual, SwiGLU requant, FP8 wire
+codec) and the C5 chain.  The CPU baseline is the oracle's
 quantize-dequantize linear on config C1 (FP8 and INT8) plus a bounded row
 sample of the QKV workload, on the host threads this process may use.
 
@@ -39,7 +42,7 @@ PEAK_BF16_TFLOPS = 2500.0  # MI355X dense BF16 MFMA (the exact-accumulation kind
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 # HBM (fabric) bytes per launch of the QKV GEMM, from rocprofv3 FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000
 # (copy-kernel calibration); profiles/hbm_traffic_c2_qkv_gemm_and_path_kernels.md holds the counts.
-QKV_GEMM_TRAFFIC_BYTES = (364876 * 2.0 + 281467 * 1.0) * 1024
+QKV_GEMM_TRAFFIC_BYTES = (364868 * 2.0 + 281395 * 1.0) * 1024
 METRIC = "FP8 W8A8 linear TFLOP/s (% MFMA peak) + quant GB/s, M=15.6k d=3072, 1 GPU"
 
 
