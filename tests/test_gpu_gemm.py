@@ -305,3 +305,29 @@ def test_operand_views(cuda, kind):
         a, w = views["row stride K + 64"]
         got = xops.scaled_mm_gate_residual(a, w, sa, sw, bias, res_v, gate_v, idx)
         assert torch.equal(got.view(torch.int16), fused.view(torch.int16))
+
+
+@pytest.mark.parametrize("kind", ["fp8", "fp8_exact", "int8"])
+def test_full_size_scale_placement(cuda, kind):
+    """Every output element of the full C2 QKV GEMM (M=15,624 x N=9,216, all 2,232 tiles) takes its
+    own token's and its own feature's scale: with no bias, scaling token m's scale by 2^u[m] and
+    feature n's by 2^v[n] (u, v in -3..3) scales out[m, n] by exactly 2^(u[m] + v[n]) — the
+    accumulators are unchanged, the dequant product moves by a power of two, and the bf16 rounding
+    commutes with it — so the whole output is checked bit for bit against the unscaled launch."""
+    M, K = workloads.M_5S, workloads.D_MODEL
+    g = workloads.generator(0, cuda)
+    x, _ = workloads.activations(M, K, g, cuda)
+    w, _ = workloads.weight("qkv", g, cuda)
+    dt = torch.int8 if kind == "int8" else torch.float8_e4m3fn
+    exact = kind == "fp8_exact"
+    qa, sa = xops.quantize_rows(x, dt)
+    qw, sw = xops.quantize_rows(w, dt)
+    gen = torch.Generator().manual_seed(11)
+    u = torch.randint(-3, 4, (M,), generator=gen).to(cuda)
+    v = torch.randint(-3, 4, (qw.shape[0],), generator=gen).to(cuda)
+    base, _ = xops.scaled_mm(qa, qw, sa, sw, None, torch.bfloat16, N.ACT_NONE, False, exact)
+    moved, _ = xops.scaled_mm(qa, qw, torch.ldexp(sa, u), torch.ldexp(sw, v), None, torch.bfloat16, N.ACT_NONE,
+                              False, exact)
+    expect = torch.ldexp(base.float(), u[:, None] + v[None, :]).to(torch.bfloat16)
+    assert torch.isfinite(base.float()).all()
+    assert torch.equal(moved.view(torch.int16), expect.view(torch.int16))
