@@ -331,3 +331,38 @@ def test_full_size_scale_placement(cuda, kind):
     expect = torch.ldexp(base.float(), u[:, None] + v[None, :]).to(torch.bfloat16)
     assert torch.isfinite(base.float()).all()
     assert torch.equal(moved.view(torch.int16), expect.view(torch.int16))
+
+
+def _sweep_shapes(n, seed):
+    g = torch.Generator().manual_seed(seed)
+    shapes = []
+    for _ in range(n):
+        M = int(torch.randint(1, 600, (1,), generator=g))
+        K = 16 * int(torch.randint(1, 70, (1,), generator=g))
+        Nf = 16 * int(torch.randint(1, 50, (1,), generator=g))
+        shapes.append((M, K, Nf))
+    return shapes
+
+
+@pytest.mark.parametrize("kind", ["fp8", "fp8_exact", "int8"])
+def test_seeded_shape_sweep(cuda, kind):
+    """Twelve seeded shapes with M in [1, 600), K and N multiples of 16 up to 1,104 / 784 (K tails of
+    16..112 bytes past a 128-byte pair, single-tile and partial-tile outputs): accumulators bit for bit
+    (INT8 against the exact sum, the FP8 kind against the MFMA model), the exact kind within the
+    float32 summation bound, outputs within the epilogue's rounding."""
+    for M, K, Nf in _sweep_shapes(12, seed=29):
+        qa, sa, qw, sw, bias = quantized_operands(M, K, Nf, cuda, "int8" if kind == "int8" else "fp8", seed=M * K)
+        out, acc = xops.scaled_mm(qa, qw, sa, sw, bias, torch.bfloat16, N.ACT_NONE, True, kind == "fp8_exact")
+        if kind == "int8":
+            assert torch.equal(acc.cpu().long(), R.int8_accumulate_exact(qa.cpu(), qw.cpu())), (M, K, Nf)
+            continue
+        exact = R.fp8_accumulate_exact(qa.cpu(), qw.cpu())
+        mag = R.decode_fp8(qa.cpu()).abs() @ R.decode_fp8(qw.cpu()).abs().T
+        if kind == "fp8":
+            assert torch.equal(acc.cpu(), R.fp8_mfma_accumulate(qa.cpu(), qw.cpu())), (M, K, Nf)
+            acc_bound = FP8_ACC_REL * mag
+        else:
+            acc_bound = K * FP32_SUM_REL * mag
+            assert ((acc.cpu().double() - exact).abs() <= acc_bound + 1e-30).all(), (M, K, Nf)
+        ref = R.w8a8_linear_fp8(qa.cpu(), sa.cpu(), qw.cpu(), sw.cpu(), bias.cpu())
+        assert_within_rounding(out, ref, exact.abs(), sa, sw, bias, acc_bound)
