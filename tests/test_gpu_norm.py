@@ -179,3 +179,18 @@ def test_prepared_one_plus_scale_is_bit_identical(cuda, norm, out, H, wdtype):
     assert torch.equal(s0.view(torch.int32), s1.view(torch.int32))
     assert torch.equal(m0.view(torch.int16), m1.view(torch.int16))
     assert torch.isnan(s0[5]) and torch.isnan(s0[41 + 5]) and not torch.isnan(s0[4])
+
+
+@pytest.mark.parametrize("H", [8, 1032, 2048, 2056, 3080, 4096, 4104, 6144, 6152])
+@pytest.mark.parametrize("wdtype", [None, torch.float32])
+def test_every_width_form(cuda, H, wdtype):
+    """Each launch form of the width dispatch at and just past its boundaries (one wave per row up
+    to 3,072 with 2 / 4 / 6 chunks per lane, two waves per row to 4,096, four beyond), LayerNorm and
+    RMSNorm, with and without a norm weight, against the oracle."""
+    x, scale, shift, idx = inputs(2, 11, H, 4, seed=H, dev=cuda)
+    w = None if wdtype is None else (torch.randn(H, generator=torch.Generator().manual_seed(H)) * 0.3 + 1).to(
+        wdtype).to(cuda)
+    for norm, eps in (("layer", 1e-6), ("rms", 1e-5)):
+        q, s, m = xops.norm_affine_quant(x, w, scale, shift, idx, eps, N.NORM_LAYER if norm == "layer" else N.NORM_RMS,
+                                         torch.float8_e4m3fn, True)
+        check(x, w, scale, shift, idx, eps, norm, "fp8", q, s, m)
