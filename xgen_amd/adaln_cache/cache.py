@@ -161,6 +161,8 @@ class AdalnScheduleCache:
             return
         self._current_table = self._tables[key]
         self._current_key = key
+        if self._current_table["packed"].is_cuda:
+            self._prepare_one_plus(self._current_table)
 
     @property
     def has_current(self) -> bool:
@@ -182,22 +184,33 @@ class AdalnScheduleCache:
 
     def one_plus_scales(self, block_idx: int):
         """(bf16(1 + scale), bf16(1 + scale_mlp)) of block block_idx, each [3M', H], for
-        norm_affine_quant(..., scale_is_one_plus=True).  Prepared on the GPU for every block of the
-        installed schedule on first use (one [num_blocks, 3M', 2H] buffer) and kept with it."""
-        t = self._current_table
-        if "one_plus" not in t:
-            from ..operator.nq2 import adaln_one_plus
-            packed = t["packed"]
-            nb, rows, six_h = packed.shape
-            h = six_h // 6
-            prepared = torch.empty((nb, rows, 2 * h), dtype=torch.bfloat16, device=packed.device)
-            for j in range(nb):
-                blk = t["blocks"][j]
-                adaln_one_plus(blk.scale, prepared[j, :, :h])
-                adaln_one_plus(blk.scale_mlp, prepared[j, :, h:])
-            t["one_plus"] = [tuple(prepared[j].chunk(2, dim=-1)) for j in range(nb)]
-        return t["one_plus"][block_idx]
+        norm_affine_quant(..., scale_is_one_plus=True).  Prepared on the GPU for every block of a
+        schedule when it is installed (one [num_blocks, 3M', 2H] buffer, kept with it)."""
+        self._prepare_one_plus(self._current_table)
+        return self._current_table["one_plus"][block_idx]
 
+    @staticmethod
+    def _prepare_one_plus(t: dict) -> None:
+        """bf16(1 + scale) of every block's scale and scale_mlp table, once per schedule, registered
+        with the fused front end (nq2.register_one_plus): its calls given these tables read the
+        prepared ones.  Waits for the preparation once, so any stream may read them."""
+        if "one_plus" in t:
+            return
+        from ..operator.nq2 import adaln_one_plus, register_one_plus
+        packed = t["packed"]
+        nb, rows, six_h = packed.shape
+        h = six_h // 6
+        prepared = torch.empty((nb, rows, 2 * h), dtype=torch.bfloat16, device=packed.device)
+        pairs = []
+        for j in range(nb):
+            blk = t["blocks"][j]
+            for raw, out in ((blk.scale, prepared[j, :, :h]), (blk.scale_mlp, prepared[j, :, h:])):
+                adaln_one_plus(raw, out)
+                pairs.append((raw, out))
+        torch.cuda.current_stream(packed.device).synchronize()
+        for raw, out in pairs:
+            register_one_plus(raw, out)
+        t["one_plus"] = [tuple(prepared[j].chunk(2, dim=-1)) for j in range(nb)]
 
 def _rows(raw: torch.Tensor) -> torch.Tensor:
     """A block table [M, 18H] as its [3M, 6H] modality rows (cache.py:116-118)."""

@@ -14,6 +14,13 @@ reference kernel's debug output, f2bc_kernel.asc:86), and
 same values).  ``blocks`` and ``cached`` are accepted for signature
 compatibility; the HIP kernel sizes its own grid and reads table rows
 through L2.
+
+A holder of scale tables (the AdaLN loader) can register bf16(1 + scale) for
+a table it keeps (``register_one_plus``): a call given that table itself —
+the same memory, shape and strides, not written since (its version counter)
+— then reads the prepared table, as the reference's callers pass the raw one.
+A table written after it was prepared is prepared again on its next use; calls
+captured into a HIP graph read the table they are given.
 """
 from __future__ import annotations
 
@@ -31,14 +38,54 @@ def library_path(cached=False):
     return N.library_path()
 
 
+# registered tables: key of the raw scale table -> [raw table, prepared table, raw version when prepared]
+_ONE_PLUS: dict = {}
+prepared_hits = 0  # calls that read a registered prepared table
+
+
+def _table_key(t: torch.Tensor):
+    return (t.device.type, t.device.index, t.data_ptr(), tuple(t.shape), tuple(t.stride()))
+
+
+def register_one_plus(scale: torch.Tensor, prepared: torch.Tensor) -> None:
+    """Have norm_affine_quant read `prepared` (= adaln_one_plus(scale), same shape) when it is given
+    `scale` itself; the registry keeps both tensors until unregister_one_plus(scale)."""
+    if prepared.shape != scale.shape or prepared.dtype != torch.bfloat16 or prepared.device != scale.device:
+        raise ValueError("register_one_plus: the prepared table must match the scale table")
+    _ONE_PLUS[_table_key(scale)] = [scale, prepared, scale._version]
+
+
+def unregister_one_plus(scale: torch.Tensor) -> None:
+    _ONE_PLUS.pop(_table_key(scale), None)
+
+
+def _registered_one_plus(scale: torch.Tensor):
+    """The prepared table registered for `scale` (re-prepared if `scale` was written since), or None."""
+    entry = _ONE_PLUS.get(_table_key(scale)) if _ONE_PLUS else None
+    if entry is None or entry[0].untyped_storage().data_ptr() != scale.untyped_storage().data_ptr():
+        return None
+    if scale._version != entry[2]:
+        adaln_one_plus(scale, entry[1])
+        entry[2] = scale._version
+    return entry[1]
+
+
 def norm_affine_quant(x, weight, scale, shift, indices, *, eps=1e-5, blocks=40, cached=False,
                       norm="rms", out_dtype=torch.int8, return_normed=False, scale_is_one_plus=False):
+    global prepared_hits
     if any(v is not None and v.requires_grad for v in (x, weight, scale, shift)):
         raise ValueError('Experimental inference only; detach parameters explicitly')
     if norm not in _NORMS:
         raise ValueError(f"norm must be one of {sorted(_NORMS)}")
     if not (0 < blocks <= 40):
         raise RuntimeError("invalid epsilon/blocks")
+    # (not under graph capture: a captured call keeps reading the table it was given, as replays
+    # of the raw form would see later writes to it)
+    if not scale_is_one_plus and not torch.cuda.is_current_stream_capturing():
+        prepared = _registered_one_plus(scale)
+        if prepared is not None:
+            scale, scale_is_one_plus = prepared, True
+            prepared_hits += 1
     kind = _NORMS[norm] | (N.NORM_SCALE_ONE_PLUS if scale_is_one_plus else 0)
     q, s, normed = xops.norm_affine_quant(x, weight, scale, shift, indices, float(eps), kind,
                                           out_dtype, bool(return_normed))
