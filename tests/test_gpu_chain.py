@@ -133,12 +133,9 @@ def test_gelu_placements_agree(cuda, kernel_gelu):
     assert not torch.equal(h1.view(torch.int16), h2.view(torch.int16))
 
 
-@pytest.mark.parametrize("accumulation", ["default", "exact", "mfma"])
-def test_chain_full_size_c5_sampled_rows(cuda, kernel_gelu, accumulation):
-    """C5 at M = 31,248 tokens (10 s clip, SP8 share), d = 3,072: the whole chain on the GPU,
-    48 seeded rows (first and last included) checked stage by stage and end to end."""
+def run_c5(cuda, kernel_gelu, accumulation, seed):
     M, d = workloads.M_10S, workloads.D_MODEL
-    g = workloads.generator(0, cuda)
+    g = workloads.generator(seed, cuda)
     x, _ = workloads.activations(M, d, g, cuda)
     shift, scale = workloads.adaln_tables(20, d, g, cuda)
     idx = torch.randint(20, (M,), generator=g, device=cuda)
@@ -158,4 +155,19 @@ def test_chain_full_size_c5_sampled_rows(cuda, kernel_gelu, accumulation):
     got[2] = kernel_gelu(got[2])
     dist = check_end_to_end(got, x[rc][None].cpu(), scale.cpu(), shift.cpu(),
                             idx[rc].cpu(), weights, accumulation, (fq.cpu(), fs.cpu()))
-    print(f"C5 end to end ({accumulation}):", {n: f"rel {r:.2e} cos {c:.7f}" for n, (r, c) in dist.items()})
+    print(f"C5 end to end ({accumulation}, seed {seed}):",
+          {n: f"rel {r:.2e} cos {c:.7f}" for n, (r, c) in dist.items()})
+
+
+@pytest.mark.parametrize("accumulation", ["default", "exact", "mfma"])
+def test_chain_full_size_c5_sampled_rows(cuda, kernel_gelu, accumulation):
+    """C5 at M = 31,248 tokens (10 s clip, SP8 share), d = 3,072: the whole chain on the GPU,
+    48 seeded rows (first and last included) checked stage by stage and end to end."""
+    run_c5(cuda, kernel_gelu, accumulation, seed=0)
+
+
+@pytest.mark.parametrize("seed", [1, 2])
+def test_default_chain_full_size_c5_other_data(cuda, kernel_gelu, seed):
+    """The default chain's end-to-end bar at C5 on two more seeded draws of activations, tables,
+    indices and weights (the bar is not tuned to one draw)."""
+    run_c5(cuda, kernel_gelu, "default", seed)
