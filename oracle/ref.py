@@ -55,7 +55,6 @@ Function -> reference -> how it is pinned (tests/test_oracle_*.py):
 from __future__ import annotations
 
 import ctypes
-import math
 from pathlib import Path
 
 import numpy as np

@@ -52,6 +52,11 @@ def test_per_tensor_module_matches_oracle(cuda):
     assert R.rel_l2(out, ref) < 1e-3 and R.cosine(out, ref) > 0.9999
     assert out.shape == (3, 41, 512)
     assert layer(x.cuda()[:, :0]).shape == (3, 0, 512)
+    # the module function itself (h3_fp8.py:9-12): bytes and scale of the oracle, on the input's device
+    for src in (weight, weight.cuda()):
+        q, sc = quantize_per_tensor(src)
+        assert q.device == src.device and sc.device == src.device and sc.dim() == 0
+        assert torch.equal(q.cpu().view(torch.uint8), qw.view(torch.uint8)) and torch.equal(sc.cpu(), sw.reshape(()))
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
