@@ -161,3 +161,25 @@ def test_row_scale_two_operation_division_exhaustive(fmt):
     assert m and float.fromhex(m.group(1)) == r_hi.value and float.fromhex(m.group(2)) == r_lo.value
     # the constants are 1/448 split: r_hi rounded toward zero, r_hi + r_lo within 2^-45 relative
     assert r_hi.value <= 1 / 448 and abs((r_hi.value + r_lo.value) * 448 - 1) < 2.0 ** -45
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_row_quantizer_symmetries(dtype):
+    """Properties the arithmetic fixes, on random rows of both input types: negating a row flips
+    exactly the sign bit of every byte (round to nearest even commutes with negation; -0 -> 0x80)
+    and keeps its scale; scaling a row by 2^k (no under- or overflow of the values or the scale)
+    keeps every byte and scales the scale by exactly 2^k; permuting a row's columns permutes its
+    bytes.  A mistaken sign, index or scale would break one of them."""
+    torch.manual_seed(3)
+    x = (torch.randn(40, 200) * torch.logspace(-2, 2, 40)[:, None]).to(dtype)
+    q, s = R.quantize_rows_fp8(x)
+    qn, sn = R.quantize_rows_fp8(-x)
+    assert torch.equal(qn.view(torch.uint8), q.view(torch.uint8) ^ 0x80)
+    assert torch.equal(sn, s)
+    for k in (-3, 1, 4):
+        qk, sk = R.quantize_rows_fp8((x.float() * 2.0 ** k).to(dtype))
+        assert torch.equal(qk.view(torch.uint8), q.view(torch.uint8))
+        assert torch.equal(sk, s * 2.0 ** k)
+    perm = torch.randperm(200, generator=torch.Generator().manual_seed(4))
+    qp, sp = R.quantize_rows_fp8(x[:, perm])
+    assert torch.equal(qp.view(torch.uint8), q.view(torch.uint8)[:, perm]) and torch.equal(sp, s)

@@ -82,3 +82,22 @@ def test_subnormal_amax_row_quantizes_to_zeros(dtype):
     if dtype == torch.bfloat16:   # f16's smallest subnormal still gives a finite 127/amax
         assert (q == 0).all()
     assert torch.equal(q, qc) and torch.equal(s.view(torch.int32), sc.view(torch.int32))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_symmetries(dtype):
+    """Negating a row negates every byte and keeps its scale (round half to even and the max are
+    symmetric); scaling a row by 2^k keeps every byte and scales the scale by exactly 2^k (the
+    multiplier 127/amax moves by 2^-k, each product is unchanged); permuting a row's columns permutes
+    its bytes."""
+    torch.manual_seed(5)
+    x = (torch.randn(40, 200) * torch.logspace(-2, 2, 40)[:, None]).to(dtype)
+    q, s = R.quantize_rows_int8(x)
+    qn, sn = R.quantize_rows_int8(-x)
+    assert torch.equal(qn, -q) and torch.equal(sn, s)
+    for k in (-3, 1, 4):
+        qk, sk = R.quantize_rows_int8((x.float() * 2.0 ** k).to(dtype))
+        assert torch.equal(qk, q) and torch.equal(sk, s * 2.0 ** k)
+    perm = torch.randperm(200, generator=torch.Generator().manual_seed(6))
+    qp, sp = R.quantize_rows_int8(x[:, perm])
+    assert torch.equal(qp, q[:, perm]) and torch.equal(sp, s)
