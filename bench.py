@@ -16,7 +16,7 @@ QKV and FFN-up GEMMs, the QKV GEMM with exact accumulation, the same QKV launch
 on all-zero and all-one operands (the clock follows the data), hipBLASLt's
 torch._scaled_mm on the QKV operands, the reference's default per-tensor
 H3FP8Linear, the path's neighbours (gated residual, SwiGLU requant, FP8 wire
-codec) and the C5 chain.  The CPU baseline is the oracle's
+codec and the asynchronous exchange's gather / return layouts) and the C5 chain.  The CPU baseline is the oracle's
 quantize-dequantize linear on config C1 (FP8 and INT8) plus a bounded row
 sample of the QKV workload, on the host threads this process may use.
 
@@ -89,6 +89,42 @@ def wire_setup(M, g, dev):
 
     values = 3 * rows * W.HEAD_DIM
     return encode, decode, values * 2 + wire.numel(), wire.numel() + values * 2
+
+
+def async_wire_setup(M, g, dev):
+    """The asynchronous exchange's layouts at the same geometry (one chunk of the 3 local heads):
+    the direct-gather decode of the Q/K/V wire into [1, 3, 8 M, 128] attention inputs, the fused return
+    pack of a [1, 3, 8 M, 128] attention output and the return-layout decode of its wire into a
+    [1, M, 24 * 128] output.  Returns ((name, fn, bytes), ...)."""
+    import torch
+    from unittest.mock import patch
+    import torch.distributed as dist
+    from xgen_amd import workloads as W
+    from xgen_amd.phaa import fp8_async_transport as A
+    P, H, D = W.SP_PEERS, W.HEADS // W.SP_PEERS, W.HEAD_DIM
+    fused = torch.randn((1, M, 3 * W.HEADS * D), generator=g, device=dev).to(torch.bfloat16)
+    shards = tuple(t.unflatten(-1, (W.HEADS, D)).unflatten(2, (P, H)).permute(2, 1, 0, 3, 4)
+                   for t in fused.chunk(3, dim=-1))
+    gathered = tuple(torch.empty((1, H, P * M, D), dtype=torch.bfloat16, device=dev) for _ in range(3))
+    attn = torch.randn((1, H, P * M, D), generator=g, device=dev).to(torch.bfloat16)
+    out = torch.empty((1, M, W.HEADS * D), dtype=torch.bfloat16, device=dev)
+    with patch.object(dist, "get_world_size", return_value=P):
+        qkv_wire, _, qkv_rows = A._pack_exchange(gathered, shards, D, None, direct_gather=True)
+        ret_wire, _, ret_rows = A._pack_exchange(None, (attn,), D, None, return_shard_seq=M)
+    values = P * M * H * D
+
+    def gather():
+        A._unpack_exchange(qkv_wire, gathered, qkv_rows)
+
+    def pack():
+        A._encode_rows((attn,), D, P, M, ret_wire)
+
+    def place():
+        A._unpack_exchange(ret_wire, (out,), ret_rows, (M, 1, P, H, H, 0))
+
+    return (("wire_async_gather_decode_h3", gather, qkv_wire.numel() + 3 * values * 2),
+            ("wire_async_return_pack_h3", pack, values * 2 + ret_wire.numel()),
+            ("wire_async_return_layout_decode_h3", place, ret_wire.numel() + values * 2))
 
 
 def profile_kernels(names, steps, warmup):
@@ -552,6 +588,11 @@ def main():
         kernels["wire_decode_h3"] = {"ms": ms_dec, "gbs": dec_bytes / (ms_dec * 1e-3) / 1e9,
                                      "frac_of_hbm": dec_bytes / (ms_dec * 1e-3) / 1e9 / PEAK_HBM_GBS,
                                      "bytes": dec_bytes}
+        del enc, dec
+        for name, fn, nbytes in async_wire_setup(M, g, dev):
+            ms_a = timed(fn, args.steps, args.warmup)
+            kernels[name] = {"ms": ms_a, "gbs": nbytes / (ms_a * 1e-3) / 1e9,
+                             "frac_of_hbm": nbytes / (ms_a * 1e-3) / 1e9 / PEAK_HBM_GBS, "bytes": nbytes}
 
     # ---- C5 chain at a 10 s clip's share (M=31,248): front end -> QKV -> out -> up -> GELU requant -> down
     if want("c5"):

@@ -342,6 +342,33 @@ int xgen_fp8_wire_encode(int in_dtype, int streams, const void *q, const void *k
 int xgen_fp8_wire_decode(int out_dtype, int streams, const void *wire, int64_t peers, int64_t peer_rows,
                          int64_t width, int64_t peer_padding, void *q, void *k, void *v, hipStream_t stream);
 
+/*
+ * The asynchronous transport's layouts (x_base/x_base/phaa/fp8_async_transport.py:13-80,
+ * _encode / _decode launched by _pack_exchange :126-180 and _unpack_exchange :183-193).
+ * Its wire has no peer padding.
+ *
+ * Encode with a valid sequence length (the fused return pack, RETURN_SEQ,
+ * :22-27,41-44): as xgen_fp8_wire_encode with peer_padding 0, except that a row
+ * (p, t, b, h) with p*seq + t >= valid_seq is not read and travels as a zero
+ * row (scale 1e-12, zero bytes).  valid_seq >= peers*seq encodes every row.
+ */
+int xgen_fp8_wire_encode_masked(int in_dtype, int streams, const void *q, const void *k, const void *v,
+                                const int64_t *strides, int64_t peers, int64_t seq, int64_t batch, int64_t heads,
+                                int64_t width, int64_t valid_seq, void *wire, hipStream_t stream);
+
+/*
+ * Decode into strided outputs (the direct gather GATHER_SEQ, :67-73, and the
+ * return layout CHUNK_HEADS / HEAD_START, :74-78): wire row (p, t, b, h) of
+ * stream s (peer_rows = seq*batch*heads, rows ordered as the encoder's) is
+ * written as `width` contiguous values at element p*dst_strides[0] +
+ * t*dst_strides[1] + b*dst_strides[2] + h*dst_strides[3] of output s (host
+ * array of 4 non-negative element strides, shared by the streams); rows with
+ * p*seq + t >= valid_seq are not written.
+ */
+int xgen_fp8_wire_decode_strided(int out_dtype, int streams, const void *wire, int64_t peers, int64_t seq,
+                                 int64_t batch, int64_t heads, int64_t width, const int64_t *dst_strides,
+                                 int64_t valid_seq, void *q, void *k, void *v, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -43,6 +43,11 @@ Function -> reference -> how it is pinned (tests/test_oracle_*.py):
         floor; decode of all 256 codes == the e4m3 table; round-trip error bound;
         the kernels' division exhaustively at the floor (bf16).  Non-finite rows:
         parity unpinned (the reference leaves NaN to its min/max lowering).
+  fp8 async layouts   phaa/fp8_async_transport.py:13-80,126-193 (fp8_async_encode / _decode)
+        plain layout == the synchronous wire without padding; the fused return
+        pack == the synchronous wire of the output zero-padded and permuted by torch
+        reshapes; the direct gather and the return layout == the synchronous decode
+        permuted / placed by torch reshapes (tests/test_oracle_wire.py).
   fp8 / int8 GEMM     h3_fp8.py:63-66 (_scaled_mm), matmul.py:63-64 (npu_quant_matmul)
         accumulators exact (float64 BLAS of decoded operands; every partial
         sum is an exact multiple of 2^-18 below 2^35) == int64 brute force on
@@ -333,6 +338,79 @@ def fp8_wire_decode(wire: torch.Tensor, streams: int, rows: int, head_dim: int, 
         sc = blk[:, W:].contiguous().view(torch.float32).reshape(rows)
         out.append((q * sc[:, None]).to(out_dtype))
     return out
+
+
+def _async_wire_rows(r: torch.Tensor, slot: int, streams: int, peer_rows: int) -> torch.Tensor:
+    """Wire row of logical row r of stream `slot` (fp8_async_transport.py:45, :63)."""
+    return r + (r // peer_rows * (streams - 1) + slot) * peer_rows
+
+
+def fp8_async_encode(tensors, head_dim: int, peers: int, return_shard_seq: int = 0) -> torch.Tensor:
+    """The send buffer of _pack_exchange (fp8_async_transport.py:126-180; _encode :13-50), restated row
+    by row: [streams * rows, head_dim + 4] uint8, no peer padding.  Logical row r of a stream reads,
+    with return_shard_seq = 0, the input's r-th row in row-major order (a [peers, seq, batch, heads,
+    head_dim] view and its contiguous copy alike, :28-36); with return_shard_seq > 0 (RETURN_SEQ) the
+    input is an attention output [batch, heads, valid_seq, head_dim] and row r = ((p * shard_seq + s)
+    * batch + b) * heads + h reads element (b, h, p * shard_seq + s), a zero row when that position is
+    at or past valid_seq (:22-27, :41-44: masked loads give 0, so scale 1e-12 and zero bytes)."""
+    streams, W = len(tensors), head_dim
+    if return_shard_seq:
+        (t,) = tensors
+        B, H, valid, _ = t.shape
+        rows = peers * return_shard_seq * B * H
+        r = torch.arange(rows)
+        head, batch, seq = r % H, r // H % B, r // (H * B)
+        live = seq < valid
+        src = torch.zeros(rows, W)
+        src[live] = t.detach().cpu().float()[batch[live], head[live], seq[live]]
+        sources = [src]
+    else:
+        rows = tensors[0].numel() // W
+        sources = [t.detach().cpu().float().reshape(rows, W) for t in tensors]
+    pr = rows // peers
+    wire = torch.zeros(streams * rows, W + 4, dtype=torch.uint8)
+    r = torch.arange(rows)
+    for slot, src in enumerate(sources):
+        q, s = wire_rows_fp8(src)
+        w = _async_wire_rows(r, slot, streams, pr)
+        wire[w, :W] = q
+        wire[w, W:] = s.contiguous().view(torch.uint8).reshape(rows, 4)
+    return wire
+
+
+def fp8_async_decode(wire: torch.Tensor, outputs, rows: int, head_dim: int, peers: int, *, gather_seq: int = 0,
+                     layout=None):
+    """_unpack_exchange / _decode (fp8_async_transport.py:183-193, :53-79) into CPU `outputs` (one per
+    stream, written in place and returned): logical row r of stream `slot` is read from its wire row
+    and stored as out_dtype(fl32(e4m3(byte) * scale)) at output row
+      * r (contiguous outputs, :62);
+      * with gather_seq (direct gather, outputs [batch, heads, gather_seq, head_dim]): head = r % heads,
+        batch = r // heads % B, seq = r // (heads * B); row (batch * heads + head) * gather_seq + seq,
+        dropped when seq >= gather_seq (:67-73);
+      * with layout = (sq, batch, peers, heads_per_peer, chunk_heads, head_start) (return layout):
+        head = r % chunk_heads, batch = r // chunk_heads % B, seq = r // (chunk_heads * B) % sq,
+        peer = r // peer_rows; row ((batch * sq + seq) * peers + peer) * heads_per_peer + head_start
+        + head (:74-78)."""
+    streams, W = len(outputs), head_dim
+    pr = rows // peers
+    r = torch.arange(rows)
+    flat = wire.detach().cpu().reshape(-1, W + 4)
+    for slot, out in enumerate(outputs):
+        rec = flat[_async_wire_rows(r, slot, streams, pr)]
+        q = rec[:, :W].contiguous().view(torch.float8_e4m3fn).float()
+        sc = rec[:, W:].contiguous().view(torch.float32).reshape(rows)
+        vals = (q * sc[:, None]).to(out.dtype)
+        dst, keep = r, torch.ones(rows, dtype=torch.bool)
+        if gather_seq:
+            B, H = out.shape[0], out.shape[1]
+            head, batch, seq = r % H, r // H % B, r // (H * B)
+            dst, keep = (batch * H + head) * gather_seq + seq, seq < gather_seq
+        elif layout is not None:
+            sq, B, P, hpp, ch, start = layout
+            head, batch, seq, peer = r % ch, r // ch % B, r // (ch * B) % sq, r // pr
+            dst = ((batch * sq + seq) * P + peer) * hpp + start + head
+        out.view(-1, W)[dst[keep]] = vals[keep]
+    return outputs
 
 
 def gelu_tanh_bf16(y: torch.Tensor) -> torch.Tensor:

@@ -94,6 +94,18 @@ _STRIDES = (N._c_i64 * 12)(384, 128, 128, 128, 384, 128, 128, 128, 384, 128, 128
      N.ERR_INVALID_ARGUMENT, b"null"),
     (lambda L: L.xgen_fp8_wire_decode(N.DTYPE_BF16, 1, 16, 2, 1 << 31, 64, 0, 16, None, None, None),
      N.ERR_UNSUPPORTED, b"2^30"),
+    (lambda L: L.xgen_fp8_wire_encode_masked(N.DTYPE_BF16, 1, 16, None, None, _STRIDES, 2, 3, 1, 1, 64, -1, 16, None),
+     N.ERR_INVALID_ARGUMENT, b"negative shape"),
+    (lambda L: L.xgen_fp8_wire_encode_masked(N.DTYPE_BF16, 1, 16, None, None, None, 2, 3, 1, 1, 64, 4, 16, None),
+     N.ERR_INVALID_ARGUMENT, b"null"),
+    (lambda L: L.xgen_fp8_wire_decode_strided(N.DTYPE_BF16, 1, 16, 2, 3, 1, 1, 64, None, 6, 16, None, None, None),
+     N.ERR_INVALID_ARGUMENT, b"null"),
+    (lambda L: L.xgen_fp8_wire_decode_strided(N.DTYPE_BF16, 1, 16, 2, 3, 1, 1, 64, (N._c_i64 * 4)(64, -64, 0, 0), 6,
+                                              16, None, None, None), N.ERR_INVALID_ARGUMENT, b"negative stride"),
+    (lambda L: L.xgen_fp8_wire_decode_strided(N.DTYPE_I8, 1, 16, 2, 3, 1, 1, 64, (N._c_i64 * 4)(192, 64, 0, 0), 6,
+                                              16, None, None, None), N.ERR_INVALID_ARGUMENT, b"output dtype"),
+    (lambda L: L.xgen_fp8_wire_decode_strided(N.DTYPE_BF16, 1, 16, 2, 1 << 31, 1, 1, 64, (N._c_i64 * 4)(0, 64, 0, 0),
+                                              6, 16, None, None, None), N.ERR_UNSUPPORTED, b"peer rows"),
 ])
 def test_validation_fails_before_launch(built_library, call, status, needle):
     L = N.lib()
@@ -108,6 +120,10 @@ def test_empty_inputs_are_no_ops(built_library):
                                 None, N.DTYPE_BF16, 16, None, None) == N.OK
     assert L.xgen_fp8_wire_encode(N.DTYPE_BF16, 3, None, None, None, None, 2, 0, 1, 3, 128, 0, None, None) == N.OK
     assert L.xgen_fp8_wire_decode(N.DTYPE_F32, 1, None, 4, 0, 64, 0, None, None, None, None) == N.OK
+    assert L.xgen_fp8_wire_encode_masked(N.DTYPE_BF16, 1, None, None, None, None, 2, 0, 1, 3, 128, 0, None,
+                                         None) == N.OK
+    assert L.xgen_fp8_wire_decode_strided(N.DTYPE_BF16, 3, None, 2, 5, 0, 3, 128, (N._c_i64 * 4)(0, 0, 0, 0), 0,
+                                          None, None, None, None) == N.OK
     assert L.xgen_last_error() == b""
 
 

@@ -53,6 +53,11 @@ IMPORTED = {
         "fp8_all_to_all": "x_base/x_base/phaa/phaa_attention.py:133",
         "fp8_all_to_all_many": "x_base/x_base/phaa/phaa_attention.py:133",
     },
+    "xgen_amd.phaa.fp8_async_transport": {
+        "AsyncFP8Options": "x_diffusers/x_diffusers/adaptor/h3_cuda.py:157, x_base/tests/test_phaa_fp8.py:77",
+        "submit_fp8_exchange": "x_base/x_base/phaa/phaa_attention.py:145",
+        "finish_fp8_exchange": "x_base/x_base/phaa/phaa_attention.py:145",
+    },
     "xgen_amd.config": {
         "QuantLayerConfig": "x_comfyui/x_comfyui/framework/transformer/minimax_h3.py:68, "
                             "h3_image_optimizations.py:69,78",

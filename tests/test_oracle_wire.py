@@ -182,3 +182,96 @@ def test_wire_division_exhaustive_at_the_floor():
         bad = sum(pool.map(lambda i: L.oracle_check_wire_division(0, int(bounds[i]), int(bounds[i + 1] - 1)),
                            range(8)))
     assert bad == 0
+
+
+# --------------------------------------------------------------------------- asynchronous layouts
+# fp8_async_encode / fp8_async_decode restate the reference's per-row index formulas
+# (fp8_async_transport.py:13-80); each is held here to the synchronous codec composed with plain
+# torch reshapes, permutes and slices, which share none of that index arithmetic.
+
+
+@pytest.mark.parametrize("streams", [1, 3])
+@pytest.mark.parametrize("batch", [1, 2])
+def test_async_plain_layout_is_the_unpadded_sync_wire(streams, batch):
+    peers, seq, heads, width = 2, 5, 3, 64
+    t = qkv(peers, seq, batch, heads, width, streams, seed=7)
+    wire = R.fp8_async_encode(t, width, peers)
+    assert torch.equal(wire, R.fp8_wire_encode(t, width, peers, align16=False))
+    rows = peers * seq * batch * heads
+    outs = R.fp8_async_decode(wire, [torch.empty(rows, width, dtype=torch.float32) for _ in range(streams)],
+                              rows, width, peers)
+    ref = R.fp8_wire_decode(wire, streams, rows, width, peers, 0, torch.float32)
+    assert all(torch.equal(a, b) for a, b in zip(outs, ref))
+
+
+@pytest.mark.parametrize("valid", [1, 7, 11, 12])
+@pytest.mark.parametrize("batch", [1, 2])
+def test_async_return_pack_is_the_sync_wire_of_the_padded_permuted_output(valid, batch):
+    """RETURN_SEQ: an attention output [batch, heads, valid, D] travels as [peers, shard_seq, batch,
+    heads] rows; positions past `valid` as zero rows (scale 1e-12, zero bytes)."""
+    peers, shard_seq, heads, width = 3, 4, 2, 32
+    g = torch.Generator().manual_seed(valid + 10 * batch)
+    out = torch.randn((batch, heads, valid, width), generator=g).to(torch.bfloat16)
+    wire = R.fp8_async_encode((out,), width, peers, return_shard_seq=shard_seq)
+    padded = torch.zeros((batch, heads, peers * shard_seq, width), dtype=out.dtype)
+    padded[:, :, :valid] = out
+    rows_view = padded.reshape(batch, heads, peers, shard_seq, width).permute(2, 3, 0, 1, 4).contiguous()
+    assert torch.equal(wire, R.fp8_wire_encode((rows_view,), width, peers))
+    rows = wire.reshape(peers, shard_seq, batch, heads, width + 4)
+    dead = rows[:, :, :, :, :width].reshape(peers * shard_seq, -1)[valid:]
+    assert bool(torch.all(dead == 0))
+    scales = rows[..., width:].contiguous().view(torch.float32).reshape(peers * shard_seq, -1)[valid:]
+    assert bool(torch.all(scales == torch.tensor(1e-12, dtype=torch.float32)))
+
+
+@pytest.mark.parametrize("gather", [1, 6, 9, 10])
+def test_async_direct_gather_is_the_sync_decode_permuted(gather):
+    """GATHER_SEQ: Q/K/V head shards [peers, shard_seq, batch, heads, D] decode into [batch, heads,
+    gather, D] attention inputs; positions at or past `gather` are dropped."""
+    peers, shard_seq, batch, heads, width = 2, 5, 2, 3, 16
+    t = qkv(peers, shard_seq, batch, heads, width, 3, seed=gather)
+    wire = R.fp8_async_encode(t, width, peers)
+    rows = peers * shard_seq * batch * heads
+    sentinel = -7.0
+    outs = [torch.full((batch, heads, gather, width), sentinel) for _ in range(3)]
+    R.fp8_async_decode(wire, outs, rows, width, peers, gather_seq=gather)
+    plain = R.fp8_wire_decode(wire, 3, rows, width, peers, 0, torch.float32)
+    for got, flat in zip(outs, plain):
+        full = flat.reshape(peers * shard_seq, batch, heads, width).permute(1, 2, 0, 3)
+        assert torch.equal(got, full[:, :, :gather])
+
+
+@pytest.mark.parametrize("start", [0, 2])
+def test_async_return_layout_is_the_sync_decode_placed(start):
+    """CHUNK_HEADS / HEAD_START: one chunk of `chunk` heads per peer decodes into its place in a
+    [batch, sq, peers * heads_per_peer * D] output; the other heads stay as they were."""
+    peers, sq, batch, chunk, hpp, width = 2, 3, 2, 2, 5, 8
+    g = torch.Generator().manual_seed(start)
+    x = torch.randn((peers * sq * batch * chunk, width), generator=g)
+    wire = R.fp8_async_encode((x,), width, peers)
+    rows = x.shape[0]
+    output = torch.full((batch, sq, peers * hpp * width), -7.0)
+    expect = output.clone()
+    R.fp8_async_decode(wire, (output,), rows, width, peers, layout=(sq, batch, peers, hpp, chunk, start))
+    flat = R.fp8_wire_decode(wire, 1, rows, width, peers, 0, torch.float32)[0]
+    placed = flat.reshape(peers, sq, batch, chunk, width).permute(2, 1, 0, 3, 4)
+    expect.view(batch, sq, peers, hpp, width)[:, :, :, start:start + chunk] = placed
+    assert torch.equal(output, expect)
+
+
+def test_async_return_round_trip():
+    """The fused return pack decoded through the return layout puts every valid position of every
+    head back (head chunk at head_start), as the unfused return does."""
+    peers, shard_seq, batch, heads, width, valid, hpp, start = 2, 3, 1, 2, 16, 5, 4, 1
+    g = torch.Generator().manual_seed(3)
+    attn = torch.randn((batch, heads, valid, width), generator=g).to(torch.bfloat16)
+    wire = R.fp8_async_encode((attn,), width, peers, return_shard_seq=shard_seq)
+    rows = peers * shard_seq * batch * heads
+    output = torch.zeros((batch, shard_seq, peers * hpp * width), dtype=torch.float32)
+    R.fp8_async_decode(wire, (output,), rows, width, peers, layout=(shard_seq, batch, peers, hpp, heads, start))
+    got = output.view(batch, shard_seq, peers, hpp, width)[:, :, :, start:start + heads]
+    got = got.permute(0, 3, 2, 1, 4).reshape(batch, heads, peers * shard_seq, width)
+    scale = (attn.float().abs().amax(-1, keepdim=True) / 448).clamp_min(1e-12)
+    err = (got[:, :, :valid] - attn.float()).abs()
+    assert bool(torch.all(err <= attn.float().abs() * 2.0 ** -4 + scale * 2.0 ** -9))
+    assert bool(torch.all(got[:, :, valid:] == 0))

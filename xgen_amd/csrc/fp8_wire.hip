@@ -18,6 +18,15 @@
 // arbitrary strides (fp8_transport.py:36-48); decoded rows are written
 // contiguously, row-major (fp8_transport.py:78).
 //
+// The asynchronous transport's layouts (fp8_async_transport.py:13-80) are the
+// same rows with two more degrees of freedom: the encoder treats rows whose
+// global sequence index peer * seq + s is at least `valid_seq` as zero rows
+// without reading them (the fused return pack of a ragged attention output,
+// RETURN_SEQ, :22-27,41-44), and the strided decoder writes row (peer, s,
+// batch, head) at any element strides over those four indices, skipping rows
+// past `valid_seq` (the direct gather into [batch, heads, seq, width], :67-73,
+// and the return layout into [batch, seq, peers * heads, width], :74-78).
+//
 // Non-finite inputs (which the reference leaves to its min/max lowering): the
 // row max propagates NaN (scale NaN, every byte 0x7f, decoded NaN); an inf
 // row max gives scale inf, byte 0x7f for +-inf and signed zero for finite values.
@@ -113,6 +122,8 @@ struct EncodeArgs {
   uint8_t *wire;
   WireGeom g;
   FastDiv heads, batch;
+  uint32_t seq;        // sequence positions per peer
+  uint32_t valid_seq;  // rows with peer * seq + s >= valid_seq encode as zeros
   int width;
   int log2_lanes;
 };
@@ -253,12 +264,14 @@ __global__ __launch_bounds__(kThreads) void wire_encode_kernel(EncodeArgs a) {
     const uint32_t head = p.pr - hb * a.heads.d;
     const uint32_t sq = fast_div(hb, a.batch);
     const uint32_t b = hb - sq * a.batch.d;
+    // a row past the valid sequence is a zero row: scale 1e-12, zero bytes
+    const bool live = ok && p.peer * a.seq + sq < a.valid_seq;
     const uint8_t *row = reinterpret_cast<const uint8_t *>(t[0] + (int64_t)p.peer * t[1] + (int64_t)sq * t[2] +
                                                            (int64_t)b * t[3] + (int64_t)head * t[4]);
 #pragma unroll
     for (int j = 0; j < C; ++j) {
       const int e0 = (lig + j * lanes) * E;
-      if (ok && e0 < a.width) {
+      if (live && e0 < a.width) {
         load_chunk<DT, E, ALIGNED, NT>(row + (int64_t)e0 * kEb, r.c[j]);
       } else {
 #pragma unroll
@@ -308,6 +321,10 @@ struct DecodeArgs {
   uint8_t *dst[3];
   WireGeom g;
   int64_t dst_row_bytes;  // width * element size
+  // strided form: output byte strides over (peer, seq, batch, head), shared by the streams
+  int64_t dst_st[4];
+  FastDiv heads, batch;
+  uint32_t seq, valid_seq;  // rows with peer * seq + s >= valid_seq are not written
   int width;
   int log2_lanes;
 };
@@ -347,7 +364,7 @@ __device__ __forceinline__ void decode4(uint32_t b, float s, float (&v)[4]) {
   v[0] = lo.x * s, v[1] = lo.y * s, v[2] = hi.x * s, v[3] = hi.y * s;
 }
 
-template <int OT, int E, bool ALIGNED, int C>
+template <int OT, int E, bool ALIGNED, int C, bool STRIDED>
 __global__ __launch_bounds__(kThreads) void wire_decode_kernel(DecodeArgs a) {
   constexpr int kOb = Elem<OT>::kBytes;
   const int lanes = 1 << a.log2_lanes;
@@ -389,12 +406,23 @@ __global__ __launch_bounds__(kThreads) void wire_decode_kernel(DecodeArgs a) {
     Row nxt;
     load_row(w + step, nxt);
     const RowPos &p = cur.p;
-    uint8_t *out = reinterpret_cast<uint8_t *>(dst_tab[p.slot]) +
-                   ((int64_t)p.peer * a.g.peer_rows.d + p.pr) * a.dst_row_bytes;
+    uint8_t *out = reinterpret_cast<uint8_t *>(dst_tab[p.slot]);
+    bool live = true;
+    if constexpr (STRIDED) {
+      const uint32_t hb = fast_div(p.pr, a.heads);
+      const uint32_t head = p.pr - hb * a.heads.d;
+      const uint32_t sq = fast_div(hb, a.batch);
+      const uint32_t b = hb - sq * a.batch.d;
+      live = p.peer * a.seq + sq < a.valid_seq;
+      out += (int64_t)p.peer * a.dst_st[0] + (int64_t)sq * a.dst_st[1] + (int64_t)b * a.dst_st[2] +
+             (int64_t)head * a.dst_st[3];
+    } else {
+      out += ((int64_t)p.peer * a.g.peer_rows.d + p.pr) * a.dst_row_bytes;
+    }
 #pragma unroll
     for (int j = 0; j < C; ++j) {
       const int e0 = (lig + j * lanes) * E;
-      if (e0 < a.width) {
+      if (live && e0 < a.width) {
         if constexpr (E == 8) {  // 16-bit output, 16-byte aligned runs of 8 values
           float v0[4], v1[4];
           decode4(cur.b[j][0], cur.s, v0);
@@ -480,7 +508,11 @@ struct EncodeNtK {
 };
 template <int OT, int E, bool ALIGNED, int C>
 struct DecodeK {
-  static constexpr auto kernel = wire_decode_kernel<OT, E, ALIGNED, C>;
+  static constexpr auto kernel = wire_decode_kernel<OT, E, ALIGNED, C, false>;
+};
+template <int OT, int E, bool ALIGNED, int C>
+struct DecodeStridedK {
+  static constexpr auto kernel = wire_decode_kernel<OT, E, ALIGNED, C, true>;
 };
 
 bool is_wire_dtype(int dt) { return dt == XGEN_DTYPE_BF16 || dt == XGEN_DTYPE_F16 || dt == XGEN_DTYPE_F32; }
@@ -524,19 +556,27 @@ extern "C" int64_t xgen_fp8_wire_peer_padding(int streams, int64_t peer_rows, in
   return (16 - peer_bytes % 16) % 16;
 }
 
-extern "C" int xgen_fp8_wire_encode(int in_dtype, int streams, const void *q, const void *k, const void *v,
-                                    const int64_t *strides, int64_t peers, int64_t seq, int64_t batch,
-                                    int64_t heads, int64_t width, int64_t peer_padding, void *wire,
-                                    hipStream_t stream) {
-  const char *fn = "xgen_fp8_wire_encode";
-  if (!is_wire_dtype(in_dtype)) return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: input dtype must be BF16, F16 or F32", fn);
-  if (seq < 0 || batch < 0 || heads < 0)
-    return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: negative shape seq=%lld batch=%lld heads=%lld", fn,
-                (long long)seq, (long long)batch, (long long)heads);
+namespace xgen {
+namespace {
+
+// (peer, seq, batch, head) row geometry of a call: checks it and sets peer_rows = seq * batch * heads.
+int row_geometry(const char *fn, int64_t seq, int64_t batch, int64_t heads, int64_t valid_seq, int64_t &peer_rows) {
+  if (seq < 0 || batch < 0 || heads < 0 || valid_seq < 0)
+    return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: negative shape seq=%lld batch=%lld heads=%lld valid_seq=%lld", fn,
+                (long long)seq, (long long)batch, (long long)heads, (long long)valid_seq);
   if (seq > 0x7fffffffLL || batch > 0x7fffffffLL || heads > 0x7fffffffLL ||
       (batch && heads && seq > 0x7fffffffLL / batch / heads))
     return fail(XGEN_ERR_UNSUPPORTED, "%s: peer rows exceed 2^31 - 1", fn);
-  const int64_t peer_rows = seq * batch * heads;
+  peer_rows = seq * batch * heads;
+  return XGEN_OK;
+}
+
+int wire_encode(const char *fn, int in_dtype, int streams, const void *q, const void *k, const void *v,
+                const int64_t *strides, int64_t peers, int64_t seq, int64_t batch, int64_t heads, int64_t width,
+                int64_t valid_seq, int64_t peer_padding, void *wire, hipStream_t stream) {
+  if (!is_wire_dtype(in_dtype)) return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: input dtype must be BF16, F16 or F32", fn);
+  int64_t peer_rows = 0;
+  if (int st = row_geometry(fn, seq, batch, heads, valid_seq, peer_rows)) return st;
   EncodeArgs a;
   if (int st = wire_geometry(fn, streams, peers, peer_rows, width, peer_padding, a.g)) return st;
   if (peer_rows == 0) return ok();
@@ -564,6 +604,9 @@ extern "C" int xgen_fp8_wire_encode(int in_dtype, int streams, const void *q, co
   a.wire = static_cast<uint8_t *>(wire);
   a.heads = make_fastdiv((uint32_t)heads);
   a.batch = make_fastdiv((uint32_t)batch);
+  a.seq = (uint32_t)seq;
+  // peers * seq < 2^30 (wire_geometry), so a larger valid_seq masks nothing
+  a.valid_seq = (uint32_t)(valid_seq < peers * seq ? valid_seq : peers * seq);
   a.width = (int)width;
   // chunks of 8 values (16-byte loads of 16-bit input) or 4 (16-byte f32 / 8-byte loads)
   const Shape sh = pick_shape((int)width, vec16 ? 8 : 4, kEncodeChunks);
@@ -590,11 +633,33 @@ extern "C" int xgen_fp8_wire_encode(int in_dtype, int streams, const void *q, co
   return launch_status(fn);
 }
 
-extern "C" int xgen_fp8_wire_decode(int out_dtype, int streams, const void *wire, int64_t peers,
-                                    int64_t peer_rows, int64_t width, int64_t peer_padding, void *q, void *k,
-                                    void *v, hipStream_t stream) {
-  const char *fn = "xgen_fp8_wire_decode";
+template <template <int, int, bool, int> class K>
+void launch_decode(int out_dtype, bool vec, const DecodeArgs &a, const Shape &sh, hipStream_t stream) {
+  switch (out_dtype) {
+    case XGEN_DTYPE_BF16:
+      if (vec) launch_ec<K, XGEN_DTYPE_BF16, true>(a, sh, stream);
+      else launch_ec<K, XGEN_DTYPE_BF16, false>(a, sh, stream);
+      break;
+    case XGEN_DTYPE_F16:
+      if (vec) launch_ec<K, XGEN_DTYPE_F16, true>(a, sh, stream);
+      else launch_ec<K, XGEN_DTYPE_F16, false>(a, sh, stream);
+      break;
+    default:
+      if (vec) launch_ec<K, XGEN_DTYPE_F32, true>(a, sh, stream);
+      else launch_ec<K, XGEN_DTYPE_F32, false>(a, sh, stream);
+      break;
+  }
+}
+
+// dst_strides: null for contiguous [peers * peer_rows, width] outputs, else 4 element strides over
+// (peer, seq, batch, head) with rows past valid_seq skipped.
+int wire_decode(const char *fn, int out_dtype, int streams, const void *wire, int64_t peers, int64_t seq,
+                int64_t batch, int64_t heads, int64_t width, int64_t peer_padding, const int64_t *dst_strides,
+                int64_t valid_seq, void *q, void *k, void *v, hipStream_t stream) {
   if (!is_wire_dtype(out_dtype)) return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: output dtype must be BF16, F16 or F32", fn);
+  int64_t peer_rows = seq;  // contiguous outputs: (seq, batch, heads) = (peer_rows, 1, 1)
+  if (dst_strides)
+    if (int st = row_geometry(fn, seq, batch, heads, valid_seq, peer_rows)) return st;
   DecodeArgs a;
   if (int st = wire_geometry(fn, streams, peers, peer_rows, width, peer_padding, a.g)) return st;
   if (peer_rows == 0) return ok();
@@ -608,26 +673,66 @@ extern "C" int xgen_fp8_wire_decode(int out_dtype, int streams, const void *wire
     vec = vec && aligned_to(dst[s], 4 * eb);
     vec16 = vec16 && aligned16(dst[s]);
   }
+  if (dst_strides) {
+    for (int d = 0; d < 4; ++d) {
+      const int64_t x = dst_strides[d];
+      if (x < 0) return fail(XGEN_ERR_INVALID_ARGUMENT, "%s: negative stride", fn);
+      if (x > (int64_t)1 << 46) return fail(XGEN_ERR_UNSUPPORTED, "%s: stride too large", fn);
+      vec16 = vec16 && x % 8 == 0;
+      vec = vec && x % 4 == 0;
+      a.dst_st[d] = x * eb;
+    }
+  } else {
+    for (int d = 0; d < 4; ++d) a.dst_st[d] = 0;
+  }
   a.wire = static_cast<const uint8_t *>(wire);
   for (int s = 0; s < 3; ++s) a.dst[s] = static_cast<uint8_t *>(dst[s]);
   a.dst_row_bytes = width * eb;
+  a.heads = make_fastdiv((uint32_t)(heads > 0 ? heads : 1));
+  a.batch = make_fastdiv((uint32_t)(batch > 0 ? batch : 1));
+  a.seq = (uint32_t)seq;
+  a.valid_seq = (uint32_t)(valid_seq < peers * seq ? valid_seq : peers * seq);
   a.width = (int)width;
   // chunks of 8 values (16-byte stores of 16-bit output) or 4 (16-byte f32 / 8-byte stores)
   const Shape sh = pick_shape((int)width, vec16 ? 8 : 4, kDecodeChunks);
   a.log2_lanes = sh.log2_lanes;
-  switch (out_dtype) {
-    case XGEN_DTYPE_BF16:
-      if (vec) launch_ec<DecodeK, XGEN_DTYPE_BF16, true>(a, sh, stream);
-      else launch_ec<DecodeK, XGEN_DTYPE_BF16, false>(a, sh, stream);
-      break;
-    case XGEN_DTYPE_F16:
-      if (vec) launch_ec<DecodeK, XGEN_DTYPE_F16, true>(a, sh, stream);
-      else launch_ec<DecodeK, XGEN_DTYPE_F16, false>(a, sh, stream);
-      break;
-    default:
-      if (vec) launch_ec<DecodeK, XGEN_DTYPE_F32, true>(a, sh, stream);
-      else launch_ec<DecodeK, XGEN_DTYPE_F32, false>(a, sh, stream);
-      break;
-  }
+  if (dst_strides) launch_decode<DecodeStridedK>(out_dtype, vec, a, sh, stream);
+  else launch_decode<DecodeK>(out_dtype, vec, a, sh, stream);
   return launch_status(fn);
+}
+
+}  // namespace
+}  // namespace xgen
+
+extern "C" int xgen_fp8_wire_encode(int in_dtype, int streams, const void *q, const void *k, const void *v,
+                                    const int64_t *strides, int64_t peers, int64_t seq, int64_t batch,
+                                    int64_t heads, int64_t width, int64_t peer_padding, void *wire,
+                                    hipStream_t stream) {
+  return wire_encode("xgen_fp8_wire_encode", in_dtype, streams, q, k, v, strides, peers, seq, batch, heads, width,
+                     INT64_MAX, peer_padding, wire, stream);
+}
+
+extern "C" int xgen_fp8_wire_encode_masked(int in_dtype, int streams, const void *q, const void *k,
+                                           const void *v, const int64_t *strides, int64_t peers, int64_t seq,
+                                           int64_t batch, int64_t heads, int64_t width, int64_t valid_seq,
+                                           void *wire, hipStream_t stream) {
+  return wire_encode("xgen_fp8_wire_encode_masked", in_dtype, streams, q, k, v, strides, peers, seq, batch, heads,
+                     width, valid_seq, 0, wire, stream);
+}
+
+extern "C" int xgen_fp8_wire_decode(int out_dtype, int streams, const void *wire, int64_t peers,
+                                    int64_t peer_rows, int64_t width, int64_t peer_padding, void *q, void *k,
+                                    void *v, hipStream_t stream) {
+  // contiguous outputs: the rows as one sequence axis
+  return wire_decode("xgen_fp8_wire_decode", out_dtype, streams, wire, peers, peer_rows, 1, 1, width, peer_padding,
+                     nullptr, INT64_MAX, q, k, v, stream);
+}
+
+extern "C" int xgen_fp8_wire_decode_strided(int out_dtype, int streams, const void *wire, int64_t peers,
+                                            int64_t seq, int64_t batch, int64_t heads, int64_t width,
+                                            const int64_t *dst_strides, int64_t valid_seq, void *q, void *k,
+                                            void *v, hipStream_t stream) {
+  if (!dst_strides) return fail(XGEN_ERR_INVALID_ARGUMENT, "xgen_fp8_wire_decode_strided: null pointer");
+  return wire_decode("xgen_fp8_wire_decode_strided", out_dtype, streams, wire, peers, seq, batch, heads, width, 0,
+                     dst_strides, valid_seq, q, k, v, stream);
 }
