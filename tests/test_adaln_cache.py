@@ -151,3 +151,37 @@ def test_adaln_indices():
     tags = torch.tensor([0, 1, 2, -1, 1, 0])
     assert adaln_indices(t, tags).tolist() == [0, 1, 5, 3, 7, 6]
     assert adaln_indices(t, tags).dtype == torch.int64
+
+
+def test_install_adaln_cache_hands_the_cache_to_its_readers(tmp_path, monkeypatch):
+    """cache.py:299-333: one cache for the transformer; every block's adaln_proj gets its index and
+    the cache, norm_out and the transformer get the cache, and a flagged transformer counts the load."""
+    from types import SimpleNamespace
+
+    from xgen_amd.adaln_cache import cache as C
+    from xgen_amd.adaln_cache import install_adaln_cache
+    path = tmp_path / "t.safetensors"
+    save_file({"step0_timesteps": torch.tensor([.5]), "step0_block0": torch.zeros(1, 36, dtype=torch.bfloat16),
+               "step0_block1": torch.ones(1, 36, dtype=torch.bfloat16),
+               "step0_final": torch.zeros(1, 4, dtype=torch.bfloat16)}, path, metadata=dict(num_steps="2"))
+
+    class OnCpu(C.AdalnScheduleCache):
+        def __init__(self, model=None, cache_file=None, conditioning_type="none"):
+            super().__init__(model, cache_file, conditioning_type, device="cpu")
+
+    monkeypatch.setattr(C, "AdalnScheduleCache", OnCpu)
+    blocks = [SimpleNamespace(adaln_proj=SimpleNamespace()) for _ in range(2)]
+    transformer = SimpleNamespace(transformer_blocks=blocks, norm_out=SimpleNamespace(),
+                                  _h3_cuda_adaln_table=True, _h3_cuda_adaln_load_count=4)
+    cache = install_adaln_cache(SimpleNamespace(transformer=transformer), str(path), conditioning_type="none")
+    assert isinstance(cache, OnCpu) and cache.model is transformer
+    assert [b.adaln_proj._block_idx for b in blocks] == [0, 1]
+    assert all(b.adaln_proj._adaln_cache is cache for b in blocks)
+    assert transformer.norm_out._adaln_cache is cache and transformer._adaln_cache is cache
+    assert transformer._h3_cuda_adaln_load_count == 5
+    plain = SimpleNamespace(transformer_blocks=blocks, norm_out=SimpleNamespace())
+    other = install_adaln_cache(SimpleNamespace(transformer=plain), str(path))
+    assert plain._adaln_cache is other and not hasattr(plain, "_h3_cuda_adaln_load_count")
+    assert all(b.adaln_proj._adaln_cache is other for b in blocks)
+    cache.maybe_install(torch.tensor([.5]))
+    assert torch.equal(cache.lookup_block(1).gate_mlp, torch.ones(3, 2, dtype=torch.bfloat16))

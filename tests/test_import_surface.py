@@ -65,6 +65,7 @@ IMPORTED = {
     "xgen_amd.adaln_cache": {
         "AdalnScheduleCache": "x_comfyui/x_comfyui/framework/transformer/minimax_h3.py:67, "
                               "tools/adaln_cache/prepare_cuda_adaln.py:119",
+        "install_adaln_cache": "server/video/video_server.py:711, x_base/x_base/__init__.py:21",
     },
 }
 

@@ -212,6 +212,26 @@ class AdalnScheduleCache:
             register_one_plus(raw, out)
         t["one_plus"] = [tuple(prepared[j].chunk(2, dim=-1)) for j in range(nb)]
 
+
+def install_adaln_cache(pipe, cache_file: str | None = None, conditioning_type: str = "none"):
+    """Builds the cache for pipe.transformer and hands it to the modules that read it
+    (x_base/x_base/adaln_cache/cache.py:299-333; called after the pipeline is built, e.g.
+    server/video/video_server.py:711): each block's adaln_proj gets `_block_idx` and `_adaln_cache`,
+    norm_out and the transformer get `_adaln_cache` (the transformer's forward installs the step's
+    schedule through it), and a transformer carrying the `_h3_cuda_adaln_table` flag counts the load in
+    `_h3_cuda_adaln_load_count`.  Returns the cache."""
+    transformer = pipe.transformer
+    cache = AdalnScheduleCache(transformer, cache_file=cache_file, conditioning_type=conditioning_type)
+    for index, block in enumerate(transformer.transformer_blocks):
+        proj = block.adaln_proj
+        proj._block_idx, proj._adaln_cache = index, cache
+    transformer.norm_out._adaln_cache = cache
+    transformer._adaln_cache = cache
+    if getattr(transformer, "_h3_cuda_adaln_table", False):
+        transformer._h3_cuda_adaln_load_count += 1
+    return cache
+
+
 def _rows(raw: torch.Tensor) -> torch.Tensor:
     """A block table [M, 18H] as its [3M, 6H] modality rows (cache.py:116-118)."""
     if raw.dim() != 2 or raw.shape[-1] % (6 * MODALITY_NUM):
