@@ -62,7 +62,8 @@ def parse():
 PROFILE_KERNELS = ("gemm_fp8_qkv", "gemm_fp8_qkv_exact", "gemm_int8_qkv", "gemm_fp8_ffn_up_gelu", "gemm_fp8_ffn_up",
                    "gemm_fp8_ffn_down",
                    "quant_rows_fp8", "requant_fp8_12288", "requant_gelu_fp8_12288", "front_end_ln_mod_quant_fp8", "gate_residual_op", "swiglu_quant_int8_h3",
-                   "wire_encode_h3", "wire_decode_h3", "copy_1gib")
+                   "wire_encode_h3", "wire_decode_h3", "wire_async_gather_decode_h3", "wire_async_return_pack_h3",
+                   "wire_async_return_layout_decode_h3", "copy_1gib")
 
 
 def wire_setup(M, g, dev):
@@ -179,6 +180,8 @@ def profile_kernels(names, steps, warmup):
         elif name == "swiglu_quant_int8_h3":
             u3 = torch.randn((1, M, 2 * 14336), generator=g, device=dev).to(torch.bfloat16)
             fn = lambda: xops.swiglu_quant(u3, False, torch.int8, 1, False)  # noqa: E731
+        elif name.startswith("wire_async_"):
+            fn = {n: f for n, f, _ in async_wire_setup(M, g, dev)}[name]
         elif name.startswith("wire_"):
             enc, dec, _, _ = wire_setup(M, g, dev)
             enc()
