@@ -12,11 +12,12 @@ Also timed (HIP events on the launch stream, same process): the GEMM alone
 (roofline), the per-token quantizer alone, the fused LayerNorm + AdaLN
 modulate + FP8 quant front end, the FFN up (with and without the GELU-tanh
 epilogue) / down GEMMs, the FFN-down requant with and without the GELU, the INT8
-QKV and FFN-up GEMMs, the QKV GEMM with exact accumulation, the same QKV launch
-on all-zero and all-one operands (the clock follows the data), hipBLASLt's
-torch._scaled_mm on the QKV operands, the reference's default per-tensor
-H3FP8Linear, the path's neighbours (gated residual, SwiGLU requant, FP8 wire
-codec and the asynchronous exchange's gather / return layouts) and the C5 chain.  The CPU baseline is the oracle's
+QKV and FFN-up GEMMs, the QKV GEMM with exact accumulation, the same QKV launches
+(FP8 both kinds, INT8) on all-zero and all-one operands (the clock follows the
+data), hipBLASLt's torch._scaled_mm on the QKV operands, the reference's default
+per-tensor H3FP8Linear, the path's neighbours (gated residual, SwiGLU requant,
+FP8 wire codec and the asynchronous exchange's gather / return layouts) and the
+C5 chain.  The CPU baseline is the oracle's
 quantize-dequantize linear on config C1 (FP8 and INT8) plus a bounded row
 sample of the QKV workload, on the host threads this process may use.
 
@@ -474,7 +475,7 @@ def main():
             "frac_of_fp8_peak": flop / (ms_ex * 1e-3) / 1e12 / PEAK_FP8_TFLOPS,
             "frac_of_bf16_peak": flop / (ms_ex * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}
 
-    # ---- the same QKV launches on all-zero and all-one e4m3 bytes: the instruction stream is
+    # ---- the same QKV launches on all-zero and all-one operands: the instruction stream is
     # unchanged, only the data the matrix cores multiply (and with it the power, so the clock) differ
     if want("operands"):
         power = {}
@@ -486,8 +487,13 @@ def main():
                 ms_o = timed(lambda: xops.scaled_mm(a_t, w_t, sa0, sw, b, torch.bfloat16, N.ACT_NONE, False, exact),
                              args.steps, args.warmup)
                 row[kind] = {"ms": ms_o, "tflops": flop / (ms_o * 1e-3) / 1e12}
+            ai, wi = torch.full(qa0.shape, int(label == "ones"), dtype=torch.int8, device=dev), \
+                torch.full(qw.shape, int(label == "ones"), dtype=torch.int8, device=dev)
+            ms_o = timed(lambda: xops.scaled_mm(ai, wi, sa0, sw, b, torch.bfloat16, N.ACT_NONE, False),
+                         args.steps, args.warmup)
+            row["int8"] = {"ms": ms_o, "tops": flop / (ms_o * 1e-3) / 1e12}
             power[label] = row
-            del a_t, w_t
+            del a_t, w_t, ai, wi
         kernels["gemm_qkv_constant_operands"] = power
 
     # ---- the reference's own GEMM call on this GPU: torch._scaled_mm (hipBLASLt) on the same QKV
