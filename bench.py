@@ -43,7 +43,7 @@ PEAK_BF16_TFLOPS = 2500.0  # MI355X dense BF16 MFMA (the exact-accumulation kind
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 # HBM (fabric) bytes per launch of the QKV GEMM, from rocprofv3 FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000
 # (copy-kernel calibration); profiles/hbm_traffic_c2_qkv_gemm_and_path_kernels.md holds the counts.
-QKV_GEMM_TRAFFIC_BYTES = (364868 * 2.0 + 281395 * 1.0) * 1024
+QKV_GEMM_TRAFFIC_BYTES = (364868 * 2.0 + 281602 * 1.0) * 1024
 METRIC = "FP8 W8A8 linear TFLOP/s (% MFMA peak) + quant GB/s, M=15.6k d=3072, 1 GPU"
 
 
