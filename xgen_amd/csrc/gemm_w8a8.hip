@@ -897,8 +897,12 @@ int gemm_entry(const char *fn, const void *a, int64_t lda, const void *w, int64_
   g.per_xcd = (g.tiles_m * g.tiles_n + 7) / 8;
   // The 32 tiles one XCD runs at once span group_m tile-rows; measured at
   // M=15,624: 8 rows beat 4 for QKV and FFN up by ~1% and tie for FFN down; 2
-  // are 4-7% slower, 16 no better.
-  g.group_m = 8;
+  // are 4-7% slower, 16 no better.  An activation operand larger than the
+  // last-level cache (C5's FFN down: 31,248 x 12,288 bytes) takes 4: the eight
+  // XCDs' groups then hold 100 instead of 200 MB of it at once (FFN down at
+  // M=31,248: 923 against 962-967 us; the H3 FFN down and the M=31,248 QKV and
+  // FFN up, whose activations fit, stay fastest with 8).
+  g.group_m = (int64_t)M * K > kLastLevelCacheBytes ? 4 : 8;
   g.a_bytes = (uint32_t)a_bytes;
   g.w_bytes = (uint32_t)w_bytes;
   g.residual = static_cast<const uint8_t *>(gp.residual);
