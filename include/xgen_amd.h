@@ -181,7 +181,9 @@ int xgen_norm_affine_quant(const void *x, int64_t batch, int64_t seq, int64_t wi
  * out_dtype BF16 or F16, out [M, N] with leading dimension ldo.
  * acc_out: NULL or float32 [M, N] (leading dimension N) receiving acc.
  * Requires K % 16 == 0 and N % 16 == 0 (the reference's alignment,
- * h3_fp8.py:20-21), 16-byte aligned a/w rows.
+ * h3_fp8.py:20-21), 16-byte aligned a/w rows, and w below 2 GiB.  M is not
+ * bounded by the kernels' 32-bit offsets: rows beyond them run as consecutive
+ * launches over row chunks, with the results of one launch.
  */
 int xgen_scaled_mm_fp8(const void *a, int64_t lda, const void *w, int64_t ldw, int64_t M,
                        int64_t N, int64_t K, const float *a_scale, int64_t a_scale_stride,

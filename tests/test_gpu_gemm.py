@@ -366,3 +366,48 @@ def test_seeded_shape_sweep(cuda, kind):
             assert ((acc.cpu().double() - exact).abs() <= acc_bound + 1e-30).all(), (M, K, Nf)
         ref = R.w8a8_linear_fp8(qa.cpu(), sa.cpu(), qw.cpu(), sw.cpu(), bias.cpu())
         assert_within_rounding(out, ref, exact.abs(), sa, sw, bias, acc_bound)
+
+
+@pytest.mark.parametrize("kind", ["fp8", "exact", "int8"])
+def test_rows_past_32bit_offsets_run_as_chunks(cuda, kind):
+    """An output above 2 GiB (66,048 x 16,384 bf16) is computed as row chunks within the kernels'
+    32-bit offsets: bit-identical, accumulators included, to the same GEMM on the two halves of the
+    rows (each half below the limits, one launch each)."""
+    M, Nf, K = 66048, 16384, 64
+    g = torch.Generator(device=cuda).manual_seed(31)
+    x = torch.randn((M, K), generator=g, device=cuda).to(torch.bfloat16)
+    w = (torch.randn((Nf, K), generator=g, device=cuda) * 0.02).to(torch.bfloat16)
+    b = (torch.randn((Nf,), generator=g, device=cuda) * 0.01).to(torch.bfloat16)
+    dt = torch.int8 if kind == "int8" else torch.float8_e4m3fn
+    qa, sa = xops.quantize_rows(x, dt)
+    qw, sw = xops.quantize_rows(w, dt)
+    exact = kind == "exact"
+    full, acc = xops.scaled_mm(qa, qw, sa, sw, b, torch.bfloat16, N.ACT_NONE, True, exact)
+    assert full.numel() * 2 > 2 ** 31
+    half = M // 2
+    for rows in (slice(0, half), slice(half, M)):
+        part, part_acc = xops.scaled_mm(qa[rows], qw, sa[rows], sw, b, torch.bfloat16, N.ACT_NONE, True, exact)
+        assert torch.equal(full[rows].view(torch.int16), part.view(torch.int16))
+        assert torch.equal(acc[rows], part_acc)
+
+
+def test_gated_rows_past_32bit_offsets_run_as_chunks(cuda):
+    """The gated form too: chunks start at token position 0 of the AdaLN index table (M a multiple
+    of seq), so the output equals the two halves computed apart."""
+    M, Nf, K, seq, T = 66048, 16384, 64, 1032, 5
+    g = torch.Generator(device=cuda).manual_seed(37)
+    x = torch.randn((M, K), generator=g, device=cuda).to(torch.bfloat16)
+    w = (torch.randn((Nf, K), generator=g, device=cuda) * 0.02).to(torch.bfloat16)
+    b = (torch.randn((Nf,), generator=g, device=cuda) * 0.01).to(torch.bfloat16)
+    res = torch.randn((M, Nf), generator=g, device=cuda).to(torch.bfloat16)
+    gate = torch.randn((T, Nf), generator=g, device=cuda).to(torch.bfloat16)
+    idx = torch.randint(T, (seq,), generator=g, device=cuda)
+    qa, sa = xops.quantize_rows(x, torch.float8_e4m3fn)
+    qw, sw = xops.quantize_rows(w, torch.float8_e4m3fn)
+    full = xops.scaled_mm_gate_residual(qa, qw, sa, sw, b, res, gate, idx)
+    assert full.numel() * 2 > 2 ** 31
+    half = M // 2
+    assert half % seq == 0
+    for rows in (slice(0, half), slice(half, M)):
+        part = xops.scaled_mm_gate_residual(qa[rows], qw, sa[rows], sw, b, res[rows], gate, idx)
+        assert torch.equal(full[rows].view(torch.int16), part.view(torch.int16))

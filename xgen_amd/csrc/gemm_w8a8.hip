@@ -863,10 +863,36 @@ int gemm_entry(const char *fn, const void *a, int64_t lda, const void *w, int64_
     if (gp.ld_residual % 8 || gp.gate_stride % 8 || !aligned16(gp.residual) || !aligned16(gp.gate))
       return fail(XGEN_ERR_UNSUPPORTED, "%s: residual and gate rows must be 16-byte aligned", fn);
     if (M >= 0x7fffffffLL) return fail(XGEN_ERR_UNSUPPORTED, "%s: too many rows", fn);
-    // 32-bit offsets of the residual rows (past M included) and of the gate rows
-    if ((uint64_t)(M + 256) * (uint64_t)gp.ld_residual * 2 >= (1ull << 31) ||
-        (uint64_t)gp.gate_rows * (uint64_t)gp.gate_stride * 2 >= (1ull << 31))
-      return fail(XGEN_ERR_UNSUPPORTED, "%s: residual or gate table above 2 GiB", fn);
+    // 32-bit offsets of the gate rows
+    if ((uint64_t)gp.gate_rows * (uint64_t)gp.gate_stride * 2 >= (1ull << 31))
+      return fail(XGEN_ERR_UNSUPPORTED, "%s: gate table above 2 GiB", fn);
+  }
+  // The kernels address the activation rows, the output rows and the residual rows through 32-bit
+  // buffer offsets (rows past M of the last tile-row included).  A call whose rows pass those
+  // limits runs as consecutive launches over row chunks: each output row is computed by the same
+  // tiles in the same K order whichever launch it falls in, so the results are those of one launch.
+  int64_t rows = M;
+  auto cap = [&](int64_t limit) { rows = limit < rows ? limit : rows; };
+  cap((0x7fffffffLL - K) / lda + 1);                   // activation bytes below 2^31
+  cap(0xffffffffLL / lda - 512);                       // DMA offsets of the rows past M below 2^32
+  cap((0x7fffffffLL - 2 * N) / (2 * ldo) + 1);         // output bytes below 2^31
+  cap(0xffffffffLL / (2 * ldo) - 256);                 // store offsets of the rows past M below 2^32
+  if (gated) cap(0x7fffffffLL / (2 * gp.ld_residual) - 256);  // residual rows past M below 2^31
+  if (rows < M) {
+    rows = rows / 256 * 256;                           // whole tile-rows
+    if (gated) rows = rows / gp.seq * gp.seq;          // chunks start at token position 0
+    if (rows <= 0) return fail(XGEN_ERR_UNSUPPORTED, "%s: operand rows too long for 32-bit offsets", fn);
+    for (int64_t m0 = 0; m0 < M; m0 += rows) {
+      const int64_t mi = M - m0 < rows ? M - m0 : rows;
+      GateParams gc = gp;
+      if (gated) gc.residual = static_cast<const uint8_t *>(gp.residual) + m0 * gp.ld_residual * 2;
+      const int st = gemm_entry<KIND>(
+          fn, static_cast<const uint8_t *>(a) + m0 * lda, lda, w, ldw, mi, N, K, sa_stride ? sa + m0 : sa, sa_stride,
+          sw, sw_stride, bias, bias_dtype, activation, static_cast<uint8_t *>(out) + m0 * ldo * 2, out_dtype, ldo,
+          acc_out ? static_cast<uint8_t *>(acc_out) + m0 * N * 4 : nullptr, stream, gc);
+      if (st != XGEN_OK) return st;
+    }
+    return ok();
   }
   const int64_t a_bytes = (M - 1) * lda + K, w_bytes = (N - 1) * ldw + K;
   if (a_bytes >= (int64_t)kOutOfRange || w_bytes >= (int64_t)kOutOfRange)
