@@ -250,3 +250,46 @@ def test_h3_geometry_direct_gather_and_return_pack(cuda):
     q, s = R.wire_rows_fp8(attn[0][:, pos].float().cpu().reshape(-1, width))
     assert torch.equal(flat[pos][:, :, :width].permute(1, 0, 2).reshape(-1, width).cpu(), q)
     assert torch.equal(sc[pos].t().reshape(-1).cpu(), s)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_return_pack_special_rows_and_odd_geometry(cuda, dtype):
+    """Three peers, three batches, the narrowest rows (width 4) and special rows in a ragged
+    attention output: zero, tiny, outlier, NaN and Inf rows, bytes and scales bit-exact against the
+    oracle, decoded through the return layout (NaN matching NaN)."""
+    peers, shard_seq, batch, heads, width, valid = 3, 5, 3, 2, 4, 13
+    g = torch.Generator().manual_seed(11)
+    attn = torch.randn((batch, heads, valid, width), generator=g)
+    attn[0, 0, 0] = 0.0
+    attn[0, 1, 1] = 1e-30
+    attn[1, 0, 2, 1] = 3e4
+    attn[1, 1, 3, 2] = float("nan")
+    attn[2, 0, 4, 0] = float("inf")
+    attn = attn.to(dtype)
+    send, recv, rows = pack(peers, None, (attn.to(cuda),), width, return_shard_seq=shard_seq)
+    ref = R.fp8_async_encode((attn,), width, peers, return_shard_seq=shard_seq)
+    assert torch.equal(send.cpu(), ref)
+    recv.copy_(send)
+    layout = (shard_seq, batch, peers, heads + 1, heads, 1)
+    out = torch.full((batch, shard_seq, peers * (heads + 1) * width), 5.0, dtype=dtype, device=cuda)
+    expect = out.cpu()
+    T._unpack_exchange(recv, (out,), rows, layout)
+    R.fp8_async_decode(ref, (expect,), rows.rows, width, peers, layout=layout)
+    assert same(out.cpu(), expect)
+
+
+@pytest.mark.parametrize("width", [4, 12, 68, 260])
+def test_direct_gather_widths(cuda, width):
+    """Row widths off the 16-byte chunk (the kernels' 4-value and element-wise forms)."""
+    peers, shard_seq, batch, heads, gather = 2, 3, 1, 2, 5
+    g = torch.Generator().manual_seed(width)
+    t = tuple(torch.randn((peers, shard_seq, batch, heads, width), generator=g).to(torch.bfloat16) for _ in range(3))
+    outs = tuple(torch.empty((batch, heads, gather, width), dtype=torch.float32, device=cuda) for _ in range(3))
+    send, recv, rows = pack(peers, outs, tuple(x.to(cuda) for x in t), width, direct_gather=True)
+    ref = R.fp8_async_encode(t, width, peers)
+    assert torch.equal(send.cpu(), ref)
+    recv.copy_(send)
+    T._unpack_exchange(recv, outs, rows)
+    expect = R.fp8_async_decode(ref, [torch.empty((batch, heads, gather, width)) for _ in range(3)], rows.rows,
+                                width, peers, gather_seq=gather)
+    assert all(same(a.cpu(), b) for a, b in zip(outs, expect))
