@@ -1,0 +1,75 @@
+"""The reference's fused operators under their own torch.ops names (xgen_amd.reference_ops): the
+schemas of their TORCH_LIBRARY definitions, and the reference's Meta contract suite
+(x_base/tests/test_npu_fusion_meta.py:33-48, 67-73) run against both the op handles and this
+package's wrapper modules, with no device initialized."""
+import pytest
+import torch
+
+import xgen_amd  # noqa: F401  (registers torch.ops.h3_phaa_*)
+from xgen_amd.operator import gate_residual, nq2, swiglu_quant
+
+M = torch.device("meta")
+
+
+def tensor(*shape, dtype=torch.bfloat16):
+    return torch.empty(shape, device=M, dtype=dtype)
+
+
+@pytest.mark.parametrize("op,schema", [
+    (lambda: torch.ops.h3_phaa_nq2.fused, "h3_phaa_nq2::fused(Tensor x, Tensor weight, Tensor scale, Tensor shift, "
+     "Tensor indices, float eps=1.0000000000000001e-05, int blocks=40) -> (Tensor, Tensor)"),
+    (lambda: torch.ops.h3_phaa_nq2_cached.fused, "h3_phaa_nq2_cached::fused(Tensor x, Tensor weight, Tensor scale, "
+     "Tensor shift, Tensor indices, float eps=1.0000000000000001e-05, int blocks=40) -> (Tensor, Tensor)"),
+    (lambda: torch.ops.h3_phaa_gate_residual.gate_residual, "h3_phaa_gate_residual::gate_residual(Tensor residual, "
+     "Tensor branch, Tensor gate_table, Tensor indices, int tile=5376, int blocks=40) -> Tensor"),
+    (lambda: torch.ops.h3_phaa_fusion_quant.swiglu_quantize, "h3_phaa_fusion_quant::swiglu_quantize(Tensor u, "
+     "int tile=2048, int blocks=40, int scale_mode=1) -> (Tensor, Tensor)"),
+    (lambda: torch.ops.h3_phaa_fusion_quant_vector.swiglu_quantize, "h3_phaa_fusion_quant_vector::swiglu_quantize("
+     "Tensor u, int tile=2048, int blocks=40, int scale_mode=1) -> (Tensor, Tensor)"),
+    (lambda: torch.ops.h3_phaa_fusion_quant_reuse.swiglu_quantize, "h3_phaa_fusion_quant_reuse::swiglu_quantize("
+     "Tensor u, int tile=4096, int blocks=40, int scale_mode=1) -> (Tensor, Tensor)"),
+])
+def test_schemas_are_the_references(op, schema):
+    """nq2_queued.asc:47-51, gate_residual_queued.asc:31, swiglu_quant*_queued.asc:33."""
+    assert str(op()._schemas[""]) == schema
+
+
+def test_swiglu_and_width_boundary():
+    """test_npu_fusion_meta.py:33-38: [B, S, 2F] -> int8 [B*S, F] + f32 [B*S]; 2F = 28,674 rejected."""
+    for fn in (swiglu_quant.swiglu_quantize_reuse, torch.ops.h3_phaa_fusion_quant_reuse.swiglu_quantize):
+        q, scale = fn(tensor(2, 17, 96))
+        assert q.shape == (34, 48) and scale.shape == (34,) and q.dtype == torch.int8
+    with pytest.raises(RuntimeError):
+        torch.ops.h3_phaa_fusion_quant_reuse.swiglu_quantize(tensor(1, 2, 28674))
+    with pytest.raises(RuntimeError, match="tile"):
+        torch.ops.h3_phaa_fusion_quant.swiglu_quantize(tensor(2, 17, 96), 4096)
+
+
+def test_gate_and_norm_contracts():
+    """test_npu_fusion_meta.py:40-48: the gate keeps the residual's shape; nq2 gives int8 [B*S, H]
+    and f32 [B*S]; H = 6,145 rejected."""
+    value, table = tensor(2, 17, 64), tensor(3, 64)
+    indices = tensor(17, dtype=torch.int64)
+    for gate in (gate_residual.gate_residual, torch.ops.h3_phaa_gate_residual.gate_residual):
+        assert gate(value, value, table, indices).shape == value.shape
+    for norm in (lambda *a: nq2.norm_affine_quant(*a, cached=True), torch.ops.h3_phaa_nq2_cached.fused,
+                 torch.ops.h3_phaa_nq2.fused):
+        q, scale = norm(value, tensor(64), table, table, indices)
+        assert q.shape == (34, 64) and scale.shape == (34,) and q.dtype == torch.int8
+    with pytest.raises(RuntimeError):
+        torch.ops.h3_phaa_nq2_cached.fused(tensor(1, 2, 6145), tensor(6145), tensor(3, 6145), tensor(3, 6145),
+                                          tensor(2, dtype=torch.int64))
+    with pytest.raises(RuntimeError, match="indices"):
+        torch.ops.h3_phaa_nq2.fused(value, tensor(64), table, table, tensor(16, dtype=torch.int64))
+    with pytest.raises(RuntimeError, match="gate_table"):
+        torch.ops.h3_phaa_gate_residual.gate_residual(value, value, tensor(3, 32), indices)
+
+
+def test_device_remains_uninitialized():
+    """test_npu_fusion_meta.py:67-73."""
+    assert not torch.cuda.is_initialized()
+
+
+def test_register_is_idempotent():
+    from xgen_amd import reference_ops
+    assert reference_ops.register() == []

@@ -7,6 +7,7 @@ operators (xgen_amd.ops) and as modules with the reference's surface
 HIP library is loaded on first use.
 """
 from . import ops  # noqa: F401  (registers torch.ops.xgen_amd.*)
+from . import reference_ops  # noqa: F401  (registers the reference's torch.ops.h3_phaa_* fused ops)
 from ._native import library_path  # noqa: F401
 
-__all__ = ["ops", "library_path"]
+__all__ = ["ops", "reference_ops", "library_path"]

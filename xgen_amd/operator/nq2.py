@@ -81,7 +81,7 @@ def norm_affine_quant(x, weight, scale, shift, indices, *, eps=1e-5, blocks=40, 
         raise RuntimeError("invalid epsilon/blocks")
     # (not under graph capture: a captured call keeps reading the table it was given, as replays
     # of the raw form would see later writes to it)
-    if not scale_is_one_plus and not torch.cuda.is_current_stream_capturing():
+    if not scale_is_one_plus and scale.is_cuda and not torch.cuda.is_current_stream_capturing():
         prepared = _registered_one_plus(scale)
         if prepared is not None:
             scale, scale_is_one_plus = prepared, True
