@@ -62,7 +62,8 @@ def parse():
 
 PROFILE_KERNELS = ("gemm_fp8_qkv", "gemm_fp8_qkv_exact", "gemm_int8_qkv", "gemm_fp8_ffn_up_gelu", "gemm_fp8_ffn_up",
                    "gemm_fp8_ffn_down",
-                   "quant_rows_fp8", "requant_fp8_12288", "requant_gelu_fp8_12288", "front_end_ln_mod_quant_fp8", "gate_residual_op", "swiglu_quant_int8_h3",
+                   "quant_rows_fp8", "requant_fp8_12288", "requant_gelu_fp8_12288", "front_end_ln_mod_quant_fp8", "gate_residual_op", "indexed_modulate_op",
+                   "swiglu_quant_int8_h3",
                    "wire_encode_h3", "wire_decode_h3", "wire_async_gather_decode_h3", "wire_async_return_pack_h3",
                    "wire_async_return_layout_decode_h3", "copy_1gib")
 
@@ -178,6 +179,11 @@ def profile_kernels(names, steps, warmup):
             gt = (torch.randn((20, K), generator=g, device=dev) * 0.1).to(torch.bfloat16)
             gi = torch.randint(20, (M,), generator=g, device=dev)
             fn = lambda: xops.gate_residual(res, yb, gt, gi)  # noqa: E731
+        elif name == "indexed_modulate_op":
+            shift, scale = W.adaln_tables(20, K, g, dev)
+            xn = torch.randn((1, M, K), generator=g, device=dev).to(torch.bfloat16)
+            gi = torch.randint(20, (M,), generator=g, device=dev)
+            fn = lambda: xops.indexed_modulate(xn, scale, shift, gi)  # noqa: E731
         elif name == "swiglu_quant_int8_h3":
             u3 = torch.randn((1, M, 2 * 14336), generator=g, device=dev).to(torch.bfloat16)
             fn = lambda: xops.swiglu_quant(u3, False, torch.int8, 1, False)  # noqa: E731
@@ -551,7 +557,14 @@ def main():
         kernels["out_proj_gate_residual_fused"] = {
             "ms": ms_fused, "tflops": f_out / (ms_fused * 1e-3) / 1e12,
             "unfused_ms": ms_plain + ms_gate, "gemm_alone_ms": ms_plain}
-        del wo, qo, res, yb
+        # the output AdaLN's indexed modulation of normalised rows (reads x, writes out; the
+        # 20-row tables stay in cache)
+        shift_t, scale_t = W.adaln_tables(20, K, g, dev)
+        mod_bytes = 2 * M * K * 2
+        ms_mod = timed(lambda: xops.indexed_modulate(yb, scale_t, shift_t, gi), args.steps, args.warmup)
+        kernels["indexed_modulate_op"] = {"ms": ms_mod, "gbs": mod_bytes / (ms_mod * 1e-3) / 1e9,
+                                          "frac_of_hbm": mod_bytes / (ms_mod * 1e-3) / 1e9 / PEAK_HBM_GBS}
+        del wo, qo, res, yb, shift_t, scale_t
 
     # ---- H3 FFN activation: SwiGLU + per-token INT8 / FP8 requant at F = 14,336 (u is 896 MB)
     if want("swiglu"):

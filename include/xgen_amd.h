@@ -228,7 +228,7 @@ int xgen_quant_matmul_int8(const void *a, int64_t lda, const void *w, int64_t ld
  * Gated residual with an indexed gate table
  * (torch.ops.h3_phaa_gate_residual.gate_residual,
  *  x_base/x_base/operator/npu_fusion/f2a/op_extension/gate_residual_queued.asc:33-35, kernel
- *  f2a/op_kernel/gate_residual_kernel.asc:57-67; eager form x_base/x_base/operator/h3_indexed_affine.py:47):
+ *  f2a/op_kernel/gate_residual_kernel.asc:57-67; eager form x_base/x_base/operator/h3_indexed_affine.py:49):
  *   out[b,s,c] = bf16(residual[b,s,c] + bf16(branch[b,s,c] * gate_table[indices[s], c]))
  * multiply, round, add, round (no fused multiply-add).  residual / branch: BF16
  * [batch, seq, width] with the given batch / seq strides (elements, last stride
@@ -241,6 +241,26 @@ int xgen_gate_residual(const void *residual, int64_t res_stride_batch, int64_t r
                        const void *gate_table, int64_t gate_row_stride, int64_t gate_rows,
                        const int64_t *indices, int64_t batch, int64_t seq, int64_t width, void *out,
                        hipStream_t stream);
+
+/*
+ * Indexed AdaLN modulation of normalised rows: the modulation half of the
+ * reference's indexed affine (x_base/x_base/operator/h3_indexed_affine.py:9-29 and
+ * :32-48, `_apply(x, scale, shift, indices, modulation=True)`, and the eager bf16
+ * expression of its fallback, :46-48; the output AdaLN of
+ * x_diffusers/x_diffusers/framework/transformer/minimax_h3.py:690-694):
+ *   out[b,s,c] = bf16(bf16(x[b,s,c] * f) + shift_table[g, c]),  g = indices[s],
+ *   f = bf16(1 + scale_table[g, c]), or scale_table[g, c] itself when
+ *   scale_is_one_plus (a table prepared by xgen_adaln_one_plus).
+ * x: BF16 [batch, seq, width] with the given batch / seq strides (elements, last
+ * stride 1); tables BF16 [table_rows, width], rows scale_row_stride /
+ * shift_row_stride apart; indices int64 [seq]; out BF16 [batch, seq, width]
+ * contiguous.  An index outside [0, table_rows) writes a NaN row.  width and
+ * strides multiples of 8 elements, buffers 16-byte aligned.
+ */
+int xgen_indexed_modulate(const void *x, int64_t x_stride_batch, int64_t x_stride_seq, const void *scale_table,
+                          int64_t scale_row_stride, const void *shift_table, int64_t shift_row_stride,
+                          int64_t table_rows, const int64_t *indices, int64_t batch, int64_t seq, int64_t width,
+                          int scale_is_one_plus, void *out, hipStream_t stream);
 
 /*
  * W8A8 GEMM whose bf16 output feeds the gated residual in the same epilogue:

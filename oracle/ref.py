@@ -29,7 +29,7 @@ Function -> reference -> how it is pinned (tests/test_oracle_*.py):
   gelu_tanh           diffusers FeedForward('gelu-approximate') = F.gelu(tanh)
         (hunyuan.py:358) — parity unpinned against diffusers itself (absent);
         checked against the closed formula in float64 within 1 bf16 ulp.
-  gate_residual       gate_residual_kernel.asc:57-67 / h3_indexed_affine.py:47
+  gate_residual       gate_residual_kernel.asc:57-67 / h3_indexed_affine.py:49
         torch bf16 expression == numpy restatement with explicit RNE after each op.
   swiglu_quant        swiglu_quant_reuse_kernel.asc:36-105, h3_swiglu.py:15-29
         silu against the float64 formula; quantizer halves as quantize_rows_*.
@@ -243,7 +243,7 @@ def gate_residual(residual, branch, gate_table, indices):
     """Gated residual out = bf16(residual + bf16(branch * gate[g])) with g = indices[r % S] for row
     r = b*S + s (npu_fusion/f2a/op_kernel/gate_residual_kernel.asc:57-67: multiply, round, add, round,
     no FMA; the eager form `residual + gate.index_select(0, indices) * x` of
-    x_base/x_base/operator/h3_indexed_affine.py:47 and tests/test_h3_indexed_affine.py:21-22).
+    x_base/x_base/operator/h3_indexed_affine.py:49 and tests/test_h3_indexed_affine.py:21-22).
     [B, S, H] bf16 in and out."""
     r = residual.detach().cpu()
     b = branch.detach().cpu()

@@ -165,6 +165,35 @@ def test_gate_residual_meta():
         xops.gate_residual(r, r, g, i.to(torch.int32))
 
 
+def test_indexed_modulate_meta():
+    m = torch.device("meta")
+    x = torch.empty(2, 5, 64, dtype=torch.bfloat16, device=m)
+    tables = torch.empty(3, 6 * 64, dtype=torch.bfloat16, device=m)
+    shift, scale = tables.chunk(6, dim=-1)[:2]
+    i = torch.empty(5, dtype=torch.int64, device=m)
+    out = xops.indexed_modulate(x, scale, shift, i)
+    assert out.shape == (2, 5, 64) and out.dtype == torch.bfloat16
+    assert xops.indexed_modulate(x, scale, shift, i, True).shape == (2, 5, 64)
+    with pytest.raises(RuntimeError):
+        xops.indexed_modulate(x, scale[:, :32], shift[:, :32], i)
+    with pytest.raises(RuntimeError):
+        xops.indexed_modulate(x, scale, shift[:2], i)
+    with pytest.raises(RuntimeError):
+        xops.indexed_modulate(x, scale, shift, i[:4])
+    with pytest.raises(RuntimeError):
+        xops.indexed_modulate(x.float(), scale, shift, i)
+
+
+def test_indexed_affine_has_no_host_path():
+    from xgen_amd.operator.h3_indexed_affine import _apply
+    x = torch.zeros(1, 3, 16, dtype=torch.bfloat16)
+    t = torch.zeros(2, 16, dtype=torch.bfloat16)
+    for modulation in (True, False):
+        with pytest.raises(RuntimeError, match="HIP"):
+            _apply(x, t, t if modulation else x, torch.zeros(3, dtype=torch.int64), modulation=modulation)
+    assert not torch.cuda.is_initialized()
+
+
 def test_scaled_mm_gate_residual_meta():
     m = torch.device("meta")
     a = torch.empty(10, 64, dtype=torch.float8_e4m3fn, device=m)

@@ -49,6 +49,10 @@ IMPORTED = {
         "gate_residual": "h3_npu_fusion.py:66 (through Kernels.get)",
         "library_path": "npu_fusion/runtime.py:125 (Kernels.get)",
     },
+    "xgen_amd.operator.h3_indexed_affine": {
+        "_apply": "x_base/x_base/operator/h3_indexed_affine.py:32, minimax_h3.py:692",
+        "fused_h3_block_forward": "x_diffusers/x_diffusers/adaptor/h3_cuda.py:36",
+    },
     "xgen_amd.phaa.fp8_transport": {
         "fp8_all_to_all": "x_base/x_base/phaa/phaa_attention.py:133",
         "fp8_all_to_all_many": "x_base/x_base/phaa/phaa_attention.py:133",

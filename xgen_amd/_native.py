@@ -82,6 +82,9 @@ SIGNATURES = {
         _c_ptr]),
     "xgen_fp8_wire_decode": (_c_int, [
         _c_int, _c_int, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr]),
+    "xgen_indexed_modulate": (_c_int, [
+        _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int,
+        _c_ptr, _c_ptr]),
     "xgen_fp8_wire_encode_masked": (_c_int, [
         _c_int, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr,
         _c_ptr]),

@@ -29,6 +29,9 @@ SCHEMAS = {
         "scaled_mm(Tensor a, Tensor w, Tensor a_scale, Tensor w_scale, Tensor? bias, "
         "ScalarType out_dtype, int activation, bool return_acc, bool exact=False) -> (Tensor, Tensor)"),
     "gate_residual": "gate_residual(Tensor residual, Tensor branch, Tensor gate_table, Tensor indices) -> Tensor",
+    "indexed_modulate": (
+        "indexed_modulate(Tensor x, Tensor scale_table, Tensor shift_table, Tensor indices, "
+        "bool scale_is_one_plus=False) -> Tensor"),
     "swiglu_quant": (
         "swiglu_quant(Tensor u, bool gate_first, ScalarType out_dtype, int scale_mode, bool return_act) "
         "-> (Tensor, Tensor, Tensor)"),
@@ -158,6 +161,17 @@ def _gate_check(residual, branch, gate_table, indices, what="gate_residual"):
 def _gate_meta(residual, branch, gate_table, indices):
     _gate_check(residual, branch, gate_table, indices)
     return torch.empty(residual.shape, dtype=torch.bfloat16, device=residual.device)
+
+
+def _modulate_meta(x, scale_table, shift_table, indices, scale_is_one_plus=False):
+    what = "indexed_modulate"
+    _require(x.dim() == 3 and x.shape[2] > 0, f"{what}: x [B,S,H] required")
+    _require(scale_table.dim() == 2 and scale_table.shape[0] > 0 and scale_table.shape[1] == x.shape[2]
+             and shift_table.shape == scale_table.shape, f"{what}: scale/shift tables [T,H] required")
+    _require(indices.dim() == 1 and indices.shape[0] == x.shape[1] and indices.dtype == torch.int64,
+             f"{what}: int64 indices [S] required")
+    _require(x.dtype == scale_table.dtype == shift_table.dtype == torch.bfloat16, f"{what}: BF16 inputs required")
+    return torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
 
 
 SWIGLU_MAX_HALF = 16384
@@ -308,6 +322,22 @@ def _gate_gpu(residual, branch, gate_table, indices):
     return out
 
 
+def _modulate_gpu(x, scale_table, shift_table, indices, scale_is_one_plus=False):
+    _on_gpu(x, scale_table, shift_table, indices)
+    out = _modulate_meta(x, scale_table, shift_table, indices, scale_is_one_plus)
+    if out.numel() == 0:
+        return out
+    x, scale_table, shift_table = _kernel_rows(x, 8), _kernel_rows(scale_table, 8), _kernel_rows(shift_table, 8)
+    indices = indices.contiguous()
+    B, S, H = x.shape
+    st = N.lib().xgen_indexed_modulate(
+        x.data_ptr(), x.stride(0), x.stride(1), scale_table.data_ptr(), scale_table.stride(0),
+        shift_table.data_ptr(), shift_table.stride(0), scale_table.shape[0], indices.data_ptr(), B, S, H,
+        int(bool(scale_is_one_plus)), out.data_ptr(), N.stream_of(x))
+    N.check(st, "xgen_indexed_modulate")
+    return out
+
+
 _SILU_TABLES: dict[int, torch.Tensor] = {}
 
 
@@ -371,6 +401,7 @@ _IMPLS = {
     "norm_affine_quant": (_norm_gpu, _norm_meta),
     "scaled_mm": (_mm_gpu, _mm_meta),
     "gate_residual": (_gate_gpu, _gate_meta),
+    "indexed_modulate": (_modulate_gpu, _modulate_meta),
     "swiglu_quant": (_swiglu_gpu, _swiglu_meta),
     "scaled_mm_gate_residual": (_mm_gate_gpu, _mm_gate_meta),
 }
