@@ -163,3 +163,34 @@ def test_block_forward_matches_eager_block(cuda):
     with torch.enable_grad():                                  # autograd: the block's own forward
         assert torch.equal(block_forward(block, hidden, temb, indices, None).detach().view(torch.int16),
                            expected.view(torch.int16))
+
+
+def test_output_adaln_allocates_only_its_output(cuda):
+    """The reference's memory check (x_base/tests/test_h3_output_adaln.py:50-66): at a full H3
+    sequence (1, 32,768, 5,376) the fused output AdaLN needs less than half the eager expression's
+    extra memory (the eager one expands both tables to the full sequence and keeps intermediates);
+    here the only allocation is the output itself."""
+    torch.manual_seed(42)
+    width, seq = 5376, 32768
+    x = torch.randn(1, seq, width, device=cuda, dtype=torch.bfloat16)
+    modulation = torch.randn(3, width * 2, device=cuda, dtype=torch.bfloat16)
+    shift, scale = modulation.chunk(2, dim=-1)
+    indices = torch.arange(seq, device=cuda) % 3
+    with torch.no_grad():
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+        base = torch.cuda.memory_allocated()
+        expected = x * (1.0 + scale.index_select(0, indices)) + shift.index_select(0, indices)
+        torch.cuda.synchronize()
+        eager_peak = torch.cuda.max_memory_allocated() - base
+        reference = expected.cpu()
+        del expected
+        torch.cuda.empty_cache()
+        torch.cuda.reset_peak_memory_stats()
+        base = torch.cuda.memory_allocated()
+        actual = output_adaln(x, scale, shift, indices)
+        torch.cuda.synchronize()
+        fused_peak = torch.cuda.max_memory_allocated() - base
+    assert torch.equal(actual.cpu().view(torch.int16), reference.view(torch.int16))
+    assert fused_peak < eager_peak / 2, (eager_peak, fused_peak)
+    assert fused_peak <= x.numel() * 2 + (1 << 21), fused_peak
