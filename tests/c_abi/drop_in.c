@@ -182,6 +182,29 @@ int main(void) {
   EXPECT(bad_acc == 0, "int8 accumulators: %d differ from the integer sums", bad_acc);
   EXPECT(bad_out == 0, "int8 outputs: %d off the epilogue of the accumulators", bad_out);
 
+  /* ---- indexed AdaLN modulation of the activations as [1, M, K] rows: bf16 after every step */
+  enum { T = 3 };
+  static uint16_t table[T * 2 * K], mod[M * K];
+  static int64_t idx[M];
+  for (int i = 0; i < T * 2 * K; ++i) table[i] = bf16_bits(bell() * 0.1f);
+  for (int m = 0; m < M; ++m) idx[m] = (m * 7) % T;
+  void *dtable = device_copy(table, sizeof table), *didx = device_copy(idx, sizeof idx);
+  void *dmod = device_copy(NULL, sizeof mod);
+  /* scale and shift are the two halves of each [2K] table row: row stride 2K */
+  XGEN_OK_CALL(xgen_indexed_modulate(dx, (int64_t)M * K, K, (uint16_t *)dtable + K, 2 * K, dtable, 2 * K, T,
+                                     didx, 1, M, K, 0, dmod, stream));
+  HIP_OK(hipStreamSynchronize(stream));
+  host_copy(mod, dmod, sizeof mod);
+  int bad_mod = 0;
+  for (int m = 0; m < M; ++m)
+    for (int k = 0; k < K; ++k) {
+      const uint16_t *row = table + idx[m] * 2 * K;
+      const float f = bf16_value(bf16_bits(1.0f + bf16_value(row[K + k])));
+      const float p = bf16_value(bf16_bits(bf16_value(x[m * K + k]) * f));
+      bad_mod += mod[m * K + k] != bf16_bits(p + bf16_value(row[k]));
+    }
+  EXPECT(bad_mod == 0, "indexed modulation: %d values differ from the eager bf16 steps", bad_mod);
+
   /* ---- the error contract: checked before any launch, message per thread */
   EXPECT(xgen_quantize_rows(XGEN_DTYPE_BF16, dx, M, K, K, 42, dqx, K, dsx, stream) == XGEN_ERR_INVALID_ARGUMENT,
          "an unknown output dtype is rejected");
@@ -190,13 +213,14 @@ int main(void) {
                             XGEN_DTYPE_BF16, N, NULL, stream) == XGEN_ERR_INVALID_ARGUMENT,
          "a null output is rejected");
 
-  void *bufs[] = {dx, dw, db, dqx, dqw, dsx, dsw, dacc, dout, dix, diw, diacc};
+  void *bufs[] = {dx, dw, db, dqx, dqw, dsx, dsw, dacc, dout, dix, diw, diacc, dtable, didx, dmod};
   for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; ++i) HIP_OK(hipFree(bufs[i]));
   HIP_OK(hipStreamDestroy(stream));
   if (failures) {
     printf("%d check(s) failed\n", failures);
     return 1;
   }
-  printf("c abi ok: fp8 and int8 quantizers bit-exact, accumulators within bounds, M=%d N=%d K=%d\n", M, N, K);
+  printf("c abi ok: fp8 and int8 quantizers and the modulation bit-exact, accumulators within bounds, "
+         "M=%d N=%d K=%d\n", M, N, K);
   return 0;
 }
