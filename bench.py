@@ -63,7 +63,7 @@ def parse():
 PROFILE_KERNELS = ("gemm_fp8_qkv", "gemm_fp8_qkv_exact", "gemm_int8_qkv", "gemm_fp8_ffn_up_gelu", "gemm_fp8_ffn_up",
                    "gemm_fp8_ffn_down",
                    "quant_rows_fp8", "requant_fp8_12288", "requant_gelu_fp8_12288", "front_end_ln_mod_quant_fp8", "gate_residual_op", "indexed_modulate_op",
-                   "swiglu_quant_int8_h3",
+                   "swiglu_quant_int8_h3", "merge_quant_int8_h3",
                    "wire_encode_h3", "wire_decode_h3", "wire_async_gather_decode_h3", "wire_async_return_pack_h3",
                    "wire_async_return_layout_decode_h3", "copy_1gib")
 
@@ -184,6 +184,9 @@ def profile_kernels(names, steps, warmup):
             xn = torch.randn((1, M, K), generator=g, device=dev).to(torch.bfloat16)
             gi = torch.randint(20, (M,), generator=g, device=dev)
             fn = lambda: xops.indexed_modulate(xn, scale, shift, gi)  # noqa: E731
+        elif name == "merge_quant_int8_h3":
+            xr = torch.randn((7, 4, M, 1, 256), generator=g, device=dev).to(torch.bfloat16)
+            fn = lambda: xops.merge_quant(xr, torch.int8)  # noqa: E731
         elif name == "swiglu_quant_int8_h3":
             u3 = torch.randn((1, M, 2 * 14336), generator=g, device=dev).to(torch.bfloat16)
             fn = lambda: xops.swiglu_quant(u3, False, torch.int8, 1, False)  # noqa: E731
@@ -576,6 +579,17 @@ def main():
             kernels[name] = {"ms": ms_sw, "gbs": sw_bytes / (ms_sw * 1e-3) / 1e9,
                              "frac_of_hbm": sw_bytes / (ms_sw * 1e-3) / 1e9 / PEAK_HBM_GBS, "bytes": sw_bytes}
         del u3
+
+    # ---- merge + INT8 quant of the head-parallel attention's returned chunks (H3: 56 heads x 128 as
+    # [7 chunks, 4 owners, S, 1, 256]), the out-projection's input, at S = M tokens
+    if want("merge"):
+        xr = torch.randn((7, 4, M, 1, 256), generator=g, device=dev).to(torch.bfloat16)
+        mq_bytes = M * 7168 * 2 + M * 7168 + 4 * M
+        ms_mq = timed(lambda: xops.merge_quant(xr, torch.int8), args.steps, args.warmup)
+        kernels["merge_quant_int8_h3"] = {"ms": ms_mq, "gbs": mq_bytes / (ms_mq * 1e-3) / 1e9,
+                                          "frac_of_hbm": mq_bytes / (ms_mq * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                                          "bytes": mq_bytes}
+        del xr
 
     # ---- H3's FFN on the same kernels (d = 5,376, F = 14,336): FP8 up -> SwiGLU + FP8 requant -> FP8 down
     if want("h3_ffn"):

@@ -243,6 +243,24 @@ int xgen_gate_residual(const void *residual, int64_t res_stride_batch, int64_t r
                        hipStream_t stream);
 
 /*
+ * Merge of the head-parallel attention's returned chunks + per-row quantization
+ * of the out-projection's input: torch.ops.h3_phaa_merge_quant.fused
+ * (x_base/x_base/operator/npu_fusion/f4_merge_quant/op_extension/merge_quant_queued.asc:9-28,
+ * kernel op_kernel/merge_quant_kernel.asc:20-87; wrapper npu_fusion/merge_quant.py:9-14;
+ * caller x_base/x_base/phaa/fused_layout.py:44-48).
+ * back_recv: BF16 [splits, owners, seq, batch, chunk], contiguous, 16-byte aligned.
+ * Row b * seq + s of the output holds back_recv[c, o, s, b, :] at columns
+ * (o * splits + c) * chunk: q [batch * seq, splits * owners * chunk] (contiguous,
+ * 8-byte aligned) of out_dtype (XGEN_DTYPE_I8: scale mode 1 of the INT8 row
+ * quantizer, as the reference's kernel; XGEN_DTYPE_E4M3: the FP8 row quantizer),
+ * scale f32 [batch * seq].  The reference's geometry is splits 7, owners 4,
+ * batch 1, chunk 256 (H3's 56 heads x 128).  chunk a multiple of 8,
+ * splits * owners * chunk <= 16384, batch * seq < 2^31.
+ */
+int xgen_merge_quant(int out_dtype, const void *back_recv, int64_t splits, int64_t owners, int64_t seq,
+                     int64_t batch, int64_t chunk, void *q, float *scale, hipStream_t stream);
+
+/*
  * Indexed AdaLN modulation of normalised rows: the modulation half of the
  * reference's indexed affine (x_base/x_base/operator/h3_indexed_affine.py:9-29 and
  * :32-48, `_apply(x, scale, shift, indices, modulation=True)`, and the eager bf16

@@ -43,6 +43,10 @@ Function -> reference -> how it is pinned (tests/test_oracle_*.py):
         floor; decode of all 256 codes == the e4m3 table; round-trip error bound;
         the kernels' division exhaustively at the floor (bf16).  Non-finite rows:
         parity unpinned (the reference leaves NaN to its min/max lowering).
+  merge_quant         f4_merge_quant/op_kernel/merge_quant_kernel.asc:20-87 (merge_rows + the
+        row quantizers).  merge_rows == a loop over the reference kernel's copy
+        (DataCopyPad of 7 stripes of 256 at source stride 4*seq*256, destination
+        owner*1792, :25-29) on small cases; the quantizer halves as quantize_rows_*.
   fp8 async layouts   phaa/fp8_async_transport.py:13-80,126-193 (fp8_async_encode / _decode)
         plain layout == the synchronous wire without padding; the fused return
         pack == the synchronous wire of the output zero-padded and permuted by torch
@@ -256,6 +260,24 @@ def gate_residual_np(residual: np.ndarray, branch: np.ndarray, gate_rows: np.nda
     bf16 values in, float32 array of bf16 values out); gate_rows already indexed [.., S, H]."""
     prod = round_bf16_np(branch.astype(np.float32) * gate_rows.astype(np.float32))
     return round_bf16_np(residual.astype(np.float32) + prod)
+
+
+def merge_rows(back_recv: torch.Tensor) -> torch.Tensor:
+    """The out-projection's input rows from the head-parallel attention's returned chunks
+    (merge_quant_kernel.asc:23-29: each owner's chunk stripes are contiguous in the output row):
+    back_recv [splits, owners, seq, batch, chunk] -> [batch * seq, owners * splits * chunk], row
+    b * seq + s, columns (o * splits + c) * chunk + j  <-  back_recv[c, o, s, b, j]."""
+    x = back_recv.detach().cpu()
+    splits, owners, seq, batch, chunk = x.shape
+    return x.permute(3, 2, 1, 0, 4).reshape(batch * seq, owners * splits * chunk)
+
+
+def merge_quant(back_recv: torch.Tensor, out: str = "int8"):
+    """torch.ops.h3_phaa_merge_quant.fused (merge_quant_kernel.asc:20-87): merge_rows, then the
+    per-row INT8 quantizer with scale mode 1 (:55-81) — or, for the FP8 path, the FP8 row quantizer.
+    Returns (q [rows, width], scale f32 [rows])."""
+    rows = merge_rows(back_recv)
+    return quantize_rows_int8(rows) if out == "int8" else quantize_rows_fp8(rows)
 
 
 def swiglu_quant(u, gate_first=False, out="int8", scale_mode=1):

@@ -106,6 +106,18 @@ _STRIDES = (N._c_i64 * 12)(384, 128, 128, 128, 384, 128, 128, 128, 384, 128, 128
                                               16, None, None, None), N.ERR_INVALID_ARGUMENT, b"output dtype"),
     (lambda L: L.xgen_fp8_wire_decode_strided(N.DTYPE_BF16, 1, 16, 2, 1 << 31, 1, 1, 64, (N._c_i64 * 4)(0, 64, 0, 0),
                                               6, 16, None, None, None), N.ERR_UNSUPPORTED, b"peer rows"),
+    (lambda L: L.xgen_merge_quant(N.DTYPE_BF16, 16, 7, 4, 17, 1, 256, 16, 16, None), N.ERR_INVALID_ARGUMENT,
+     b"output dtype"),
+    (lambda L: L.xgen_merge_quant(N.DTYPE_I8, 16, 0, 4, 17, 1, 256, 16, 16, None), N.ERR_INVALID_ARGUMENT,
+     b"bad geometry"),
+    (lambda L: L.xgen_merge_quant(N.DTYPE_I8, 16, 7, 4, 17, 1, 252, 16, 16, None), N.ERR_UNSUPPORTED,
+     b"multiple of 8"),
+    (lambda L: L.xgen_merge_quant(N.DTYPE_I8, 16, 9, 8, 17, 1, 256, 16, 16, None), N.ERR_UNSUPPORTED, b"16384"),
+    (lambda L: L.xgen_merge_quant(N.DTYPE_I8, 16, 7, 4, 1 << 20, 1 << 12, 256, 16, 16, None), N.ERR_UNSUPPORTED,
+     b"2^31"),
+    (lambda L: L.xgen_merge_quant(N.DTYPE_I8, None, 7, 4, 17, 1, 256, 16, 16, None), N.ERR_INVALID_ARGUMENT,
+     b"null"),
+    (lambda L: L.xgen_merge_quant(N.DTYPE_I8, 16, 7, 4, 17, 1, 256, 12, 16, None), N.ERR_UNSUPPORTED, b"aligned"),
     (lambda L: L.xgen_indexed_modulate(16, 0, 64, 16, 64, 16, 64, 0, 16, 1, 4, 64, 0, 16, None),
      N.ERR_INVALID_ARGUMENT, b"bad shape"),
     (lambda L: L.xgen_indexed_modulate(16, 0, 32, 16, 64, 16, 64, 3, 16, 1, 4, 64, 0, 16, None),
@@ -135,6 +147,7 @@ def test_empty_inputs_are_no_ops(built_library):
     assert L.xgen_fp8_wire_decode_strided(N.DTYPE_BF16, 3, None, 2, 5, 0, 3, 128, (N._c_i64 * 4)(0, 0, 0, 0), 0,
                                           None, None, None, None) == N.OK
     assert L.xgen_indexed_modulate(None, 0, 64, None, 64, None, 64, 3, None, 2, 0, 64, 0, None, None) == N.OK
+    assert L.xgen_merge_quant(N.DTYPE_I8, None, 7, 4, 0, 1, 256, None, None, None) == N.OK
     assert L.xgen_last_error() == b""
 
 

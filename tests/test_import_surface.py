@@ -49,6 +49,13 @@ IMPORTED = {
         "gate_residual": "h3_npu_fusion.py:66 (through Kernels.get)",
         "library_path": "npu_fusion/runtime.py:125 (Kernels.get)",
     },
+    "xgen_amd.operator.merge_quant": {
+        "merge_quant": "x_base/x_base/phaa/fused_layout.py:47 (through Kernels.get), test_npu_fusion_meta.py:60",
+        "library_path": "npu_fusion/runtime.py:125 (Kernels.get)",
+    },
+    "xgen_amd.operator.quantized": {
+        "QuantizedRows": "x_base/x_base/phaa/fused_layout.py:5, h3_npu_fusion.py:17",
+    },
     "xgen_amd.operator.h3_indexed_affine": {
         "_apply": "x_base/x_base/operator/h3_indexed_affine.py:32, minimax_h3.py:692",
         "fused_h3_block_forward": "x_diffusers/x_diffusers/adaptor/h3_cuda.py:36",

@@ -101,3 +101,62 @@ def test_symmetries(dtype):
     perm = torch.randperm(200, generator=torch.Generator().manual_seed(6))
     qp, sp = R.quantize_rows_int8(x[:, perm])
     assert torch.equal(qp, q[:, perm]) and torch.equal(sp, s)
+
+
+# ------------------------------------------------------------------ merge + quant
+def _reference_copy(back_recv):
+    """The reference kernel's copy, restated from its DataCopyPad parameters
+    (merge_quant_kernel.asc:25-29): for each row and owner, 7 blocks of 512 bytes read from
+    element (owner * seq + row) * 256 at a source stride of (4 * seq - 1) * 512 bytes between
+    blocks, written contiguously from element owner * 1792 of the row."""
+    flat = back_recv.reshape(-1)
+    seq = back_recv.shape[2]
+    rows = torch.empty((seq, 7168), dtype=back_recv.dtype)
+    for row in range(seq):
+        for owner in range(4):
+            src = (owner * seq + row) * 256
+            for block in range(7):
+                rows[row, owner * 1792 + block * 256: owner * 1792 + (block + 1) * 256] = \
+                    flat[src + block * 4 * seq * 256: src + block * 4 * seq * 256 + 256]
+    return rows
+
+
+@pytest.mark.parametrize("seq", [1, 3, 17])
+def test_merge_rows_is_the_reference_copy(seq):
+    g = torch.Generator().manual_seed(seq)
+    x = torch.randn((7, 4, seq, 1, 256), generator=g).to(torch.bfloat16)
+    assert torch.equal(R.merge_rows(x), _reference_copy(x))
+    # plausible mistakes fail it: chunk-major columns, or the owner and chunk axes read swapped
+    wrong_order = x.permute(3, 2, 0, 1, 4).reshape(seq, 7168)
+    wrong_axes = x.reshape(4, 7, seq, 1, 256).permute(3, 2, 0, 1, 4).reshape(seq, 7168)
+    assert not torch.equal(wrong_order, _reference_copy(x))
+    assert not torch.equal(wrong_axes, _reference_copy(x))
+
+
+def test_merge_rows_general_geometry():
+    """Row b * seq + s, column (o * splits + c) * chunk + j holds back_recv[c, o, s, b, j]
+    (element by element, on a batch of 2)."""
+    splits, owners, seq, batch, chunk = 3, 2, 4, 2, 8
+    x = torch.arange(splits * owners * seq * batch * chunk, dtype=torch.float32).reshape(
+        splits, owners, seq, batch, chunk)
+    rows = R.merge_rows(x)
+    assert rows.shape == (batch * seq, owners * splits * chunk)
+    for c in range(splits):
+        for o in range(owners):
+            for s in range(seq):
+                for b in range(batch):
+                    col = (o * splits + c) * chunk
+                    assert torch.equal(rows[b * seq + s, col: col + chunk], x[c, o, s, b])
+
+
+def test_merge_quant_is_the_row_quantizer_of_the_merged_rows():
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn((7, 4, 9, 1, 256), generator=g).to(torch.bfloat16)
+    x[:, :, 2] = 0  # a zero row: zero bytes and scale
+    q, s = R.merge_quant(x)
+    rq, rs = R.quantize_rows_int8(_reference_copy(x))
+    assert torch.equal(q, rq) and torch.equal(s, rs)
+    assert s[2] == 0 and not q[2].any()
+    q8, s8 = R.merge_quant(x, out="fp8")
+    f8, fs = R.quantize_rows_fp8(_reference_copy(x))
+    assert torch.equal(q8.view(torch.uint8), f8.view(torch.uint8)) and torch.equal(s8, fs)

@@ -1,12 +1,12 @@
 """The reference's fused operators under their own torch.ops names (xgen_amd.reference_ops): the
 schemas of their TORCH_LIBRARY definitions, and the reference's Meta contract suite
-(x_base/tests/test_npu_fusion_meta.py:33-48, 67-73) run against both the op handles and this
+(x_base/tests/test_npu_fusion_meta.py:33-48, 60-61, 67-73) run against both the op handles and this
 package's wrapper modules, with no device initialized."""
 import pytest
 import torch
 
 import xgen_amd  # noqa: F401  (registers torch.ops.h3_phaa_*)
-from xgen_amd.operator import gate_residual, nq2, swiglu_quant
+from xgen_amd.operator import gate_residual, merge_quant, nq2, swiglu_quant
 
 M = torch.device("meta")
 
@@ -28,9 +28,12 @@ def tensor(*shape, dtype=torch.bfloat16):
      "Tensor u, int tile=2048, int blocks=40, int scale_mode=1) -> (Tensor, Tensor)"),
     (lambda: torch.ops.h3_phaa_fusion_quant_reuse.swiglu_quantize, "h3_phaa_fusion_quant_reuse::swiglu_quantize("
      "Tensor u, int tile=4096, int blocks=40, int scale_mode=1) -> (Tensor, Tensor)"),
+    (lambda: torch.ops.h3_phaa_merge_quant.fused,
+     "h3_phaa_merge_quant::fused(Tensor back_recv, int blocks=40) -> (Tensor, Tensor)"),
 ])
 def test_schemas_are_the_references(op, schema):
-    """nq2_queued.asc:47-51, gate_residual_queued.asc:31, swiglu_quant*_queued.asc:33."""
+    """nq2_queued.asc:47-51, gate_residual_queued.asc:31, swiglu_quant*_queued.asc:33,
+    merge_quant_queued.asc:26."""
     assert str(op()._schemas[""]) == schema
 
 
@@ -63,6 +66,36 @@ def test_gate_and_norm_contracts():
         torch.ops.h3_phaa_nq2.fused(value, tensor(64), table, table, tensor(16, dtype=torch.int64))
     with pytest.raises(RuntimeError, match="gate_table"):
         torch.ops.h3_phaa_gate_residual.gate_residual(value, value, tensor(3, 32), indices)
+
+
+def test_merge_contract():
+    """test_npu_fusion_meta.py:60-61: [7, 4, 17, 1, 256] -> int8 [17, 7168] + f32 [17]; and the op's
+    checks (merge_quant_queued.asc:10-13)."""
+    for merge in (merge_quant.merge_quant, torch.ops.h3_phaa_merge_quant.fused):
+        quantized, scale = merge(tensor(7, 4, 17, 1, 256))
+        assert quantized.shape == (17, 7168) and scale.shape == (17,)
+        assert quantized.dtype == torch.int8 and scale.dtype == torch.float32
+    op = torch.ops.h3_phaa_merge_quant.fused
+    with pytest.raises(RuntimeError, match=r"\[7,4,S,1,256\] required"):
+        op(tensor(7, 4, 17, 2, 256))
+    with pytest.raises(RuntimeError, match="contiguous BF16 required"):
+        op(tensor(7, 4, 17, 1, 256, dtype=torch.float16))
+    with pytest.raises(RuntimeError, match="contiguous BF16 required"):
+        op(tensor(4, 7, 17, 1, 256).transpose(0, 1))
+    with pytest.raises(RuntimeError, match="DataCopy"):
+        op(tensor(7, 4, (1 << 20) + 1, 1, 256))
+    with pytest.raises(RuntimeError, match="blocks"):
+        op(tensor(7, 4, 17, 1, 256), 41)
+    with pytest.raises(ValueError, match="Inference only"):
+        merge_quant.merge_quant(tensor(7, 4, 17, 1, 256).requires_grad_())
+    q8, _ = merge_quant.merge_quant(tensor(7, 4, 17, 1, 256), out_dtype=torch.float8_e4m3fn)
+    assert q8.dtype == torch.float8_e4m3fn
+    q, s = torch.ops.xgen_amd.merge_quant(tensor(3, 2, 5, 2, 64), torch.int8)   # general geometry
+    assert q.shape == (10, 384) and s.shape == (10,)
+    with pytest.raises(RuntimeError, match="multiple of 8"):
+        torch.ops.xgen_amd.merge_quant(tensor(3, 2, 5, 2, 60), torch.int8)
+    with pytest.raises(RuntimeError, match="16384"):
+        torch.ops.xgen_amd.merge_quant(tensor(9, 8, 5, 1, 256), torch.int8)
 
 
 def test_device_remains_uninitialized():

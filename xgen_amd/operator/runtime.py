@@ -19,9 +19,10 @@ the attributes below (h3_npu_fusion.py:196-273), so they keep that contract:
                                    errors after dispatch propagate
 
 Features map onto this package's modules: "norm_quant" -> nq2, "swiglu" ->
-swiglu_quant, "gate_residual" -> gate_residual, all in libxgen_amd.so.  The
-reference's other features (rope, PHAA layout, laser preprocessing, merge
-quantization) are outside the W8A8 linear path and always fall back.
+swiglu_quant, "gate_residual" -> gate_residual, "merge_quant" -> merge_quant,
+all in libxgen_amd.so.  The reference's other features (rope, PHAA layout,
+laser preprocessing) are attention work outside the W8A8 linear path and
+always fall back.
 """
 from __future__ import annotations
 
@@ -205,7 +206,7 @@ class Kernels:
         "rope": None,
         "phaa_layout": None,
         "laser_preprocess": None,
-        "merge_quant": None,
+        "merge_quant": ("merge_quant", None),
     }
 
     def __init__(self, diagnostics):

@@ -32,6 +32,7 @@ SCHEMAS = {
     "indexed_modulate": (
         "indexed_modulate(Tensor x, Tensor scale_table, Tensor shift_table, Tensor indices, "
         "bool scale_is_one_plus=False) -> Tensor"),
+    "merge_quant": "merge_quant(Tensor back_recv, ScalarType out_dtype) -> (Tensor, Tensor)",
     "swiglu_quant": (
         "swiglu_quant(Tensor u, bool gate_first, ScalarType out_dtype, int scale_mode, bool return_act) "
         "-> (Tensor, Tensor, Tensor)"),
@@ -172,6 +173,23 @@ def _modulate_meta(x, scale_table, shift_table, indices, scale_is_one_plus=False
              f"{what}: int64 indices [S] required")
     _require(x.dtype == scale_table.dtype == shift_table.dtype == torch.bfloat16, f"{what}: BF16 inputs required")
     return torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+
+
+MERGE_MAX_WIDTH = 16384
+
+
+def _merge_meta(back_recv, out_dtype):
+    what = "merge_quant"
+    _require(back_recv.dim() == 5 and back_recv.dtype == torch.bfloat16,
+             f"{what}: BF16 back_recv [splits, owners, seq, batch, chunk] required")
+    splits, owners, seq, batch, chunk = back_recv.shape
+    _require(splits > 0 and owners > 0 and chunk > 0 and chunk % 8 == 0,
+             f"{what}: chunk must be a positive multiple of 8")
+    _require(splits * owners * chunk <= MERGE_MAX_WIDTH, f"{what}: splits*owners*chunk must be <= {MERGE_MAX_WIDTH}")
+    _require(seq * batch < 2 ** 31, f"{what}: seq*batch must be below 2^31")
+    _require(out_dtype in (torch.float8_e4m3fn, torch.int8), f"{what}: out_dtype must be float8_e4m3fn or int8")
+    q = torch.empty((batch * seq, splits * owners * chunk), dtype=out_dtype, device=back_recv.device)
+    return q, torch.empty((batch * seq,), dtype=torch.float32, device=back_recv.device)
 
 
 SWIGLU_MAX_HALF = 16384
@@ -338,6 +356,19 @@ def _modulate_gpu(x, scale_table, shift_table, indices, scale_is_one_plus=False)
     return out
 
 
+def _merge_gpu(back_recv, out_dtype):
+    _on_gpu(back_recv)
+    q, scale = _merge_meta(back_recv, out_dtype)
+    if q.numel() == 0:
+        return q, scale
+    back_recv = _aligned_flat(back_recv)
+    splits, owners, seq, batch, chunk = back_recv.shape
+    st = N.lib().xgen_merge_quant(N.dtype_code(out_dtype), back_recv.data_ptr(), splits, owners, seq, batch, chunk,
+                                  q.data_ptr(), scale.data_ptr(), N.stream_of(back_recv))
+    N.check(st, "xgen_merge_quant")
+    return q, scale
+
+
 _SILU_TABLES: dict[int, torch.Tensor] = {}
 
 
@@ -402,6 +433,7 @@ _IMPLS = {
     "scaled_mm": (_mm_gpu, _mm_meta),
     "gate_residual": (_gate_gpu, _gate_meta),
     "indexed_modulate": (_modulate_gpu, _modulate_meta),
+    "merge_quant": (_merge_gpu, _merge_meta),
     "swiglu_quant": (_swiglu_gpu, _swiglu_meta),
     "scaled_mm_gate_residual": (_mm_gate_gpu, _mm_gate_meta),
 }

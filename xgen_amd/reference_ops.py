@@ -12,6 +12,9 @@ libraries define (TORCH_LIBRARY + device + Meta registrations):
   h3_phaa_fusion_quant[_vector|_reuse]::swiglu_quantize
       (u, tile, blocks=40, scale_mode=1) -> (q int8, scale)
       npu_fusion/f1b/op_extension/swiglu_quant{,_vector,_reuse}_queued.asc:33
+  h3_phaa_merge_quant::fused
+      (back_recv, blocks=40) -> (q int8, scale)
+      npu_fusion/f4_merge_quant/op_extension/merge_quant_queued.asc:26
 
 Here they are defined with the same schemas, with CUDA (HIP) and Meta
 implementations that are the xgen_amd.operator functions mirroring those
@@ -28,6 +31,7 @@ import logging
 import torch
 
 from .operator import gate_residual as _gate
+from .operator import merge_quant as _merge
 from .operator import nq2 as _nq2
 from .operator import swiglu_quant as _swiglu
 
@@ -35,6 +39,9 @@ _NQ2 = ("fused(Tensor x, Tensor weight, Tensor scale, Tensor shift, Tensor indic
         "int blocks=40) -> (Tensor, Tensor)")
 _GATE = ("gate_residual(Tensor residual, Tensor branch, Tensor gate_table, Tensor indices, int tile=5376, "
          "int blocks=40) -> Tensor")
+
+
+_MERGE = "fused(Tensor back_recv, int blocks=40) -> (Tensor, Tensor)"
 
 
 def _swiglu_schema(tile: int) -> str:
@@ -76,6 +83,12 @@ def _gate_impl(residual, branch, gate_table, indices, tile=5376, blocks=40):
     return _gate.gate_residual(residual, branch, gate_table, indices, tile=tile, blocks=blocks)
 
 
+def _merge_impl(back_recv, blocks=40):
+    # merge_quant_queued.asc:10-13
+    _merge.check_back_recv(back_recv, blocks)
+    return _merge.xops.merge_quant(back_recv, torch.int8)
+
+
 def _swiglu_impl(fn, tiles, default_tile):
     # (the schema's defaults again: a Python kernel receives the arguments as the caller gave them)
     def impl(u, tile=default_tile, blocks=40, scale_mode=1):
@@ -99,6 +112,7 @@ OPS = {
                                     _swiglu_impl(_swiglu.swiglu_quantize_vector, (1024, 2048), 2048)),
     "h3_phaa_fusion_quant_reuse": (_swiglu_schema(4096), "swiglu_quantize",
                                    _swiglu_impl(_swiglu.swiglu_quantize_reuse, (1024, 2048, 4096), 4096)),
+    "h3_phaa_merge_quant": (_MERGE, "fused", _merge_impl),
 }
 
 _LIBS: dict = {}
