@@ -63,7 +63,7 @@ def parse():
 PROFILE_KERNELS = ("gemm_fp8_qkv", "gemm_fp8_qkv_exact", "gemm_int8_qkv", "gemm_fp8_ffn_up_gelu", "gemm_fp8_ffn_up",
                    "gemm_fp8_ffn_down",
                    "quant_rows_fp8", "requant_fp8_12288", "requant_gelu_fp8_12288", "front_end_ln_mod_quant_fp8", "gate_residual_op", "indexed_modulate_op",
-                   "swiglu_quant_int8_h3", "merge_quant_int8_h3",
+                   "swiglu_quant_int8_h3", "merge_quant_int8_h3", "phaa_pack_qkv_h3", "phaa_merge_back_h3",
                    "wire_encode_h3", "wire_decode_h3", "wire_async_gather_decode_h3", "wire_async_return_pack_h3",
                    "wire_async_return_layout_decode_h3", "copy_1gib")
 
@@ -187,6 +187,17 @@ def profile_kernels(names, steps, warmup):
         elif name == "merge_quant_int8_h3":
             xr = torch.randn((7, 4, M, 1, 256), generator=g, device=dev).to(torch.bfloat16)
             fn = lambda: xops.merge_quant(xr, torch.int8)  # noqa: E731
+        elif name in ("phaa_pack_qkv_h3", "phaa_merge_back_h3"):
+            from xgen_amd.operator import phaa_layout
+            if name == "phaa_pack_qkv_h3":
+                qkv = torch.randn((1, M, 3 * 7168), generator=g, device=dev).to(torch.bfloat16)
+                q3 = [qkv[..., i * 7168:(i + 1) * 7168].view(1, M, 56, 128) for i in range(3)]
+                snd = [torch.empty((7, 4, M, 1, 2, 128), dtype=torch.bfloat16, device=dev) for _ in range(3)]
+                fn = lambda: phaa_layout.pack_qkv(*q3, *snd)  # noqa: E731
+            else:
+                xr = torch.randn((7, 4, M, 1, 256), generator=g, device=dev).to(torch.bfloat16)
+                merged = torch.empty((1, M, 7168), dtype=torch.bfloat16, device=dev)
+                fn = lambda: phaa_layout.merge_back(xr, merged)  # noqa: E731
         elif name == "swiglu_quant_int8_h3":
             u3 = torch.randn((1, M, 2 * 14336), generator=g, device=dev).to(torch.bfloat16)
             fn = lambda: xops.swiglu_quant(u3, False, torch.int8, 1, False)  # noqa: E731
@@ -589,7 +600,20 @@ def main():
         kernels["merge_quant_int8_h3"] = {"ms": ms_mq, "gbs": mq_bytes / (ms_mq * 1e-3) / 1e9,
                                           "frac_of_hbm": mq_bytes / (ms_mq * 1e-3) / 1e9 / PEAK_HBM_GBS,
                                           "bytes": mq_bytes}
-        del xr
+        # the BF16 layouts around the same exchange: Q/K/V read in place from a fused [M, 3 x 7168]
+        # projection output into the send buffers, and the returned chunks merged into [1, M, 7168]
+        from xgen_amd.operator import phaa_layout
+        qkv = torch.randn((1, M, 3 * 7168), generator=g, device=dev).to(torch.bfloat16)
+        q3 = [qkv[..., i * 7168:(i + 1) * 7168].view(1, M, 56, 128) for i in range(3)]
+        snd = [torch.empty((7, 4, M, 1, 2, 128), dtype=torch.bfloat16, device=dev) for _ in range(3)]
+        merged = torch.empty((1, M, 7168), dtype=torch.bfloat16, device=dev)
+        pk_bytes, mg_bytes = 3 * 2 * M * 7168 * 2, 2 * M * 7168 * 2
+        ms_pk = timed(lambda: phaa_layout.pack_qkv(*q3, *snd), args.steps, args.warmup)
+        ms_mg = timed(lambda: phaa_layout.merge_back(xr, merged), args.steps, args.warmup)
+        for name, ms, nbytes in (("phaa_pack_qkv_h3", ms_pk, pk_bytes), ("phaa_merge_back_h3", ms_mg, mg_bytes)):
+            kernels[name] = {"ms": ms, "gbs": nbytes / (ms * 1e-3) / 1e9,
+                             "frac_of_hbm": nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, "bytes": nbytes}
+        del xr, qkv, q3, snd, merged
 
     # ---- H3's FFN on the same kernels (d = 5,376, F = 14,336): FP8 up -> SwiGLU + FP8 requant -> FP8 down
     if want("h3_ffn"):

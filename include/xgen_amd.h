@@ -243,6 +243,33 @@ int xgen_gate_residual(const void *residual, int64_t res_stride_batch, int64_t r
                        hipStream_t stream);
 
 /*
+ * BF16 layouts of the head-parallel attention's exchange: torch.ops.h3_phaa_layout.{pack, back,
+ * merge} (x_base/x_base/operator/npu_fusion/f4/op_extension/layout_queued.asc:27-55, kernels
+ * f4/op_kernel/layout_kernel.asc:33-59, wrapper npu_fusion/phaa_layout.py:13-28; caller
+ * x_base/x_base/phaa/fused_layout.py:27-52).  Byte moves only; buffers 16-byte aligned, strides
+ * in elements and multiples of 8, each tensor below 2^31 16-byte units.
+ *
+ * xgen_phaa_pack_qkv: q/k/v [1, seq, heads, head_dim] (heads contiguous, row strides given),
+ *   heads = owners * chunks * heads_per_chunk, into q/k/v_send [chunks, owners, seq, 1,
+ *   heads_per_chunk, head_dim] contiguous: send[c, d, s, 0, i] = x[0, s, d * chunks *
+ *   heads_per_chunk + c * heads_per_chunk + i].  The reference's geometry: owners 4, chunks 7,
+ *   heads_per_chunk 2, head_dim 128.
+ * xgen_phaa_pack_back: attn [1, heads, length, head_dim] (head / position strides given) into
+ *   back_send [rows, heads * head_dim] contiguous: row s < length holds attn[0, :, s, :], rows
+ *   from length on are zero (padding tokens); the reference's rows = 4 * S, length 4S or 4S - 1.
+ * xgen_phaa_merge_back: back_recv [chunks, owners, seq, batch, chunk] contiguous into merged
+ *   [batch, seq, owners * chunks * chunk] contiguous: merged[b, s, (o * chunks + c) * chunk + j] =
+ *   back_recv[c, o, s, b, j] (the layout xgen_merge_quant quantizes).
+ */
+int xgen_phaa_pack_qkv(const void *q, const void *k, const void *v, int64_t seq, int64_t owners, int64_t chunks,
+                       int64_t heads_per_chunk, int64_t head_dim, int64_t q_row_stride, int64_t k_row_stride,
+                       int64_t v_row_stride, void *q_send, void *k_send, void *v_send, hipStream_t stream);
+int xgen_phaa_pack_back(const void *attn, int64_t heads, int64_t length, int64_t head_dim, int64_t head_stride,
+                        int64_t position_stride, int64_t rows, void *back_send, hipStream_t stream);
+int xgen_phaa_merge_back(const void *back_recv, int64_t chunks, int64_t owners, int64_t seq, int64_t batch,
+                         int64_t chunk, void *merged, hipStream_t stream);
+
+/*
  * Merge of the head-parallel attention's returned chunks + per-row quantization
  * of the out-projection's input: torch.ops.h3_phaa_merge_quant.fused
  * (x_base/x_base/operator/npu_fusion/f4_merge_quant/op_extension/merge_quant_queued.asc:9-28,

@@ -47,6 +47,9 @@ Function -> reference -> how it is pinned (tests/test_oracle_*.py):
         row quantizers).  merge_rows == a loop over the reference kernel's copy
         (DataCopyPad of 7 stripes of 256 at source stride 4*seq*256, destination
         owner*1792, :25-29) on small cases; the quantizer halves as quantize_rows_*.
+  phaa layouts        f4/op_kernel/layout_kernel.asc:26-59 (phaa_pack_qkv / _pack_back / _merge_back)
+        == loops restating the reference kernels' copies (source and destination
+        element offsets of each DataCopy) on small cases (tests/test_oracle_int8.py).
   fp8 async layouts   phaa/fp8_async_transport.py:13-80,126-193 (fp8_async_encode / _decode)
         plain layout == the synchronous wire without padding; the fused return
         pack == the synchronous wire of the output zero-padded and permuted by torch
@@ -270,6 +273,31 @@ def merge_rows(back_recv: torch.Tensor) -> torch.Tensor:
     x = back_recv.detach().cpu()
     splits, owners, seq, batch, chunk = x.shape
     return x.permute(3, 2, 1, 0, 4).reshape(batch * seq, owners * splits * chunk)
+
+
+def phaa_pack_qkv(x: torch.Tensor, owners=4, chunks=7, heads_per_chunk=2) -> torch.Tensor:
+    """The send layout of one of Q/K/V (layout_kernel.asc:33-44): x [1, S, heads, D] ->
+    [chunks, owners, S, 1, heads_per_chunk, D], owner d's chunk c holding heads
+    d * chunks * heads_per_chunk + c * heads_per_chunk + i."""
+    _, S, H, D = x.shape
+    y = x.detach().cpu()[0].reshape(S, owners, chunks, heads_per_chunk, D)
+    return y.permute(2, 1, 0, 3, 4).reshape(chunks, owners, S, 1, heads_per_chunk, D).contiguous()
+
+
+def phaa_pack_back(attn: torch.Tensor, S: int, owners=4) -> torch.Tensor:
+    """The return layout (layout_kernel.asc:45-52): attn [1, heads, L, D] -> [owners, S, 1, heads * D]
+    rows of every head of one position, rows from L on zero."""
+    _, H, L, D = attn.shape
+    out = torch.zeros((owners * S, H * D), dtype=attn.dtype)
+    out[:L] = attn.detach().cpu()[0].permute(1, 0, 2).reshape(L, H * D)
+    return out.reshape(owners, S, 1, H * D)
+
+
+def phaa_merge_back(back_recv: torch.Tensor) -> torch.Tensor:
+    """The merged attention output (layout_kernel.asc:53-59): [chunks, owners, S, batch, chunk] ->
+    [batch, S, owners * chunks * chunk], the rows merge_rows gives."""
+    _, _, S, B, _ = back_recv.shape
+    return merge_rows(back_recv).reshape(B, S, -1)
 
 
 def merge_quant(back_recv: torch.Tensor, out: str = "int8"):

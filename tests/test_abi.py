@@ -106,6 +106,19 @@ _STRIDES = (N._c_i64 * 12)(384, 128, 128, 128, 384, 128, 128, 128, 384, 128, 128
                                               16, None, None, None), N.ERR_INVALID_ARGUMENT, b"output dtype"),
     (lambda L: L.xgen_fp8_wire_decode_strided(N.DTYPE_BF16, 1, 16, 2, 1 << 31, 1, 1, 64, (N._c_i64 * 4)(0, 64, 0, 0),
                                               6, 16, None, None, None), N.ERR_UNSUPPORTED, b"peer rows"),
+    (lambda L: L.xgen_phaa_pack_qkv(16, 16, 16, 17, 4, 7, 2, 128, 7168, 7168, 100, 16, 16, 16, None),
+     N.ERR_INVALID_ARGUMENT, b"row stride"),
+    (lambda L: L.xgen_phaa_pack_qkv(16, 16, None, 17, 4, 7, 2, 128, 7168, 7168, 7168, 16, 16, 16, None),
+     N.ERR_INVALID_ARGUMENT, b"null"),
+    (lambda L: L.xgen_phaa_pack_qkv(16, 16, 16, 17, 4, 7, 2, 128, 7168, 7172, 7168, 16, 16, 16, None),
+     N.ERR_UNSUPPORTED, b"multiples of 8"),
+    (lambda L: L.xgen_phaa_pack_back(16, 2, 69, 128, 128, 256, 68, 16, None), N.ERR_INVALID_ARGUMENT,
+     b"bad geometry"),
+    (lambda L: L.xgen_phaa_pack_back(16, 2, 68, 100, 128, 256, 68, 16, None), N.ERR_UNSUPPORTED, b"multiples of 8"),
+    (lambda L: L.xgen_phaa_merge_back(16, 7, 4, -1, 1, 256, 16, None), N.ERR_INVALID_ARGUMENT, b"bad geometry"),
+    (lambda L: L.xgen_phaa_merge_back(16, 7, 4, 17, 1, 252, 16, None), N.ERR_UNSUPPORTED, b"multiple of 8"),
+    (lambda L: L.xgen_phaa_merge_back(16, 7, 4, 1 << 20, 1 << 10, 256, 16, None), N.ERR_UNSUPPORTED,
+     b"2^31 16-byte units"),
     (lambda L: L.xgen_merge_quant(N.DTYPE_BF16, 16, 7, 4, 17, 1, 256, 16, 16, None), N.ERR_INVALID_ARGUMENT,
      b"output dtype"),
     (lambda L: L.xgen_merge_quant(N.DTYPE_I8, 16, 0, 4, 17, 1, 256, 16, 16, None), N.ERR_INVALID_ARGUMENT,
@@ -148,6 +161,9 @@ def test_empty_inputs_are_no_ops(built_library):
                                           None, None, None, None) == N.OK
     assert L.xgen_indexed_modulate(None, 0, 64, None, 64, None, 64, 3, None, 2, 0, 64, 0, None, None) == N.OK
     assert L.xgen_merge_quant(N.DTYPE_I8, None, 7, 4, 0, 1, 256, None, None, None) == N.OK
+    assert L.xgen_phaa_pack_qkv(None, None, None, 0, 4, 7, 2, 128, 7168, 7168, 7168, None, None, None, None) == N.OK
+    assert L.xgen_phaa_pack_back(None, 2, 0, 128, 128, 256, 0, None, None) == N.OK
+    assert L.xgen_phaa_merge_back(None, 7, 4, 0, 1, 256, None, None) == N.OK
     assert L.xgen_last_error() == b""
 
 

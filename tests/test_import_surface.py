@@ -53,6 +53,13 @@ IMPORTED = {
         "merge_quant": "x_base/x_base/phaa/fused_layout.py:47 (through Kernels.get), test_npu_fusion_meta.py:60",
         "library_path": "npu_fusion/runtime.py:125 (Kernels.get)",
     },
+    "xgen_amd.operator.phaa_layout": {
+        "pack_qkv": "x_base/x_base/phaa/fused_layout.py:33 (through Kernels.get), test_npu_fusion_meta.py:66",
+        "unpack_qkv": "x_base/x_base/operator/npu_fusion/phaa_layout.py:17 (module function)",
+        "pack_back": "x_base/x_base/phaa/fused_layout.py:42, test_npu_fusion_meta.py:68",
+        "merge_back": "x_base/x_base/phaa/fused_layout.py:51, test_npu_fusion_meta.py:69",
+        "library_path": "npu_fusion/runtime.py:125 (Kernels.get)",
+    },
     "xgen_amd.operator.quantized": {
         "QuantizedRows": "x_base/x_base/phaa/fused_layout.py:5, h3_npu_fusion.py:17",
     },

@@ -160,3 +160,60 @@ def test_merge_quant_is_the_row_quantizer_of_the_merged_rows():
     q8, s8 = R.merge_quant(x, out="fp8")
     f8, fs = R.quantize_rows_fp8(_reference_copy(x))
     assert torch.equal(q8.view(torch.uint8), f8.view(torch.uint8)) and torch.equal(s8, fs)
+
+
+# ------------------------------------------------------------------ PHAA bf16 layouts
+def _loop_pack(x):
+    """layout_kernel.asc:36-43: for each (chunk c, owner d), rows of 256 values copied from
+    s * row_stride + (d * 14 + c * 2) * 128 to ((c * 4 + d) * S + s) * 256."""
+    S, sr = x.shape[1], x.stride(1)
+    flat = x.as_strided(((S - 1) * sr + 56 * 128,), (1,))   # the rows with the gaps between them
+    out = torch.empty(7 * 4 * S * 256, dtype=x.dtype)
+    for c in range(7):
+        for d in range(4):
+            for s in range(S):
+                src = s * sr + (d * 14 + c * 2) * 128
+                out[((c * 4 + d) * S + s) * 256: ((c * 4 + d) * S + s + 1) * 256] = flat[src: src + 256]
+    return out.reshape(7, 4, S, 1, 2, 128)
+
+
+def _loop_back(x, S):
+    """layout_kernel.asc:45-52: rows s < L of head h from h * sh + s * st to s * 256 + h * 128; row L
+    (when L < 4S) zero."""
+    L = x.shape[2]
+    out = torch.full((4 * S * 256,), float("nan"), dtype=x.dtype)
+    for h in range(2):
+        for s in range(L):
+            out[s * 256 + h * 128: s * 256 + h * 128 + 128] = x[0, h, s]
+    if L < 4 * S:
+        out[L * 256: L * 256 + 256] = 0
+    return out.reshape(4, S, 1, 256)
+
+
+def _loop_merge(x):
+    """layout_kernel.asc:53-58: rows of 256 from ((c * 4 + d) * S + s) * 256 to s * 7168 + (d * 14 + c * 2) * 128."""
+    S = x.shape[2]
+    flat = x.reshape(-1)
+    out = torch.empty(S * 7168, dtype=x.dtype)
+    for c in range(7):
+        for d in range(4):
+            for s in range(S):
+                src = ((c * 4 + d) * S + s) * 256
+                out[s * 7168 + (d * 14 + c * 2) * 128: s * 7168 + (d * 14 + c * 2) * 128 + 256] = flat[src: src + 256]
+    return out.reshape(1, S, 7168)
+
+
+@pytest.mark.parametrize("S", [1, 5])
+def test_phaa_layouts_are_the_reference_copies(S):
+    g = torch.Generator().manual_seed(S)
+    x = torch.randn((1, S, 56, 128), generator=g).to(torch.bfloat16)
+    assert torch.equal(R.phaa_pack_qkv(x), _loop_pack(x))
+    wide = torch.randn((1, S, 60, 128), generator=g).to(torch.bfloat16)[:, :, :56]   # row stride 7,680
+    assert torch.equal(R.phaa_pack_qkv(wide), _loop_pack(wide))
+    for L in (4 * S, 4 * S - 1):
+        attn = torch.randn((1, 2, L, 128), generator=g).to(torch.bfloat16)
+        assert torch.equal(R.phaa_pack_back(attn, S), _loop_back(attn, S))
+    back = torch.randn((7, 4, S, 1, 256), generator=g).to(torch.bfloat16)
+    assert torch.equal(R.phaa_merge_back(back), _loop_merge(back))
+    # the round trip of the layouts a peer applies: merge(pack) of one position's heads is the identity
+    assert torch.equal(R.phaa_merge_back(R.phaa_pack_qkv(x).reshape(7, 4, S, 1, 256)), x.reshape(1, S, 7168))

@@ -1,12 +1,12 @@
 """The reference's fused operators under their own torch.ops names (xgen_amd.reference_ops): the
 schemas of their TORCH_LIBRARY definitions, and the reference's Meta contract suite
-(x_base/tests/test_npu_fusion_meta.py:33-48, 60-61, 67-73) run against both the op handles and this
+(x_base/tests/test_npu_fusion_meta.py:33-48, 60-61, 63-73) run against both the op handles and this
 package's wrapper modules, with no device initialized."""
 import pytest
 import torch
 
 import xgen_amd  # noqa: F401  (registers torch.ops.h3_phaa_*)
-from xgen_amd.operator import gate_residual, merge_quant, nq2, swiglu_quant
+from xgen_amd.operator import gate_residual, merge_quant, nq2, phaa_layout, swiglu_quant
 
 M = torch.device("meta")
 
@@ -96,6 +96,65 @@ def test_merge_contract():
         torch.ops.xgen_amd.merge_quant(tensor(3, 2, 5, 2, 60), torch.int8)
     with pytest.raises(RuntimeError, match="16384"):
         torch.ops.xgen_amd.merge_quant(tensor(9, 8, 5, 1, 256), torch.int8)
+
+
+def test_layout_and_mutation_schema():
+    """test_npu_fusion_meta.py:63-71: the three layout ops accept the reference's shapes on Meta
+    tensors and their schemas mark the written outputs."""
+    q = tensor(1, 17, 56, 128)
+    sends = [tensor(7, 4, 17, 1, 2, 128) for _ in range(3)]
+    phaa_layout.pack_qkv(q, q, q, *sends)
+    phaa_layout.pack_back(tensor(1, 2, 67, 128), tensor(4, 17, 1, 256), L=67, S=17)
+    phaa_layout.merge_back(tensor(7, 4, 17, 1, 256), tensor(1, 17, 7168))
+    schema = str(torch.ops.h3_phaa_layout.pack._schemas[""])
+    assert "Tensor(a!)" in schema and "Tensor(b!)" in schema and "Tensor(c!)" in schema
+    assert str(torch.ops.h3_phaa_layout.back._schemas[""]) == (
+        "h3_phaa_layout::back(Tensor x, Tensor(a!) y, int S, int L, int tile=64, int blocks=40) -> ()")
+    assert str(torch.ops.h3_phaa_layout.merge._schemas[""]) == (
+        "h3_phaa_layout::merge(Tensor x, Tensor(a!) y, int tile=64, int blocks=40) -> ()")
+
+
+def test_layout_contracts():
+    """layout_queued.asc:10-49 checks and phaa_layout.py:13-28's own."""
+    q = tensor(1, 17, 56, 128)
+    sends = [tensor(7, 4, 17, 1, 2, 128) for _ in range(3)]
+    with pytest.raises(ValueError, match="SP4/PHAA7"):
+        phaa_layout.pack_qkv(q, q, q, *sends, P=8)
+    with pytest.raises(ValueError, match="Inference only"):
+        phaa_layout.pack_qkv(tensor(1, 17, 56, 128).requires_grad_(), q, q, *sends)
+    with pytest.raises(RuntimeError, match=r"\[1,S,56,128\] required"):
+        phaa_layout.pack_qkv(tensor(1, 17, 48, 128), q, q, *sends)
+    with pytest.raises(RuntimeError, match="send shape mismatch"):
+        phaa_layout.pack_qkv(q, q, q, tensor(7, 4, 16, 1, 2, 128), *sends[1:])
+    with pytest.raises(RuntimeError, match="tile"):
+        torch.ops.h3_phaa_layout.pack(q, q, q, *sends, 48)
+    with pytest.raises(RuntimeError, match="single memory location"):
+        phaa_layout.pack_qkv(q, q, q, sends[0], sends[0], sends[2])
+    with pytest.raises(RuntimeError, match="zero/one padding"):
+        phaa_layout.pack_back(tensor(1, 2, 65, 128), tensor(4, 17, 1, 256), L=65, S=17)
+    with pytest.raises(RuntimeError, match="back_send shape mismatch"):
+        phaa_layout.pack_back(tensor(1, 2, 68, 128), tensor(4, 17, 256), L=68, S=17)
+    with pytest.raises(RuntimeError, match="contiguous"):
+        phaa_layout.merge_back(tensor(7, 4, 17, 1, 256), tensor(1, 7168, 17).transpose(1, 2))
+    with pytest.raises(RuntimeError, match="merged shape mismatch"):
+        phaa_layout.merge_back(tensor(7, 4, 17, 1, 256), tensor(1, 16, 7168))
+    with pytest.raises(RuntimeError, match="BF16"):
+        phaa_layout.merge_back(tensor(7, 4, 17, 1, 256, dtype=torch.float16), tensor(1, 17, 7168))
+
+
+def test_unpack_qkv_views():
+    """phaa_layout.py:17-23 on the CPU (views only): position p of the attention input is peer p // S's
+    position p % S."""
+    S, L = 3, 11
+    recv = [torch.arange(4 * S * 2 * 128, dtype=torch.float32).to(torch.bfloat16).reshape(4, S, 1, 2, 128)
+            for _ in range(3)]
+    views = phaa_layout.unpack_qkv(*recv, L=L)
+    for x, v in zip(recv, views):
+        assert v.shape == (1, 2, L, 128) and v.data_ptr() == x.data_ptr()
+        for p in range(L):
+            assert torch.equal(v[0, :, p], x[p // S, p % S, 0])
+    with pytest.raises(ValueError, match="effective length"):
+        phaa_layout.unpack_qkv(*recv, L=13)
 
 
 def test_device_remains_uninitialized():

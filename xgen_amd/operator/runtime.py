@@ -20,9 +20,9 @@ the attributes below (h3_npu_fusion.py:196-273), so they keep that contract:
 
 Features map onto this package's modules: "norm_quant" -> nq2, "swiglu" ->
 swiglu_quant, "gate_residual" -> gate_residual, "merge_quant" -> merge_quant,
-all in libxgen_amd.so.  The reference's other features (rope, PHAA layout,
-laser preprocessing) are attention work outside the W8A8 linear path and
-always fall back.
+"phaa_layout" -> phaa_layout, all in libxgen_amd.so.  The reference's other
+features (rope, laser preprocessing) are attention work outside the W8A8
+linear path and always fall back.
 """
 from __future__ import annotations
 
@@ -204,7 +204,7 @@ class Kernels:
         "gate_residual": ("gate_residual", None),
         "norm_quant": ("nq2", True),
         "rope": None,
-        "phaa_layout": None,
+        "phaa_layout": ("phaa_layout", None),
         "laser_preprocess": None,
         "merge_quant": ("merge_quant", None),
     }

@@ -15,6 +15,9 @@ libraries define (TORCH_LIBRARY + device + Meta registrations):
   h3_phaa_merge_quant::fused
       (back_recv, blocks=40) -> (q int8, scale)
       npu_fusion/f4_merge_quant/op_extension/merge_quant_queued.asc:26
+  h3_phaa_layout::pack / back / merge
+      (inputs, Tensor(a!) outputs..., tile=64, blocks=40) -> ()
+      npu_fusion/f4/op_extension/layout_queued.asc:59-63
 
 Here they are defined with the same schemas, with CUDA (HIP) and Meta
 implementations that are the xgen_amd.operator functions mirroring those
@@ -32,6 +35,7 @@ import torch
 
 from .operator import gate_residual as _gate
 from .operator import merge_quant as _merge
+from .operator import phaa_layout as _layout
 from .operator import nq2 as _nq2
 from .operator import swiglu_quant as _swiglu
 
@@ -42,6 +46,14 @@ _GATE = ("gate_residual(Tensor residual, Tensor branch, Tensor gate_table, Tenso
 
 
 _MERGE = "fused(Tensor back_recv, int blocks=40) -> (Tensor, Tensor)"
+_LAYOUT = (
+    ("pack", "pack(Tensor q, Tensor k, Tensor v, Tensor(a!) qo, Tensor(b!) ko, Tensor(c!) vo, int tile=64, "
+             "int blocks=40) -> ()", _layout.pack_op, _layout.check_pack),
+    ("back", "back(Tensor x, Tensor(a!) y, int S, int L, int tile=64, int blocks=40) -> ()",
+     _layout.back_op, _layout.check_back),
+    ("merge", "merge(Tensor x, Tensor(a!) y, int tile=64, int blocks=40) -> ()", _layout.merge_op,
+     _layout.check_merge),
+)
 
 
 def _swiglu_schema(tile: int) -> str:
@@ -135,6 +147,19 @@ def register() -> list:
         lib.impl(name, impl, "Meta")
         _LIBS[ns] = lib
         defined.append(ns)
+    if "h3_phaa_layout" not in _LIBS:
+        try:
+            lib = torch.library.Library("h3_phaa_layout", "DEF")
+            for name, schema, _, _ in _LAYOUT:
+                lib.define(schema)
+        except RuntimeError as error:
+            logging.getLogger(__name__).info("torch.ops.h3_phaa_layout left to its earlier registration: %s", error)
+        else:
+            for name, _, gpu, meta in _LAYOUT:
+                lib.impl(name, gpu, "CUDA")
+                lib.impl(name, meta, "Meta")   # the Meta implementations only check, as the reference's
+            _LIBS["h3_phaa_layout"] = lib
+            defined.append("h3_phaa_layout")
     return defined
 
 
