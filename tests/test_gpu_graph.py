@@ -129,3 +129,46 @@ def test_h3_ffn_ops_replay(cuda, kind):
         eager = run()
         assert same(static, eager), rep
         assert torch.equal(bits(static[2]), bits(static[3].reshape(M, d)))
+
+
+def test_exchange_neighbours_replay(cuda):
+    """The out-projection's side of the head-parallel exchange and the output AdaLN under capture:
+    Q/K/V packed from a fused projection output into send buffers, the returned chunks merged (BF16)
+    and merged + quantized (INT8), and the indexed modulation of normalised rows (H3 geometry,
+    S = 96)."""
+    from xgen_amd.operator import phaa_layout
+    from xgen_amd.operator.h3_indexed_affine import output_adaln
+    from xgen_amd.operator.merge_quant import merge_quant
+
+    S = 96
+    g = torch.Generator(device=cuda).manual_seed(5)
+    qkv = torch.empty((1, S, 3 * 7168), dtype=torch.bfloat16, device=cuda)
+    back = torch.empty((7, 4, S, 1, 256), dtype=torch.bfloat16, device=cuda)
+    normed = torch.empty((1, S, 7168), dtype=torch.bfloat16, device=cuda)
+    tables = torch.randn((3, 2 * 7168), generator=g, device=cuda).to(torch.bfloat16)
+    shift, scale = tables.chunk(2, dim=-1)
+    idx = torch.arange(S, device=cuda) % 3
+    sends = [torch.empty((7, 4, S, 1, 2, 128), dtype=torch.bfloat16, device=cuda) for _ in range(3)]
+    merged = torch.empty((1, S, 7168), dtype=torch.bfloat16, device=cuda)
+
+    def fill():
+        for t in (qkv, back, normed):
+            t.copy_(torch.randn(t.shape, generator=g, device=cuda).to(torch.bfloat16))
+
+    def step():
+        q, k, v = (qkv[..., i * 7168:(i + 1) * 7168].view(1, S, 56, 128) for i in range(3))
+        phaa_layout.pack_qkv(q, k, v, *sends)
+        phaa_layout.merge_back(back, merged)
+        qm, sm = merge_quant(back)
+        return (*sends, merged, qm, sm, output_adaln(normed, scale, shift, idx))
+
+    fill()
+    graph, static = capture(step)
+    for rep in range(4):
+        fill()
+        graph.replay()
+        torch.cuda.synchronize()
+        replayed = [t.clone() for t in static]
+        eager = step()
+        torch.cuda.synchronize()
+        assert same(replayed, eager), f"replay {rep}"
