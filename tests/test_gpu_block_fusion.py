@@ -89,3 +89,57 @@ def test_gate_first_swiglu_matches_oracle(cuda):
     assert amax.dim() == 0 and amax.dtype == torch.float32 and torch.isnan(amax.cpu())
     out3, amax3 = swiglu_quant.gate_first_swiglu(x[1:].to(cuda), with_amax=True)
     assert float(amax3) == float(v[1:].float().abs().max())
+
+
+def test_attention_half_linear_path_through_kernels(cuda):
+    """The block's attention half outside the attention itself, reached through Kernels.get as
+    h3_npu_fusion.py reaches it: the front end's shared INT8 rows feed the Q/K/V projections
+    (_h3_project_qkv :103-119), Q/K/V are packed into the exchange's send buffers
+    (phaa/fused_layout.py:27-33), the returned chunks are merged and quantized into QuantizedRows
+    (:44-48) for the INT8 out-projection (_h3_project_output :142-145), and the gated residual
+    closes the half (:56-72).  One GPU stands in for the four owners: the 'returned' chunks are the
+    V send buffer (the layout a peer's attention output comes back in), i.e. attention = identity on
+    V.  Against the oracle composite of the same chain."""
+    from xgen_amd.operator import merge_quant as mq
+    from xgen_amd.operator import phaa_layout
+    from xgen_amd.operator.quantized import QuantizedRows
+
+    g = torch.Generator().manual_seed(23)
+    S, H, W, T, eps = 64, 1024, 7168, 5, 1e-5
+    x = torch.randn((1, S, H), generator=g).to(torch.bfloat16)
+    norm_w = (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16)
+    shift, scale = ((torch.randn((T, H), generator=g) * 0.1).to(torch.bfloat16) for _ in range(2))
+    gate = (torch.randn((T, H), generator=g) * 0.5).to(torch.bfloat16)
+    idx = torch.randint(T, (S,), generator=g)
+    ws = [((torch.randn((n, k), generator=g) * 0.02).to(torch.bfloat16),
+           (torch.randn(n, generator=g) * 0.01).to(torch.bfloat16)) for n, k in ((W, H),) * 3 + ((H, W),)]
+    to_q, to_k, to_v, to_out = (WeightQuantLinearModule(w, b).to(cuda) for w, b in ws)
+    xc, sc, sh, gt, ic, wc = (t.to(cuda) for t in (x, scale, shift, gate, idx, norm_w))
+
+    diag = Diagnostics(prefix="H3_OPT")
+    kernels = Kernels(diag)
+    with torch.no_grad():
+        q, s = kernels.get("norm_quant", xc).norm_affine_quant(xc, wc, sc, sh, ic, eps=eps, cached=True)
+        proj = [quant_matmul(q, s, lin, (1, S, H)) for lin in (to_q, to_k, to_v)]   # [1, S, 7168] each
+        layout = kernels.get("phaa_layout", xc)
+        sends = [torch.empty((7, 4, S, 1, 2, 128), dtype=torch.bfloat16, device=cuda) for _ in range(3)]
+        layout.pack_qkv(*(p.view(1, S, 56, 128) for p in proj), *sends)
+        merge = kernels.get("merge_quant", xc)
+        qm, smq = merge.merge_quant(sends[2].view(7, 4, S, 1, 256))
+        value = QuantizedRows(qm, smq, (1, S, W))
+        branch = quant_matmul(value.q, value.scale, to_out, value.shape)
+        out = kernels.get("gate_residual", xc).gate_residual(xc, branch, gt, ic)
+    assert mq.merge_quant is merge.merge_quant and not diag.fallbacks
+
+    qr, sr, _ = R.norm_affine_quant(x, norm_w, scale, shift, idx, eps, "rms", "int8")
+    qws = [R.quantize_rows_int8(w) for w, _ in ws]
+    v_ref = R.w8a8_linear_int8(qr, sr, *qws[2], ws[2][1])                       # [S, 7168]
+    # the merged rows of V's send buffer are V's rows (pack then merge is the identity)
+    assert torch.equal(R.merge_rows(R.phaa_pack_qkv(v_ref.reshape(1, S, 56, 128)).reshape(7, 4, S, 1, 256)), v_ref)
+    qv, sv = R.quantize_rows_int8(proj[2].reshape(S, W))                       # from the kernel's own V
+    assert torch.equal(qm.cpu(), qv) and torch.equal(smq.cpu(), sv)
+    br_ref = R.w8a8_linear_int8(qv, sv, *qws[3], ws[3][1]).reshape(1, S, H)
+    out_ref = R.gate_residual(x, br_ref, gate, idx)
+    for got, ref in ((proj[2].reshape(S, W), v_ref), (branch, br_ref), (out, out_ref)):
+        rel, cos = R.rel_l2(got, ref), R.cosine(got, ref)
+        assert rel <= 1e-2 and cos >= 0.9999, (rel, cos)
