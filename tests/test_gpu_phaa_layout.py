@@ -100,3 +100,24 @@ def test_kernels_resolve_phaa_layout(cuda):
     d = runtime.Diagnostics()
     module = runtime.Kernels(d).get("phaa_layout", torch.zeros(1, dtype=torch.bfloat16, device=cuda))
     assert module is phaa_layout and not d.fallbacks
+
+
+def test_outputs_off_the_16_byte_grid(cuda):
+    """Contiguous outputs that start 2 bytes into their storage (views of a larger buffer): the
+    kernels write aligned scratch that is copied into them; inputs off the grid are read from
+    aligned copies."""
+    S = 9
+    x = bf16((1, S, 56, 128), seed=11, device=cuda)
+    store = torch.full((3, 7 * 4 * S * 256 + 1), float("nan"), dtype=torch.bfloat16, device=cuda)
+    outs = [store[i, 1:].view(7, 4, S, 1, 2, 128) for i in range(3)]
+    src = torch.empty(x.numel() + 1, dtype=torch.bfloat16, device=cuda)[1:].view_as(x).copy_(x)
+    phaa_layout.pack_qkv(src, x, x, *outs)
+    for y in outs:
+        assert torch.equal(y.cpu().view(torch.int16), R.phaa_pack_qkv(x.cpu()).view(torch.int16))
+    merged = torch.empty(S * 7168 + 1, dtype=torch.bfloat16, device=cuda)[1:].view(1, S, 7168)
+    phaa_layout.merge_back(outs[0].view(7, 4, S, 1, 256), merged)
+    assert torch.equal(merged, x.reshape(1, S, 7168))
+    back = torch.empty(4 * S * 256 + 1, dtype=torch.bfloat16, device=cuda)[1:].view(4, S, 1, 256)
+    attn = bf16((1, 2, 4 * S - 1, 128), seed=12, device=cuda)
+    phaa_layout.pack_back(attn, back, L=4 * S - 1, S=S)
+    assert torch.equal(back.cpu().view(torch.int16), R.phaa_pack_back(attn.cpu(), S).view(torch.int16))

@@ -96,16 +96,30 @@ def _aligned(*ts):
     return all(t.data_ptr() % 16 == 0 for t in ts)
 
 
+def _written(outs):
+    """The buffers the kernel writes for `outs`: each output itself, or an aligned scratch copied
+    into it afterwards (the kernels store 16-byte units)."""
+    return [y if _aligned(y) else torch.empty_like(y, memory_format=torch.contiguous_format) for y in outs]
+
+
+def _copy_back(outs, written):
+    for y, w in zip(outs, written):
+        if w is not y:
+            y.copy_(w)
+
+
 def pack_op(q, k, v, qo, ko, vo, tile=64, blocks=40):
     """torch.ops.h3_phaa_layout.pack on a HIP device (layout_queued.asc:27-34)."""
     check_pack(q, k, v, qo, ko, vo, tile, blocks)
     _require(q.is_cuda, "HIP (cuda) device required")
     # (a base or row stride off the 16-byte grid: the kernel reads from an aligned copy)
-    srcs = [x if _aligned(x) and x.stride(1) % 8 == 0 else x.contiguous() for x in (q, k, v)]
+    srcs = [x if _aligned(x) and x.stride(1) % 8 == 0 else x.clone(memory_format=torch.contiguous_format)
+            for x in (q, k, v)]
+    outs = _written((qo, ko, vo))
     st = N.lib().xgen_phaa_pack_qkv(*(x.data_ptr() for x in srcs), q.shape[1], 4, 7, 2, 128,
-                                    *(x.stride(1) for x in srcs), qo.data_ptr(), ko.data_ptr(), vo.data_ptr(),
-                                    N.stream_of(q))
+                                    *(x.stride(1) for x in srcs), *(y.data_ptr() for y in outs), N.stream_of(q))
     N.check(st, "xgen_phaa_pack_qkv")
+    _copy_back((qo, ko, vo), outs)
 
 
 def back_op(x, y, S, L, tile=64, blocks=40):
@@ -113,10 +127,12 @@ def back_op(x, y, S, L, tile=64, blocks=40):
     check_back(x, y, S, L, tile, blocks)
     _require(x.is_cuda, "HIP (cuda) device required")
     if not (_aligned(x) and x.stride(1) % 8 == 0 and x.stride(2) % 8 == 0):
-        x = x.contiguous()
-    st = N.lib().xgen_phaa_pack_back(x.data_ptr(), 2, L, 128, x.stride(1), x.stride(2), 4 * S, y.data_ptr(),
+        x = x.clone(memory_format=torch.contiguous_format)
+    (out,) = _written((y,))
+    st = N.lib().xgen_phaa_pack_back(x.data_ptr(), 2, L, 128, x.stride(1), x.stride(2), 4 * S, out.data_ptr(),
                                      N.stream_of(x))
     N.check(st, "xgen_phaa_pack_back")
+    _copy_back((y,), (out,))
 
 
 def merge_op(x, y, tile=64, blocks=40):
@@ -125,8 +141,10 @@ def merge_op(x, y, tile=64, blocks=40):
     _require(x.is_cuda, "HIP (cuda) device required")
     if not _aligned(x):
         x = x.clone()
-    st = N.lib().xgen_phaa_merge_back(x.data_ptr(), 7, 4, x.shape[2], 1, 256, y.data_ptr(), N.stream_of(x))
+    (out,) = _written((y,))
+    st = N.lib().xgen_phaa_merge_back(x.data_ptr(), 7, 4, x.shape[2], 1, 256, out.data_ptr(), N.stream_of(x))
     N.check(st, "xgen_phaa_merge_back")
+    _copy_back((y,), (out,))
 
 
 def _inference_only(*xs):
