@@ -20,7 +20,8 @@ def bits(t):
 
 
 def make_job(seed, cuda):
-    """One small block front: front end -> QKV GEMM (both kinds) -> requant -> gated out-projection."""
+    """One small block front: front end -> QKV GEMM (both kinds) -> requant -> gated out-projection,
+    plus the output AdaLN modulation and a merge + quant of a Q slice."""
     g = torch.Generator().manual_seed(seed)
     B, S, d, T = 1, 1536, 1024, 6
     x = torch.randn((B, S, d), generator=g).to(torch.bfloat16).to(cuda)
@@ -37,7 +38,9 @@ def make_job(seed, cuda):
         qkv_exact, _ = xops.scaled_mm(q, wq, s, sq, None, torch.bfloat16, N.ACT_NONE, False, True)
         qv, sv = xops.quantize_rows(qkv[:, 2 * d:], FP8)
         out = xops.scaled_mm_gate_residual(qv, wo, sv, so, None, x.reshape(-1, d), gate, idx)
-        return [q, s, qkv, qkv_exact, qv, sv, out]
+        mod = xops.indexed_modulate(x, scale, shift, idx)
+        mq, ms = xops.merge_quant(qkv[:, :d].reshape(4, 2, S, 1, 128), torch.int8)
+        return [q, s, qkv, qkv_exact, qv, sv, out, mod, mq, ms]
 
     return run
 
