@@ -120,3 +120,23 @@ def test_beyond_the_last_level_cache(cuda):
     sample = x[:, :, rows.to(cuda)].cpu()
     rq, rs = R.merge_quant(sample)
     assert torch.equal(q[rows.to(cuda)].cpu(), rq) and torch.equal(s[rows.to(cuda)].cpu(), rs)
+
+
+@pytest.mark.parametrize("accumulation", ["exact", "mfma"])
+def test_fp8_rows_feed_the_fp8_out_projection(cuda, accumulation):
+    """The FP8 form (out_dtype=float8_e4m3fn) into the FP8 out-projection (H3FP8Linear with per-token
+    activation scales) through quant_matmul: equal to that module's own forward on the merged rows
+    (which quantizes them with the same FP8 row quantizer)."""
+    from xgen_amd.operator.h3_fp8 import H3FP8Linear
+    seq, width, n_out = 48, 7168, 384
+    x = back_recv((7, 4, seq, 1, 256), seed=13).to(cuda)
+    g = torch.Generator().manual_seed(14)
+    w = (torch.randn((n_out, width), generator=g) * 0.02).to(torch.bfloat16).to(cuda)
+    b = (torch.randn((n_out,), generator=g) * 0.01).to(torch.bfloat16).to(cuda)
+    layer = H3FP8Linear(w, b, activation_scaling="token", accumulation=accumulation)
+    assert runtime.quant_linear(layer, width, x.device)
+    q, s = merge_quant(x, out_dtype=FP8)
+    value = QuantizedRows(q, s, (1, seq, width))
+    out = runtime.quant_matmul(value.q, value.scale, layer, value.shape)
+    rows = R.merge_rows(x).to(cuda).view(1, seq, width)
+    assert torch.equal(out.view(torch.int16), layer(rows).view(torch.int16))
