@@ -140,3 +140,22 @@ def test_fp8_rows_feed_the_fp8_out_projection(cuda, accumulation):
     out = runtime.quant_matmul(value.q, value.scale, layer, value.shape)
     rows = R.merge_rows(x).to(cuda).view(1, seq, width)
     assert torch.equal(out.view(torch.int16), layer(rows).view(torch.int16))
+
+
+def test_reference_maximum_sequence(cuda):
+    """S = 2^20, the reference op's largest (merge_quant_queued.asc:12): a 15 GB back_recv whose source
+    offsets pass 2^32 bytes, merged + quantized (7.5 GB of rows) and merged in BF16; sampled rows
+    (first, last, around each 2^30-byte segment boundary) against the oracle."""
+    from xgen_amd.operator import phaa_layout
+    seq = 1 << 20
+    g = torch.Generator(device=cuda).manual_seed(15)
+    x = torch.randn((7, 4, seq, 1, 256), generator=g, device=cuda, dtype=torch.bfloat16)
+    q, s = merge_quant(x)
+    rows = torch.tensor([0, 1, 2047, 2048, 524287, 524288, seq - 2, seq - 1])
+    sample = x[:, :, rows.to(cuda)].cpu()
+    rq, rs = R.merge_quant(sample)
+    assert torch.equal(q[rows.to(cuda)].cpu(), rq) and torch.equal(s[rows.to(cuda)].cpu(), rs)
+    del q, s
+    merged = torch.empty((1, seq, 7168), dtype=torch.bfloat16, device=cuda)
+    phaa_layout.merge_back(x, merged)
+    assert torch.equal(merged[0, rows.to(cuda)].cpu(), R.merge_rows(sample))
